@@ -1,0 +1,366 @@
+#!/usr/bin/env python3
+"""Benchmark of the silarray GPU hot path on one MI355X.
+
+Headline (BASELINE.json metric): fp32 SGEMM TFLOP/s at M=N=K=8192 (the
+compute-bound config) with the 1x4096x4096 GEMV GB/s beside it, each as a
+fraction of the MI355X roofline.  A "step" is one 8192^3 SGEMM (C = A.B) on
+uniform[-1,1] inputs already resident in HBM.  Every kernel runs through the
+C ABI (libsilgpu.so); times come from HIP events recorded on the library's
+stream around back-to-back launches, and the wall clock brackets the timed
+steps with a device synchronisation on both sides.
+
+The other rows of the workload (GEMV, small-batch SGEMM, linear_sigmoid, row
+softmax / layer_norm / sum(axis=1), full sum/min/max/argmax, the 20-op affine
+chain, the 2048^3 and 4096^3 SGEMMs) are reported under "secondary" with
+their own roofline fractions.  Bandwidth rows rotate >= 1 GiB of buffers so
+the 256 MiB Infinity Cache cannot serve repeated reads.
+
+cpu_baseline: cblas_sgemm from OpenBLAS (the x86 stand-in for the
+reference's Accelerate call, include/cpu.h:239-264) on the host cores of the
+same machine, bounded to ~10 s.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "fp32 SGEMM TFLOPS (8192^3) + GEMV GB/s (1x4096x4096); % of roofline"
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+SEED = 20261201
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", default="", help="comma list of workloads (default: all)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+def log(msg: str) -> None:
+    sys.stderr.write(f"[bench] {msg}\n")
+    sys.stderr.flush()
+
+
+class Timer:
+    """HIP events on the library stream around `reps` launches of fn."""
+
+    def __init__(self, nat):
+        self.nat = nat
+        self.e0 = nat.Event()
+        self.e1 = nat.Event()
+
+    def ms_per_launch(self, fn, reps: int, warmup: int = 2) -> float:
+        for i in range(warmup):
+            fn(i)
+        self.nat.sync()
+        self.e0.record()
+        for i in range(reps):
+            fn(i)
+        self.e1.record()
+        return self.e0.elapsed_ms(self.e1) / reps
+
+
+def roofline(bound: str, achieved: float, traffic=None) -> dict:
+    peak = PEAK_FP32_MFMA_TFLOPS if bound == "mfma" else PEAK_HBM_GBS
+    return {"bound": bound, "achieved": round(achieved, 3), "peak": peak,
+            "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+def load_traffic(name: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, copy-kernel calibrated), committed under profiles/."""
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get(name)
+    except Exception:
+        return None
+
+
+def uniform(g, shape):
+    return g.uniform(-1.0, 1.0, shape).astype(np.float32)
+
+
+def normal(g, shape, std):
+    return g.normal(0.0, std, shape).astype(np.float32)
+
+
+# ---- workloads -------------------------------------------------------------------
+
+def bench_sgemm(nat, S, steps, warmup, g):
+    A = nat.DeviceBuffer.from_array(uniform(g, (S, S)))
+    B = nat.DeviceBuffer.from_array(uniform(g, (S, S)))
+    C = nat.DeviceBuffer(S * S * 4)
+
+    def step(_i):
+        nat.sgemm(0, 0, S, S, S, A, S, 0, B, S, 0, C, S, 0)
+
+    for i in range(warmup):
+        step(i)
+    nat.sync()
+    t = Timer(nat)
+    t0 = time.perf_counter()
+    t.e0.record()
+    for i in range(steps):
+        step(i)
+    t.e1.record()
+    nat.sync()
+    wall = time.perf_counter() - t0
+    kern_ms = t.e0.elapsed_ms(t.e1) / steps
+    flops = 2.0 * S * S * S
+    return {"wall_ms_per_step": wall * 1e3 / steps, "kernel_ms": kern_ms,
+            "tflops_wall": flops / (wall / steps) / 1e12, "tflops_kernel": flops / (kern_ms / 1e3) / 1e12}
+
+
+def bench_gemv(nat, g, reps=200):
+    K = N = 4096
+    copies = 16  # 16 x 64 MiB = 1 GiB in rotation
+    x = nat.DeviceBuffer.from_array(normal(g, K, 0.02))
+    B0 = normal(g, (K, N), 0.02)
+    Bs = [nat.DeviceBuffer.from_array(B0) for _ in range(copies)]
+    y = nat.DeviceBuffer(N * 4)
+    t = Timer(nat)
+    ms = t.ms_per_launch(lambda i: nat.sgemv(x, Bs[i % copies], N, y, N, K), reps, warmup=copies)
+    ms_hot = t.ms_per_launch(lambda i: nat.sgemv(x, Bs[0], N, y, N, K), reps)
+    nbytes = 4 * (K + K * N + N)
+    return {"gbs": nbytes / (ms / 1e3) / 1e9, "gbs_hot": nbytes / (ms_hot / 1e3) / 1e9,
+            "us": ms * 1e3, "bytes": nbytes}
+
+
+def bench_small_batch(nat, g, reps=200):
+    M, N, K = 32, 768, 4096
+    copies = 64
+    A = nat.DeviceBuffer.from_array(normal(g, (M, K), 0.02))
+    B0 = normal(g, (K, N), 0.02)
+    Bs = [nat.DeviceBuffer.from_array(B0) for _ in range(copies)]
+    C = nat.DeviceBuffer(M * N * 4)
+    t = Timer(nat)
+    ms = t.ms_per_launch(lambda i: nat.sgemm(0, 0, M, N, K, A, K, 0, Bs[i % copies], N, 0, C, N, 0),
+                         reps, warmup=copies)
+    nbytes = 4 * (M * K + K * N + M * N)
+    return {"gbs": nbytes / (ms / 1e3) / 1e9, "us": ms * 1e3,
+            "tflops": 2 * M * N * K / (ms / 1e3) / 1e12, "bytes": nbytes}
+
+
+def bench_linear_sigmoid(nat, g, reps=50):
+    M, N, K = 256, 4096, 4096
+    X = nat.DeviceBuffer.from_array(normal(g, (M, K), 0.02))
+    W = nat.DeviceBuffer.from_array(normal(g, (K, N), 0.02))
+    b = nat.DeviceBuffer.from_array(normal(g, N, 0.02))
+    Y = nat.DeviceBuffer(M * N * 4)
+    t = Timer(nat)
+    ms = t.ms_per_launch(lambda i: nat.sgemm(0, 0, M, N, K, X, K, 0, W, N, 0, Y, N, 0, 1, b, N,
+                                             nat.EPI_BIAS_SIGMOID), reps)
+    return {"tflops": 2.0 * M * N * K / (ms / 1e3) / 1e12, "us": ms * 1e3}
+
+
+def bench_rowops(nat, g, reps=20):
+    R, Cc = 4096, 8192
+    pairs = 4  # 4 x (128 MiB in + 128 MiB out) = 1 GiB in rotation
+    x0 = normal(g, (R, Cc), 3.0)
+    xs = [nat.DeviceBuffer.from_array(x0) for _ in range(pairs)]
+    ys = [nat.DeviceBuffer(R * Cc * 4) for _ in range(pairs)]
+    gamma = nat.DeviceBuffer.from_array(np.ones(Cc, np.float32))
+    beta = nat.DeviceBuffer.from_array(np.zeros(Cc, np.float32))
+    t = Timer(nat)
+    out = {}
+    ms = t.ms_per_launch(lambda i: nat.softmax_rows_f32(xs[i % pairs], ys[i % pairs], R, Cc), reps, pairs)
+    out["softmax"] = {"gbs": 8 * R * Cc / (ms / 1e3) / 1e9, "us": ms * 1e3, "bytes": 8 * R * Cc}
+    ms = t.ms_per_launch(lambda i: nat.layer_norm_rows_f32(xs[i % pairs], ys[i % pairs], gamma, beta,
+                                                           R, Cc, 1e-5), reps, pairs)
+    nb = 8 * R * Cc + 8 * Cc
+    out["layer_norm"] = {"gbs": nb / (ms / 1e3) / 1e9, "us": ms * 1e3, "bytes": nb}
+    ms = t.ms_per_launch(lambda i: nat.sum_axis_f32(xs[i % pairs], R, Cc, 1, ys[i % pairs]), reps, pairs)
+    nb = 4 * R * Cc + 4 * R
+    out["sum_axis1"] = {"gbs": nb / (ms / 1e3) / 1e9, "us": ms * 1e3, "bytes": nb}
+    return out
+
+
+def bench_reductions(nat, g, reps=20):
+    n = 64 * 1024 * 1024
+    copies = 4  # 4 x 256 MiB
+    x0 = uniform(g, n)
+    x0[(n * 7) // 9 + 1] = 2.0  # unique planted maximum, not 4- or chunk-aligned
+    xs = [nat.DeviceBuffer.from_array(x0) for _ in range(copies)]
+    o = nat.DeviceBuffer(4096)
+    t = Timer(nat)
+    out = {}
+    for name, fn in [("sum", nat.sum_f32), ("min", nat.min_f32), ("max", nat.max_f32)]:
+        ms = t.ms_per_launch(lambda i, fn=fn: fn(xs[i % copies], n, o), reps, copies)
+        out[name] = {"gbs": 4 * n / (ms / 1e3) / 1e9, "us": ms * 1e3, "bytes": 4 * n}
+    ms = t.ms_per_launch(lambda i: nat.argmax_rows_f32(xs[i % copies], 1, n, o), reps, copies)
+    out["argmax"] = {"gbs": 4 * n / (ms / 1e3) / 1e9, "us": ms * 1e3, "bytes": 4 * n}
+    nat.sync()
+    idx = int(o.download(1, np.int32)[0])
+    out["argmax"]["index_ok"] = idx == (n * 7) // 9 + 1
+    return out
+
+
+def bench_affine_chain(nat, g, reps=20):
+    n = 64 * 1024 * 1024
+    copies = 2  # 2 x (256 MiB in + 256 MiB out)
+    x0 = uniform(g, n)
+    xs = [nat.DeviceBuffer.from_array(x0) for _ in range(copies)]
+    ys = [nat.DeviceBuffer(4 * n) for _ in range(copies)]
+    sc = g.uniform(0.9, 1.1, 20).astype(np.float32)
+    of = g.uniform(-0.1, 0.1, 20).astype(np.float32)
+    progs = []
+    for k in range(copies):
+        instrs = [(nat.PI_LOAD, 0, 0, 0, 0.0, 0.0)] + [(nat.PI_FMAI, 0, 0, 0, float(a), float(b))
+                                                       for a, b in zip(sc, of)]
+        progs.append(nat.make_program((n,), [(xs[k], (1,))], instrs))
+    t = Timer(nat)
+    ms = t.ms_per_launch(lambda i: nat.program_f32(progs[i % copies], ys[i % copies]), reps, copies)
+    return {"gbs": 8 * n / (ms / 1e3) / 1e9, "us": ms * 1e3, "bytes": 8 * n, "ops": 20}
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """cblas_sgemm (OpenBLAS) 2048^3 fp32 on this host's cores, repeated for
+    about `seconds`; TFLOP/s of the same SGEMM shape family as the headline."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import openblas  # test-infrastructure baseline, oracle/openblas.py
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except Exception:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, 16))
+    openblas.set_threads(cores)
+    S = 2048
+    g = np.random.default_rng(SEED)
+    A = uniform(g, (S, S))
+    B = uniform(g, (S, S))
+    Cm = np.empty((S, S), np.float32)
+    openblas.sgemm(A, B, Cm)  # warmup
+    runs = 0
+    t0 = time.perf_counter()
+    while True:
+        openblas.sgemm(A, B, Cm)
+        runs += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or runs >= 200:
+            break
+    tflops = 2.0 * S ** 3 * runs / el / 1e12
+    return {"value": round(tflops, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"cblas_sgemm (OpenBLAS, {Path(openblas.LIB_PATH).name}) {S}^3 fp32 "
+                      f"row-major NN, {runs} runs in {el:.1f} s, {cores} threads"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "multi-GPU sharding is described in DESIGN.md but not run.", file=sys.stderr)
+        return 2
+    from silarray_amd import _native as nat
+
+    nat.init()
+    info = nat.device_info()
+    log(f"device {info}")
+    only = set(filter(None, args.only.split(",")))
+    want = (lambda k: not only or k in only)
+    g = np.random.default_rng(SEED)
+
+    res = {}
+    S = 8192
+    if want("sgemm"):
+        log(f"sgemm {S}^3: warmup {args.warmup}, steps {args.steps}")
+        res["sgemm"] = bench_sgemm(nat, S, args.steps, args.warmup, g)
+        log(f"sgemm {res['sgemm']}")
+    secondary = {}
+    if want("gemv"):
+        r = bench_gemv(nat, g)
+        log(f"gemv {r}")
+        secondary["gemv_1x4096x4096"] = {
+            "value": round(r["gbs"], 1), "unit": "GB/s", "hot_cache_gbs": round(r["gbs_hot"], 1),
+            "us": round(r["us"], 2),
+            "roofline": roofline("hbm", r["gbs"], load_traffic("gemv_1x4096x4096"))}
+    if want("small_batch"):
+        r = bench_small_batch(nat, g)
+        log(f"small_batch {r}")
+        secondary["sgemm_32x768x4096"] = {
+            "value": round(r["gbs"], 1), "unit": "GB/s", "tflops": round(r["tflops"], 2),
+            "us": round(r["us"], 2), "roofline": roofline("hbm", r["gbs"])}
+    if want("linear_sigmoid"):
+        r = bench_linear_sigmoid(nat, g)
+        log(f"linear_sigmoid {r}")
+        secondary["linear_sigmoid_256x4096x4096"] = {
+            "value": round(r["tflops"], 2), "unit": "TFLOP/s", "us": round(r["us"], 1),
+            "roofline": roofline("mfma", r["tflops"])}
+    if want("rowops"):
+        r = bench_rowops(nat, g)
+        log(f"rowops {r}")
+        for k, v in r.items():
+            secondary[f"{k}_4096x8192"] = {"value": round(v["gbs"], 1), "unit": "GB/s",
+                                           "us": round(v["us"], 2),
+                                           "roofline": roofline("hbm", v["gbs"],
+                                                                load_traffic(f"{k}_4096x8192"))}
+    if want("reductions"):
+        r = bench_reductions(nat, g)
+        log(f"reductions {r}")
+        for k, v in r.items():
+            e = {"value": round(v["gbs"], 1), "unit": "GB/s", "us": round(v["us"], 2),
+                 "roofline": roofline("hbm", v["gbs"], load_traffic(f"{k}_64M"))}
+            if "index_ok" in v:
+                e["index_ok"] = v["index_ok"]
+            secondary[f"{k}_64M"] = e
+    if want("affine_chain"):
+        r = bench_affine_chain(nat, g)
+        log(f"affine_chain {r}")
+        secondary["affine_chain20_64M"] = {"value": round(r["gbs"], 1), "unit": "GB/s",
+                                           "us": round(r["us"], 2),
+                                           "roofline": roofline("hbm", r["gbs"],
+                                                                load_traffic("affine_chain20_64M"))}
+    if want("sgemm_sweep"):
+        for s in (2048, 4096):
+            r = bench_sgemm(nat, s, 10, 3, g)
+            log(f"sgemm {s}^3 {r}")
+            secondary[f"sgemm_{s}"] = {"value": round(r["tflops_kernel"], 2), "unit": "TFLOP/s",
+                                       "roofline": roofline("mfma", r["tflops_kernel"])}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        cpu = cpu_baseline(args.cpu_seconds)
+        log(f"cpu {cpu}")
+
+    line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": f"synthetic: uniform[-1,1] fp32 A, B from numpy PCG64 seed {SEED}",
+            "config": {"workload": "sgemm_8192x8192x8192", "M": S, "N": S, "K": S,
+                       "layout": "row-major NN", "parallelism": "single GPU"}}
+    if "sgemm" in res:
+        r = res["sgemm"]
+        line.update({"value": round(r["tflops_wall"], 2), "unit": "TFLOP/s",
+                     "ms_per_step": round(r["wall_ms_per_step"], 4),
+                     "roofline": roofline("mfma", r["tflops_kernel"],
+                                          load_traffic("sgemm_8192x8192x8192"))})
+    else:
+        line.update({"value": None, "unit": "TFLOP/s", "ms_per_step": None, "roofline": None})
+    line["cpu_baseline"] = cpu
+    line["secondary"] = secondary
+    line["device"] = info
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,278 @@
+/*
+ * silgpu.h — C ABI of the MI355X (gfx950) backend for the silarray hot path.
+ *
+ * The reference (yhirose/silarray) has no FFI: its operator boundary is the
+ * header-only C++ class `sil::gpu` (include/gpu.h:266-1036) plus the
+ * `gpu_context` singleton (include/gpu.h:49-260) and the unified-memory
+ * `storage`/`buffer_pool` pair (include/unified_memory.h:17-79).  Every entry
+ * point below replaces one of those; the reference interface it stands in for
+ * is cited on each declaration.  The C++ mirror `silarray_amd/include/sil/gpu.h`
+ * keeps the reference's method names and `storage` signatures and calls only
+ * these functions.
+ *
+ * Conventions
+ *   - Every function returns SILGPU_OK (0) or a negative status; the message of
+ *     the last failure on the calling thread is returned by silgpu_last_error().
+ *   - Pointers named d_* are device pointers (from silgpu_alloc or hipMalloc).
+ *     Pointers named h_* are host pointers.
+ *   - All launches are asynchronous on the library's single HIP stream and run
+ *     in issue order, like the reference's single command buffer
+ *     (include/gpu.h:66-77).  silgpu_sync() waits for them.
+ *   - Sizes are element counts (int64_t) unless a name says bytes.
+ *   - Nothing here allocates device memory except silgpu_alloc and the
+ *     one-time scratch area reserved by silgpu_init.
+ */
+#ifndef SILGPU_H
+#define SILGPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------- */
+#define SILGPU_OK 0
+#define SILGPU_ERR_INVALID (-1)     /* bad argument (shape, null pointer, range) */
+#define SILGPU_ERR_HIP (-2)         /* a HIP runtime call or launch failed */
+#define SILGPU_ERR_NOMEM (-3)       /* device or pinned allocation failed */
+#define SILGPU_ERR_UNSUPPORTED (-4) /* valid request this build does not run */
+#define SILGPU_ERR_NODEVICE (-5)    /* no HIP device visible */
+
+/* ---- binary / unary operation codes ------------------------------------- */
+/* Order follows the reference's ArithmeticOperation enum (include/array.h:570-576)
+ * and PSO list (include/gpu.h:21-25). */
+#define SILGPU_ADD 0
+#define SILGPU_SUB 1
+#define SILGPU_MUL 2
+#define SILGPU_DIV 3
+#define SILGPU_POW 4
+
+#define SILGPU_SIGMOID 0 /* 1/(1+exp(-x)), include/gpu.h:314-316 */
+#define SILGPU_RELU 1    /* max(x,0),      include/gpu.h:318-320 */
+
+/* GEMM epilogues.  BIAS adds bias[col % bias_len] (include/gpu_kernels.metal:506-522);
+ * BIAS_SIGMOID applies 1/(1+exp(-v)) after the bias (include/gpu_kernels.metal:524-542). */
+#define SILGPU_EPI_NONE 0
+#define SILGPU_EPI_BIAS 1
+#define SILGPU_EPI_BIAS_SIGMOID 2
+#define SILGPU_EPI_RELU 3
+#define SILGPU_EPI_BIAS_RELU 4
+
+/* ---- context, errors, memory -------------------------------------------- */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *silgpu_last_error(void);
+
+/* Select device 0, create the stream, reserve scratch.  Idempotent.
+ * Replaces gpu_context::instance() construction (include/gpu.h:59-62, 132-185)
+ * and buffer_pool::instance() (include/unified_memory.h:33-36, 55-61). */
+int silgpu_init(void);
+
+/* Wait for all work issued so far.  Replaces gpu_context::flush()
+ * (include/gpu.h:107-123) and sil::synchronize() (include/gpu.h:1375-1377). */
+int silgpu_sync(void);
+
+/* Device properties of the active device (CU count, clock in kHz, LDS bytes
+ * per workgroup, gcnArchName).  No reference counterpart; used for roofline
+ * reporting. */
+int silgpu_device_info(int *cu_count, int *clock_khz, int *lds_bytes, char *arch,
+                       size_t arch_len);
+
+/* Pooled device allocation.  Replaces buffer_pool::acquire/release
+ * (include/unified_memory.h:38-53) behind storage::make (:66-79).  Blocks are
+ * reused by size class and returned to the pool by silgpu_free; the pool
+ * never returns memory to HIP until silgpu_pool_trim(). */
+int silgpu_alloc(size_t bytes, void **d_ptr);
+int silgpu_free(void *d_ptr);
+int silgpu_pool_trim(void);
+/* Bytes currently handed out and bytes cached in the pool. */
+int silgpu_pool_stats(size_t *in_use, size_t *cached);
+
+/* Pinned host memory for the host mirror of a storage (hipHostMalloc). */
+int silgpu_host_alloc(size_t bytes, void **h_ptr);
+int silgpu_host_free(void *h_ptr);
+
+/* Copies, ordered on the library stream.  h2d returns once the source may be
+ * reused; d2h returns once the destination holds the data; d2d is async.
+ * Together they stand in for the host's direct access to MTLBuffer contents
+ * (include/unified_memory.h:76, include/array.h:951-958). */
+int silgpu_memcpy_h2d(void *d_dst, const void *h_src, size_t bytes);
+int silgpu_memcpy_d2h(void *h_dst, const void *d_src, size_t bytes);
+int silgpu_memcpy_d2d(void *d_dst, const void *d_src, size_t bytes);
+
+/* d[i] = value for i < n (4-byte elements).  Replaces the host fill in
+ * array::constants (include/array.h:1268-1272) for device-resident data. */
+int silgpu_fill_u32(void *d_dst, uint32_t value, int64_t n);
+
+/* ---- elementwise -------------------------------------------------------- */
+
+/* out[i] = a[i % a_len] op b[i % b_len] for i < n, op in SILGPU_ADD..POW.
+ * Replaces gpu::add/sub/mul/div/pow (include/gpu.h:289-312) and
+ * arithmetic_dispatch_ (include/gpu.h:1331-1369).  Float pow is powf; int
+ * pow rounds powf of the float-converted operands (gpu_kernels.metal:860-862);
+ * int division truncates. */
+int silgpu_binary_f32(int op, const float *d_a, int64_t a_len, const float *d_b,
+                      int64_t b_len, float *d_out, int64_t n);
+int silgpu_binary_i32(int op, const int32_t *d_a, int64_t a_len, const int32_t *d_b,
+                      int64_t b_len, int32_t *d_out, int64_t n);
+
+/* Stride-based broadcast: out (contiguous, shape[0..ndim)) = a op b where a
+ * and b are read through element strides (0 on broadcast axes).  ndim <= 8.
+ * Covers the cases the reference materialises on the host
+ * (include/array.h:2500-2518) and middle-axis broadcasts that its i%len rule
+ * cannot express (include/gpu_kernels.metal:838-841). */
+int silgpu_binary_strided_f32(int op, int ndim, const int64_t *shape, const float *d_a,
+                              const int64_t *a_strides, const float *d_b,
+                              const int64_t *b_strides, float *d_out);
+
+/* out[i] = f(in[i]), f = SILGPU_SIGMOID | SILGPU_RELU.  Replaces gpu::sigmoid
+ * and gpu::relu (include/gpu.h:314-320, 1008-1031). */
+int silgpu_unary_f32(int op, const float *d_in, float *d_out, int64_t n);
+
+/* out[i] = dout[i]*s*(1-s), s = sigmoid(x[i]).  Replaces gpu::sigmoid_backward
+ * (include/gpu.h:945-962). */
+int silgpu_sigmoid_backward_f32(const float *d_dout, const float *d_x, float *d_out,
+                                int64_t n);
+
+/* In place: data[i] = sigmoid(data[i] + bias[i % cols]).  Replaces
+ * gpu::bias_sigmoid (include/gpu.h:965-982). */
+int silgpu_bias_sigmoid_f32(float *d_data, const float *d_bias, int64_t n, int64_t cols);
+
+/* out[i] = in[i]*scale + offset (one rounding: fused multiply-add).  Replaces
+ * gpu::affine (include/gpu.h:985-1004). */
+int silgpu_affine_f32(const float *d_in, float *d_out, int64_t n, float scale,
+                      float offset);
+
+/* Fused elementwise program: the lowering target of sil::eval() for chains of
+ * elementwise nodes (include/array.h:1888-2022, 2836-2888), one HBM pass for a
+ * whole chain.  A program is a list of register-machine instructions over
+ * n_inputs input streams; every instruction rounds to fp32, no contraction,
+ * so the result equals node-by-node fp32 evaluation. */
+#define SILGPU_PROG_MAX_INPUTS 8
+#define SILGPU_PROG_MAX_INSTRS 64
+#define SILGPU_PROG_MAX_REGS 8
+#define SILGPU_PROG_MAX_DIMS 6
+
+/* instruction opcodes */
+#define SILGPU_PI_LOAD 0    /* r[dst] = input[a] at this element */
+#define SILGPU_PI_CONST 1   /* r[dst] = imm */
+#define SILGPU_PI_ADD 2     /* r[dst] = r[a] + r[b] */
+#define SILGPU_PI_SUB 3     /* r[dst] = r[a] - r[b] */
+#define SILGPU_PI_MUL 4     /* r[dst] = r[a] * r[b] */
+#define SILGPU_PI_DIV 5     /* r[dst] = r[a] / r[b] */
+#define SILGPU_PI_POW 6     /* r[dst] = powf(r[a], r[b]) */
+#define SILGPU_PI_ADDI 7    /* r[dst] = r[a] + imm */
+#define SILGPU_PI_MULI 8    /* r[dst] = r[a] * imm */
+#define SILGPU_PI_RSUBI 9   /* r[dst] = imm - r[a] */
+#define SILGPU_PI_RDIVI 10  /* r[dst] = imm / r[a] */
+#define SILGPU_PI_SIGMOID 11 /* r[dst] = 1/(1+exp(-r[a])) */
+#define SILGPU_PI_RELU 12   /* r[dst] = max(r[a], 0) */
+#define SILGPU_PI_FMAI 13   /* r[dst] = fma(r[a], imm, imm2) (reference affine node) */
+#define SILGPU_PI_SIGBWD 14 /* r[dst] = r[b]*s*(1-s), s = sigmoid(r[a]) */
+
+typedef struct silgpu_prog_instr {
+  int32_t op;
+  int32_t dst;
+  int32_t a;
+  int32_t b;
+  float imm;
+  float imm2;
+} silgpu_prog_instr;
+
+typedef struct silgpu_prog_input {
+  const float *ptr;                          /* device pointer */
+  int64_t strides[SILGPU_PROG_MAX_DIMS];     /* element strides, 0 = broadcast */
+} silgpu_prog_input;
+
+typedef struct silgpu_program {
+  int32_t n_inputs;
+  int32_t n_instrs;
+  int32_t ndim;                              /* output rank (<= 6) */
+  int32_t out_reg;                           /* register holding the result */
+  int64_t shape[SILGPU_PROG_MAX_DIMS];       /* output shape, row-major */
+  silgpu_prog_input inputs[SILGPU_PROG_MAX_INPUTS];
+  silgpu_prog_instr instrs[SILGPU_PROG_MAX_INSTRS];
+} silgpu_program;
+
+int silgpu_program_f32(const silgpu_program *prog, float *d_out);
+
+/* ---- reductions --------------------------------------------------------- */
+
+/* *d_out = sum / min / max of d_in[0..n).  One launch, device-side final
+ * reduction, fp64 accumulation for the sum.  Replaces gpu::sum_f32 /
+ * min_f32 / max_f32 plus the host finish (include/gpu.h:323-354, 409-470;
+ * include/array.h:1535-1545, 1612-1619, 1642-1649).  n == 0 gives 0 for sum
+ * and SILGPU_ERR_INVALID for min/max. */
+int silgpu_sum_f32(const float *d_in, int64_t n, float *d_out);
+int silgpu_min_f32(const float *d_in, int64_t n, float *d_out);
+int silgpu_max_f32(const float *d_in, int64_t n, float *d_out);
+
+/* Sum over the middle axis of a contiguous [outer, axis_len, inner] array:
+ * out[o, i] = sum_a in[o, a, i].  Covers array::sum(axis) for every axis
+ * (include/array.h:1554-1583, 2275-2319): gpu::sum_axis0_f32
+ * (include/gpu.h:385-406) is outer == 1, and the reference's CPU-only
+ * sum(axis != 0) (include/array.h:2303-2316) is the rest. */
+int silgpu_sum_axis_f32(const float *d_in, int64_t outer, int64_t axis_len,
+                        int64_t inner, float *d_out);
+
+/* out[r] = first index of the maximum of row r of a contiguous [rows, cols]
+ * array (NaN never wins).  Replaces gpu::argmax_f32 (include/gpu.h:890-913);
+ * long rows are split across workgroups. */
+int silgpu_argmax_rows_f32(const float *d_in, int64_t rows, int64_t cols,
+                           int32_t *d_out);
+
+/* ---- row ops ------------------------------------------------------------ */
+
+/* Row softmax of a contiguous [rows, cols] array: exp(x - rowmax) / sum.
+ * Replaces gpu::softmax (include/gpu.h:916-942). */
+int silgpu_softmax_rows_f32(const float *d_in, float *d_out, int64_t rows, int64_t cols);
+
+/* Row layer_norm: (x - mean) / sqrt(var + eps) * gamma + beta with the
+ * two-pass variance of cpu::layer_norm (include/cpu.h:352-373).  Replaces
+ * gpu::layer_norm (include/gpu.h:473-501). */
+int silgpu_layer_norm_rows_f32(const float *d_in, float *d_out, const float *d_gamma,
+                               const float *d_beta, int64_t rows, int64_t cols,
+                               float eps);
+
+/* ---- matrix products ---------------------------------------------------- */
+
+/* C[b] = epilogue(op(A[b]) * op(B[b])) for b < batch, row-major.
+ *   op(A) is M x K: A[m*lda + k] (trans_a = 0) or A[k*lda + m] (trans_a = 1)
+ *   op(B) is K x N: B[k*ldb + n] (trans_b = 0) or B[n*ldb + k] (trans_b = 1)
+ *   C[m*ldc + n]; batch b adds b*stride_{a,b,c}.
+ *   bias (EPI_BIAS*, may be NULL otherwise) is read as bias[n % bias_len].
+ * One entry point for every reference GEMM: gpu::sgemm / sgemm_batched /
+ * sgemm_steel / sgemm_steel_batched / sgemm_bias_steel /
+ * sgemm_bias_sigmoid_steel / sgemv / mps::dot_f32_ex (include/gpu.h:509-535,
+ * 549-590, 609-615, 1296-1328).  The library picks the kernel (fp32 MFMA
+ * tiles, split-K, GEMV) from the shape. */
+int silgpu_sgemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                 const float *d_A, int64_t lda, int64_t stride_a, const float *d_B,
+                 int64_t ldb, int64_t stride_b, float *d_C, int64_t ldc,
+                 int64_t stride_c, int64_t batch, const float *d_bias,
+                 int64_t bias_len, int epilogue);
+
+/* y[1 x N] = x[1 x K] * B[K x N] (B row-major, ldb >= N).  Replaces gpu::sgemv
+ * (include/gpu.h:549-574).  silgpu_sgemm routes M == 1 here as well. */
+int silgpu_sgemv(const float *d_x, const float *d_B, int64_t ldb, float *d_y, int64_t N,
+                 int64_t K);
+
+/* ---- timing (no reference counterpart; used by bench.py) ---------------- */
+
+/* Events recorded on the library stream, for kernel time of back-to-back
+ * launches. */
+int silgpu_event_create(void **ev);
+int silgpu_event_destroy(void *ev);
+int silgpu_event_record(void *ev);
+int silgpu_event_elapsed_ms(void *ev_start, void *ev_end, float *ms);
+
+/* The library's hipStream_t, for callers that interoperate with it. */
+int silgpu_get_stream(void **stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SILGPU_H */

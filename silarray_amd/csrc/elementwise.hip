@@ -1,0 +1,719 @@
+// Elementwise kernels: binary ops with the reference's i % len broadcast,
+// stride-based broadcast, unary ops, affine, bias+sigmoid, sigmoid backward,
+// fills and the fused elementwise program that sil::eval() lowers chains to.
+//
+// All of these are HBM-bound: 8 (unary) or 12 (binary) bytes per element.
+// Each thread moves 16-byte vectors (global_load_dwordx4) in a grid-stride
+// loop so a launch keeps enough bytes in flight to approach HBM bandwidth.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "internal.h"
+
+namespace silgpu {
+namespace {
+
+constexpr int kBlock = 256;
+
+// Grid size for a grid-stride loop over `work` items: enough workgroups to
+// fill 256 CUs several times over, never more than the work needs.
+inline unsigned grid_for(int64_t work, int64_t per_block = kBlock) {
+  int64_t g = cdiv(work, per_block);
+  if (g < 1) g = 1;
+  if (g > 16384) g = 16384;
+  return static_cast<unsigned>(g);
+}
+
+template <int OP>
+__device__ __forceinline__ float apply_f(float a, float b) {
+  if constexpr (OP == SILGPU_ADD) return a + b;
+  else if constexpr (OP == SILGPU_SUB) return a - b;
+  else if constexpr (OP == SILGPU_MUL) return a * b;
+  else if constexpr (OP == SILGPU_DIV) return a / b;
+  else return powf(a, b);
+}
+
+template <int OP>
+__device__ __forceinline__ int32_t apply_i(int32_t a, int32_t b) {
+  if constexpr (OP == SILGPU_ADD) return a + b;
+  else if constexpr (OP == SILGPU_SUB) return a - b;
+  else if constexpr (OP == SILGPU_MUL) return a * b;
+  else if constexpr (OP == SILGPU_DIV) return b == 0 ? 0 : a / b;
+  // gpu_kernels.metal:860-862: round(pow(float(a), float(b)))
+  else return static_cast<int32_t>(rintf(powf(static_cast<float>(a), static_cast<float>(b))));
+}
+
+template <int OP>
+__device__ __forceinline__ float4 apply4(float4 a, float4 b) {
+  return make_float4(apply_f<OP>(a.x, b.x), apply_f<OP>(a.y, b.y), apply_f<OP>(a.z, b.z),
+                     apply_f<OP>(a.w, b.w));
+}
+
+// Both operands full length, 16-byte aligned: pure streaming.
+template <int OP>
+__global__ __launch_bounds__(kBlock) void binary_full_vec(const float4 *__restrict__ a,
+                                                          const float4 *__restrict__ b,
+                                                          float4 *__restrict__ out,
+                                                          int64_t n4) {
+  int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n4; i += stride)
+    out[i] = apply4<OP>(a[i], b[i]);
+}
+
+// One side is a single value (scalar operand, the reference's B_length == 1
+// fast path, gpu_kernels.metal:891-893).  SCALAR_ON_B selects the side.
+template <int OP, bool SCALAR_ON_B>
+__global__ __launch_bounds__(kBlock) void binary_scalar_vec(const float4 *__restrict__ v,
+                                                            const float *__restrict__ s,
+                                                            float4 *__restrict__ out,
+                                                            int64_t n4) {
+  float sv = s[0];
+  float4 s4 = make_float4(sv, sv, sv, sv);
+  int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n4; i += stride)
+    out[i] = SCALAR_ON_B ? apply4<OP>(v[i], s4) : apply4<OP>(s4, v[i]);
+}
+
+// Full-length operand against a repeating operand whose length is a multiple
+// of 4 (row-vector bias add and the like).  ROW_ON_B selects the side.
+template <int OP, bool ROW_ON_B>
+__global__ __launch_bounds__(kBlock) void binary_row_vec(const float4 *__restrict__ v,
+                                                         const float4 *__restrict__ row,
+                                                         float4 *__restrict__ out,
+                                                         int64_t n4, int64_t row4) {
+  int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n4; i += stride) {
+    float4 r = row[i % row4];
+    out[i] = ROW_ON_B ? apply4<OP>(v[i], r) : apply4<OP>(r, v[i]);
+  }
+}
+
+// General rule of the reference kernel: out[i] = a[i % a_len] op b[i % b_len]
+// (gpu_kernels.metal:826-842), one element per thread iteration.
+template <int OP, typename T>
+__global__ __launch_bounds__(kBlock) void binary_mod(const T *__restrict__ a, int64_t a_len,
+                                                     const T *__restrict__ b, int64_t b_len,
+                                                     T *__restrict__ out, int64_t n) {
+  int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+    T x = a[a_len == n ? i : i % a_len];
+    T y = b[b_len == n ? i : i % b_len];
+    if constexpr (sizeof(T) == 4 && std::is_same<T, float>::value)
+      out[i] = apply_f<OP>(x, y);
+    else
+      out[i] = apply_i<OP>(x, y);
+  }
+}
+
+struct strided_args {
+  int ndim;
+  int64_t shape[8];
+  int64_t sa[8];
+  int64_t sb[8];
+};
+
+template <int OP>
+__global__ __launch_bounds__(kBlock) void binary_strided(const float *__restrict__ a,
+                                                         const float *__restrict__ b,
+                                                         float *__restrict__ out, int64_t n,
+                                                         strided_args g) {
+  int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+    int64_t rem = i, oa = 0, ob = 0;
+    for (int d = g.ndim - 1; d >= 0; --d) {
+      int64_t idx = rem % g.shape[d];
+      rem /= g.shape[d];
+      oa += idx * g.sa[d];
+      ob += idx * g.sb[d];
+    }
+    out[i] = apply_f<OP>(a[oa], b[ob]);
+  }
+}
+
+template <int OP>
+int launch_binary_f32(const float *a, int64_t a_len, const float *b, int64_t b_len,
+                      float *out, int64_t n, hipStream_t s) {
+  bool al = aligned16(a) && aligned16(b) && aligned16(out);
+  if (al && n % 4 == 0) {
+    int64_t n4 = n / 4;
+    if (a_len == n && b_len == n) {
+      binary_full_vec<OP><<<grid_for(n4), kBlock, 0, s>>>(
+          reinterpret_cast<const float4 *>(a), reinterpret_cast<const float4 *>(b),
+          reinterpret_cast<float4 *>(out), n4);
+      SILGPU_LAUNCH_CHECK("binary_full_vec");
+      return SILGPU_OK;
+    }
+    if (a_len == n && b_len == 1) {
+      binary_scalar_vec<OP, true><<<grid_for(n4), kBlock, 0, s>>>(
+          reinterpret_cast<const float4 *>(a), b, reinterpret_cast<float4 *>(out), n4);
+      SILGPU_LAUNCH_CHECK("binary_scalar_vec");
+      return SILGPU_OK;
+    }
+    if (b_len == n && a_len == 1) {
+      binary_scalar_vec<OP, false><<<grid_for(n4), kBlock, 0, s>>>(
+          reinterpret_cast<const float4 *>(b), a, reinterpret_cast<float4 *>(out), n4);
+      SILGPU_LAUNCH_CHECK("binary_scalar_vec");
+      return SILGPU_OK;
+    }
+    if (a_len == n && b_len % 4 == 0 && n % b_len == 0) {
+      binary_row_vec<OP, true><<<grid_for(n4), kBlock, 0, s>>>(
+          reinterpret_cast<const float4 *>(a), reinterpret_cast<const float4 *>(b),
+          reinterpret_cast<float4 *>(out), n4, b_len / 4);
+      SILGPU_LAUNCH_CHECK("binary_row_vec");
+      return SILGPU_OK;
+    }
+    if (b_len == n && a_len % 4 == 0 && n % a_len == 0) {
+      binary_row_vec<OP, false><<<grid_for(n4), kBlock, 0, s>>>(
+          reinterpret_cast<const float4 *>(b), reinterpret_cast<const float4 *>(a),
+          reinterpret_cast<float4 *>(out), n4, a_len / 4);
+      SILGPU_LAUNCH_CHECK("binary_row_vec");
+      return SILGPU_OK;
+    }
+  }
+  binary_mod<OP, float><<<grid_for(n), kBlock, 0, s>>>(a, a_len, b, b_len, out, n);
+  SILGPU_LAUNCH_CHECK("binary_mod<f32>");
+  return SILGPU_OK;
+}
+
+// ---- unary ------------------------------------------------------------------
+
+template <int OP>
+__device__ __forceinline__ float unary_f(float x) {
+  if constexpr (OP == SILGPU_SIGMOID) return sigmoidf_dev(x);
+  else return fmaxf(x, 0.0f);
+}
+
+template <int OP>
+__global__ __launch_bounds__(kBlock) void unary_vec(const float4 *__restrict__ in,
+                                                    float4 *__restrict__ out, int64_t n4) {
+  int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n4; i += stride) {
+    float4 v = in[i];
+    out[i] = make_float4(unary_f<OP>(v.x), unary_f<OP>(v.y), unary_f<OP>(v.z),
+                         unary_f<OP>(v.w));
+  }
+}
+
+template <int OP>
+__global__ __launch_bounds__(kBlock) void unary_scalar(const float *__restrict__ in,
+                                                       float *__restrict__ out, int64_t n) {
+  int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+    out[i] = unary_f<OP>(in[i]);
+}
+
+template <int OP>
+int launch_unary(const float *in, float *out, int64_t n, hipStream_t s) {
+  if (aligned16(in) && aligned16(out) && n % 4 == 0) {
+    unary_vec<OP><<<grid_for(n / 4), kBlock, 0, s>>>(
+        reinterpret_cast<const float4 *>(in), reinterpret_cast<float4 *>(out), n / 4);
+    SILGPU_LAUNCH_CHECK("unary_vec");
+  } else {
+    unary_scalar<OP><<<grid_for(n), kBlock, 0, s>>>(in, out, n);
+    SILGPU_LAUNCH_CHECK("unary_scalar");
+  }
+  return SILGPU_OK;
+}
+
+__global__ __launch_bounds__(kBlock) void sigmoid_backward_k(const float *__restrict__ dout,
+                                                             const float *__restrict__ x,
+                                                             float *__restrict__ out,
+                                                             int64_t n) {
+  int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+    float s = sigmoidf_dev(x[i]);
+    out[i] = dout[i] * s * (1.0f - s);
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void bias_sigmoid_k(float *__restrict__ data,
+                                                         const float *__restrict__ bias,
+                                                         int64_t n, int64_t cols) {
+  int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+    data[i] = sigmoidf_dev(data[i] + bias[i % cols]);
+}
+
+__global__ __launch_bounds__(kBlock) void affine_vec(const float4 *__restrict__ in,
+                                                     float4 *__restrict__ out, int64_t n4,
+                                                     float scale, float offset) {
+  int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n4; i += stride) {
+    float4 v = in[i];
+    out[i] = make_float4(fmaf(v.x, scale, offset), fmaf(v.y, scale, offset),
+                         fmaf(v.z, scale, offset), fmaf(v.w, scale, offset));
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void affine_scalar(const float *__restrict__ in,
+                                                        float *__restrict__ out, int64_t n,
+                                                        float scale, float offset) {
+  int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+    out[i] = fmaf(in[i], scale, offset);
+}
+
+__global__ __launch_bounds__(kBlock) void fill_u32_k(uint32_t *__restrict__ d, uint32_t v,
+                                                     int64_t n) {
+  int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) d[i] = v;
+}
+
+// ---- fused elementwise program ------------------------------------------------
+//
+// Each thread evaluates the program for kVec consecutive output elements per
+// grid-stride step.  Register indices are uniform across the workgroup, so
+// the switch statements below become scalar branches and the per-element
+// values stay in VGPRs.  Every operation rounds to fp32 (the file is compiled
+// with -ffp-contract=off), which makes the fused result bit-identical to
+// evaluating the graph node by node.
+
+constexpr int kVec = 8;
+
+struct vreg {
+  float v[kVec];
+};
+
+// Uniform-index register access by value: every case names a constant index,
+// so the register file is scalar-replaced into VGPRs instead of scratch.
+__device__ __forceinline__ vreg reg_get(const vreg (&r)[SILGPU_PROG_MAX_REGS], int i) {
+  switch (i) {
+    case 0: return r[0];
+    case 1: return r[1];
+    case 2: return r[2];
+    case 3: return r[3];
+    case 4: return r[4];
+    case 5: return r[5];
+    case 6: return r[6];
+    default: return r[7];
+  }
+}
+
+__device__ __forceinline__ void reg_set(vreg (&r)[SILGPU_PROG_MAX_REGS], int i,
+                                        const vreg &v) {
+  switch (i) {
+    case 0: r[0] = v; break;
+    case 1: r[1] = v; break;
+    case 2: r[2] = v; break;
+    case 3: r[3] = v; break;
+    case 4: r[4] = v; break;
+    case 5: r[5] = v; break;
+    case 6: r[6] = v; break;
+    default: r[7] = v; break;
+  }
+}
+
+struct prog_launch {
+  silgpu_program p;
+  int32_t mode[SILGPU_PROG_MAX_INPUTS];  // 0 contiguous, 1 scalar, 2 strided
+};
+
+__device__ __forceinline__ int64_t strided_offset(const silgpu_program &p, int in,
+                                                  int64_t i) {
+  int64_t rem = i, off = 0;
+  for (int d = p.ndim - 1; d >= 0; --d) {
+    int64_t idx = rem % p.shape[d];
+    rem /= p.shape[d];
+    off += idx * p.inputs[in].strides[d];
+  }
+  return off;
+}
+
+__global__ __launch_bounds__(kBlock) void program_k(prog_launch L, float *__restrict__ out,
+                                                    int64_t n) {
+  const silgpu_program &p = L.p;
+  int64_t stride = int64_t(gridDim.x) * kBlock * kVec;
+  for (int64_t base = (int64_t(blockIdx.x) * kBlock + threadIdx.x) * kVec; base < n;
+       base += stride) {
+    const bool full = base + kVec <= n;
+    vreg r[SILGPU_PROG_MAX_REGS];
+    for (int pc = 0; pc < p.n_instrs; ++pc) {
+      const silgpu_prog_instr ins = p.instrs[pc];
+      vreg d;
+      switch (ins.op) {
+        case SILGPU_PI_LOAD: {
+          const float *src = p.inputs[ins.a].ptr;
+          int mode = L.mode[ins.a];
+          if (mode == 1) {
+            float s = src[0];
+#pragma unroll
+            for (int e = 0; e < kVec; ++e) d.v[e] = s;
+          } else if (mode == 0 && full) {
+#pragma unroll
+            for (int e = 0; e < kVec; ++e) d.v[e] = src[base + e];
+          } else {
+#pragma unroll
+            for (int e = 0; e < kVec; ++e) {
+              int64_t i = base + e;
+              if (i < n) d.v[e] = src[mode == 0 ? i : strided_offset(p, ins.a, i)];
+            }
+          }
+          break;
+        }
+        case SILGPU_PI_CONST:
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) d.v[e] = ins.imm;
+          break;
+        case SILGPU_PI_ADD: {
+          vreg a = reg_get(r, ins.a), b = reg_get(r, ins.b);
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) d.v[e] = a.v[e] + b.v[e];
+          break;
+        }
+        case SILGPU_PI_SUB: {
+          vreg a = reg_get(r, ins.a), b = reg_get(r, ins.b);
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) d.v[e] = a.v[e] - b.v[e];
+          break;
+        }
+        case SILGPU_PI_MUL: {
+          vreg a = reg_get(r, ins.a), b = reg_get(r, ins.b);
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) d.v[e] = a.v[e] * b.v[e];
+          break;
+        }
+        case SILGPU_PI_DIV: {
+          vreg a = reg_get(r, ins.a), b = reg_get(r, ins.b);
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) d.v[e] = a.v[e] / b.v[e];
+          break;
+        }
+        case SILGPU_PI_POW: {
+          vreg a = reg_get(r, ins.a), b = reg_get(r, ins.b);
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) d.v[e] = powf(a.v[e], b.v[e]);
+          break;
+        }
+        case SILGPU_PI_ADDI: {
+          vreg a = reg_get(r, ins.a);
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) d.v[e] = a.v[e] + ins.imm;
+          break;
+        }
+        case SILGPU_PI_MULI: {
+          vreg a = reg_get(r, ins.a);
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) d.v[e] = a.v[e] * ins.imm;
+          break;
+        }
+        case SILGPU_PI_RSUBI: {
+          vreg a = reg_get(r, ins.a);
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) d.v[e] = ins.imm - a.v[e];
+          break;
+        }
+        case SILGPU_PI_RDIVI: {
+          vreg a = reg_get(r, ins.a);
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) d.v[e] = ins.imm / a.v[e];
+          break;
+        }
+        case SILGPU_PI_SIGMOID: {
+          vreg a = reg_get(r, ins.a);
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) d.v[e] = sigmoidf_dev(a.v[e]);
+          break;
+        }
+        case SILGPU_PI_RELU: {
+          vreg a = reg_get(r, ins.a);
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) d.v[e] = fmaxf(a.v[e], 0.0f);
+          break;
+        }
+        case SILGPU_PI_FMAI: {
+          vreg a = reg_get(r, ins.a);
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) d.v[e] = fmaf(a.v[e], ins.imm, ins.imm2);
+          break;
+        }
+        case SILGPU_PI_SIGBWD: {
+          vreg a = reg_get(r, ins.a), b = reg_get(r, ins.b);
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) {
+            float s = sigmoidf_dev(a.v[e]);
+            d.v[e] = b.v[e] * s * (1.0f - s);
+          }
+          break;
+        }
+        default:
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) d.v[e] = 0.0f;
+          break;
+      }
+      reg_set(r, ins.dst, d);
+    }
+    const vreg res = reg_get(r, p.out_reg);
+    if (full) {
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) out[base + e] = res.v[e];
+    } else {
+      for (int e = 0; e < kVec; ++e)
+        if (base + e < n) out[base + e] = res.v[e];
+    }
+  }
+}
+
+// Program that is one input followed only by FMAI on the same register: the
+// lowering of a chain of scalar affine nodes (x*a+b repeated).  No register
+// file, so the loop body is one fma per element per step.
+struct chain_launch {
+  const float *in;
+  int32_t n_steps;
+  float scale[SILGPU_PROG_MAX_INSTRS];
+  float offset[SILGPU_PROG_MAX_INSTRS];
+};
+
+constexpr int kChainVec = 4;  // float4s per thread per grid-stride step
+
+__global__ __launch_bounds__(kBlock) void affine_chain_k(chain_launch L,
+                                                         float4 *__restrict__ out,
+                                                         int64_t n4) {
+  const float4 *in = reinterpret_cast<const float4 *>(L.in);
+  int64_t stride = int64_t(gridDim.x) * kBlock * kChainVec;
+  for (int64_t base = int64_t(blockIdx.x) * kBlock * kChainVec + threadIdx.x; base < n4;
+       base += stride) {
+    float4 v[kChainVec];
+#pragma unroll
+    for (int u = 0; u < kChainVec; ++u) {
+      int64_t i = base + int64_t(u) * kBlock;
+      v[u] = i < n4 ? in[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    for (int s = 0; s < L.n_steps; ++s) {
+      float a = L.scale[s], b = L.offset[s];
+#pragma unroll
+      for (int u = 0; u < kChainVec; ++u) {
+        v[u].x = fmaf(v[u].x, a, b);
+        v[u].y = fmaf(v[u].y, a, b);
+        v[u].z = fmaf(v[u].z, a, b);
+        v[u].w = fmaf(v[u].w, a, b);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kChainVec; ++u) {
+      int64_t i = base + int64_t(u) * kBlock;
+      if (i < n4) out[i] = v[u];
+    }
+  }
+}
+
+}  // namespace
+}  // namespace silgpu
+
+using namespace silgpu;
+
+#define SILGPU_DISPATCH_OP(op, FN, ...)                                           \
+  switch (op) {                                                                   \
+    case SILGPU_ADD: return FN<SILGPU_ADD>(__VA_ARGS__);                          \
+    case SILGPU_SUB: return FN<SILGPU_SUB>(__VA_ARGS__);                          \
+    case SILGPU_MUL: return FN<SILGPU_MUL>(__VA_ARGS__);                          \
+    case SILGPU_DIV: return FN<SILGPU_DIV>(__VA_ARGS__);                          \
+    case SILGPU_POW: return FN<SILGPU_POW>(__VA_ARGS__);                          \
+    default: return set_error(SILGPU_ERR_INVALID, "unknown binary op %d", op);    \
+  }
+
+namespace {
+
+template <int OP>
+int launch_binary_i32(const int32_t *a, int64_t a_len, const int32_t *b, int64_t b_len,
+                      int32_t *out, int64_t n, hipStream_t s) {
+  binary_mod<OP, int32_t><<<grid_for(n), kBlock, 0, s>>>(a, a_len, b, b_len, out, n);
+  SILGPU_LAUNCH_CHECK("binary_mod<i32>");
+  return SILGPU_OK;
+}
+
+template <int OP>
+int launch_strided(const float *a, const float *b, float *out, int64_t n,
+                   const strided_args &g, hipStream_t s) {
+  binary_strided<OP><<<grid_for(n), kBlock, 0, s>>>(a, b, out, n, g);
+  SILGPU_LAUNCH_CHECK("binary_strided");
+  return SILGPU_OK;
+}
+
+int check_binary_lens(int64_t a_len, int64_t b_len, int64_t n) {
+  SILGPU_REQUIRE(n >= 0, "binary: n = %lld is negative", (long long)n);
+  if (n == 0) return SILGPU_OK;
+  SILGPU_REQUIRE(a_len > 0 && b_len > 0, "binary: operand length 0 with n = %lld",
+                 (long long)n);
+  return SILGPU_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int silgpu_binary_f32(int op, const float *d_a, int64_t a_len, const float *d_b,
+                      int64_t b_len, float *d_out, int64_t n) {
+  int rc = check_binary_lens(a_len, b_len, n);
+  if (rc != SILGPU_OK || n == 0) return rc;
+  SILGPU_REQUIRE(d_a && d_b && d_out, "silgpu_binary_f32: null pointer");
+  SILGPU_CTX(c);
+  SILGPU_DISPATCH_OP(op, launch_binary_f32, d_a, a_len, d_b, b_len, d_out, n, c->stream);
+}
+
+int silgpu_binary_i32(int op, const int32_t *d_a, int64_t a_len, const int32_t *d_b,
+                      int64_t b_len, int32_t *d_out, int64_t n) {
+  int rc = check_binary_lens(a_len, b_len, n);
+  if (rc != SILGPU_OK || n == 0) return rc;
+  SILGPU_REQUIRE(d_a && d_b && d_out, "silgpu_binary_i32: null pointer");
+  SILGPU_CTX(c);
+  SILGPU_DISPATCH_OP(op, launch_binary_i32, d_a, a_len, d_b, b_len, d_out, n, c->stream);
+}
+
+int silgpu_binary_strided_f32(int op, int ndim, const int64_t *shape, const float *d_a,
+                              const int64_t *a_strides, const float *d_b,
+                              const int64_t *b_strides, float *d_out) {
+  SILGPU_REQUIRE(ndim >= 0 && ndim <= 8, "silgpu_binary_strided_f32: ndim %d not in [0, 8]",
+                 ndim);
+  SILGPU_REQUIRE(ndim == 0 || (shape && a_strides && b_strides),
+                 "silgpu_binary_strided_f32: null shape/strides");
+  strided_args g{};
+  g.ndim = ndim;
+  int64_t n = 1;
+  for (int d = 0; d < ndim; ++d) {
+    SILGPU_REQUIRE(shape[d] >= 0, "silgpu_binary_strided_f32: negative extent");
+    g.shape[d] = shape[d];
+    g.sa[d] = a_strides[d];
+    g.sb[d] = b_strides[d];
+    n *= shape[d];
+  }
+  if (n == 0) return SILGPU_OK;
+  SILGPU_REQUIRE(d_a && d_b && d_out, "silgpu_binary_strided_f32: null pointer");
+  SILGPU_CTX(c);
+  SILGPU_DISPATCH_OP(op, launch_strided, d_a, d_b, d_out, n, g, c->stream);
+}
+
+int silgpu_unary_f32(int op, const float *d_in, float *d_out, int64_t n) {
+  SILGPU_REQUIRE(n >= 0, "silgpu_unary_f32: negative n");
+  if (n == 0) return SILGPU_OK;
+  SILGPU_REQUIRE(d_in && d_out, "silgpu_unary_f32: null pointer");
+  SILGPU_CTX(c);
+  switch (op) {
+    case SILGPU_SIGMOID: return launch_unary<SILGPU_SIGMOID>(d_in, d_out, n, c->stream);
+    case SILGPU_RELU: return launch_unary<SILGPU_RELU>(d_in, d_out, n, c->stream);
+    default: return set_error(SILGPU_ERR_INVALID, "unknown unary op %d", op);
+  }
+}
+
+int silgpu_sigmoid_backward_f32(const float *d_dout, const float *d_x, float *d_out,
+                                int64_t n) {
+  SILGPU_REQUIRE(n >= 0, "silgpu_sigmoid_backward_f32: negative n");
+  if (n == 0) return SILGPU_OK;
+  SILGPU_REQUIRE(d_dout && d_x && d_out, "silgpu_sigmoid_backward_f32: null pointer");
+  SILGPU_CTX(c);
+  sigmoid_backward_k<<<grid_for(n), kBlock, 0, c->stream>>>(d_dout, d_x, d_out, n);
+  SILGPU_LAUNCH_CHECK("sigmoid_backward_k");
+  return SILGPU_OK;
+}
+
+int silgpu_bias_sigmoid_f32(float *d_data, const float *d_bias, int64_t n, int64_t cols) {
+  SILGPU_REQUIRE(n >= 0 && cols > 0, "silgpu_bias_sigmoid_f32: bad n/cols");
+  if (n == 0) return SILGPU_OK;
+  SILGPU_REQUIRE(d_data && d_bias, "silgpu_bias_sigmoid_f32: null pointer");
+  SILGPU_CTX(c);
+  bias_sigmoid_k<<<grid_for(n), kBlock, 0, c->stream>>>(d_data, d_bias, n, cols);
+  SILGPU_LAUNCH_CHECK("bias_sigmoid_k");
+  return SILGPU_OK;
+}
+
+int silgpu_affine_f32(const float *d_in, float *d_out, int64_t n, float scale,
+                      float offset) {
+  SILGPU_REQUIRE(n >= 0, "silgpu_affine_f32: negative n");
+  if (n == 0) return SILGPU_OK;
+  SILGPU_REQUIRE(d_in && d_out, "silgpu_affine_f32: null pointer");
+  SILGPU_CTX(c);
+  if (aligned16(d_in) && aligned16(d_out) && n % 4 == 0) {
+    affine_vec<<<grid_for(n / 4), kBlock, 0, c->stream>>>(
+        reinterpret_cast<const float4 *>(d_in), reinterpret_cast<float4 *>(d_out), n / 4,
+        scale, offset);
+    SILGPU_LAUNCH_CHECK("affine_vec");
+  } else {
+    affine_scalar<<<grid_for(n), kBlock, 0, c->stream>>>(d_in, d_out, n, scale, offset);
+    SILGPU_LAUNCH_CHECK("affine_scalar");
+  }
+  return SILGPU_OK;
+}
+
+int silgpu_fill_u32(void *d_dst, uint32_t value, int64_t n) {
+  SILGPU_REQUIRE(n >= 0, "silgpu_fill_u32: negative n");
+  if (n == 0) return SILGPU_OK;
+  SILGPU_REQUIRE(d_dst != nullptr, "silgpu_fill_u32: null pointer");
+  SILGPU_CTX(c);
+  fill_u32_k<<<grid_for(n), kBlock, 0, c->stream>>>(static_cast<uint32_t *>(d_dst), value,
+                                                     n);
+  SILGPU_LAUNCH_CHECK("fill_u32_k");
+  return SILGPU_OK;
+}
+
+int silgpu_program_f32(const silgpu_program *prog, float *d_out) {
+  SILGPU_REQUIRE(prog != nullptr, "silgpu_program_f32: prog is null");
+  const silgpu_program &p = *prog;
+  SILGPU_REQUIRE(p.n_inputs >= 0 && p.n_inputs <= SILGPU_PROG_MAX_INPUTS,
+                 "silgpu_program_f32: n_inputs %d out of range", p.n_inputs);
+  SILGPU_REQUIRE(p.n_instrs >= 1 && p.n_instrs <= SILGPU_PROG_MAX_INSTRS,
+                 "silgpu_program_f32: n_instrs %d out of range", p.n_instrs);
+  SILGPU_REQUIRE(p.ndim >= 0 && p.ndim <= SILGPU_PROG_MAX_DIMS,
+                 "silgpu_program_f32: ndim %d out of range", p.ndim);
+  SILGPU_REQUIRE(p.out_reg >= 0 && p.out_reg < SILGPU_PROG_MAX_REGS,
+                 "silgpu_program_f32: out_reg %d out of range", p.out_reg);
+  int64_t n = 1;
+  for (int d = 0; d < p.ndim; ++d) {
+    SILGPU_REQUIRE(p.shape[d] >= 0, "silgpu_program_f32: negative extent");
+    n *= p.shape[d];
+  }
+  if (n == 0) return SILGPU_OK;
+  SILGPU_REQUIRE(d_out != nullptr, "silgpu_program_f32: d_out is null");
+  prog_launch L{};
+  L.p = p;
+  for (int i = 0; i < p.n_inputs; ++i) {
+    SILGPU_REQUIRE(p.inputs[i].ptr != nullptr, "silgpu_program_f32: input %d is null", i);
+    bool all_zero = true, contiguous = true;
+    int64_t expect = 1;
+    for (int d = p.ndim - 1; d >= 0; --d) {
+      if (p.inputs[i].strides[d] != 0) all_zero = false;
+      if (p.shape[d] != 1 && p.inputs[i].strides[d] != expect) contiguous = false;
+      expect *= p.shape[d];
+    }
+    L.mode[i] = all_zero ? 1 : (contiguous ? 0 : 2);
+  }
+  bool chain = p.n_inputs == 1 && L.mode[0] == 0 && p.instrs[0].op == SILGPU_PI_LOAD &&
+               p.instrs[0].a == 0 && p.out_reg == p.instrs[0].dst && n % 4 == 0 &&
+               aligned16(p.inputs[0].ptr) && aligned16(d_out);
+  for (int pc = 0; pc < p.n_instrs; ++pc) {
+    const silgpu_prog_instr &ins = p.instrs[pc];
+    SILGPU_REQUIRE(ins.dst >= 0 && ins.dst < SILGPU_PROG_MAX_REGS && ins.a >= 0 &&
+                       ins.b >= 0 && ins.b < SILGPU_PROG_MAX_REGS,
+                   "silgpu_program_f32: register index out of range at %d", pc);
+    if (ins.op == SILGPU_PI_LOAD)
+      SILGPU_REQUIRE(ins.a < p.n_inputs, "silgpu_program_f32: load of input %d of %d", ins.a,
+                     p.n_inputs);
+    else
+      SILGPU_REQUIRE(ins.a < SILGPU_PROG_MAX_REGS,
+                     "silgpu_program_f32: register index out of range at %d", pc);
+    SILGPU_REQUIRE(ins.op >= SILGPU_PI_LOAD && ins.op <= SILGPU_PI_SIGBWD,
+                   "silgpu_program_f32: unknown opcode %d at %d", ins.op, pc);
+    if (pc > 0 && !(ins.op == SILGPU_PI_FMAI && ins.dst == p.instrs[0].dst &&
+                    ins.a == p.instrs[0].dst))
+      chain = false;
+  }
+  SILGPU_CTX(c);
+  if (chain) {
+    chain_launch C{};
+    C.in = p.inputs[0].ptr;
+    C.n_steps = p.n_instrs - 1;
+    for (int s = 0; s < C.n_steps; ++s) {
+      C.scale[s] = p.instrs[s + 1].imm;
+      C.offset[s] = p.instrs[s + 1].imm2;
+    }
+    int64_t n4 = n / 4;
+    affine_chain_k<<<grid_for(n4, int64_t(kBlock) * kChainVec), kBlock, 0, c->stream>>>(
+        C, reinterpret_cast<float4 *>(d_out), n4);
+    SILGPU_LAUNCH_CHECK("affine_chain_k");
+    return SILGPU_OK;
+  }
+  program_k<<<grid_for(n, int64_t(kBlock) * kVec), kBlock, 0, c->stream>>>(L, d_out, n);
+  SILGPU_LAUNCH_CHECK("program_k");
+  return SILGPU_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,615 @@
+// Matrix products on gfx950: fp32 MFMA SGEMM and HBM-bound GEMV.
+//
+// SGEMM (the reference's STEEL / sgemm_32 / MPS paths, include/gpu.h:509-615,
+// 1296-1328) runs on v_mfma_f32_32x32x2_f32: one instruction multiplies a
+// 32x2 A fragment by a 2x32 B fragment into a 32x32 fp32 accumulator held
+// in 16 registers per lane.  On MI355X this instruction keeps the matrix
+// core busy for 64 cycles, so the kernel's job is to issue one every 64
+// cycles on every SIMD: operands are staged through LDS in k-major tiles
+// (lanes 0-31 read 32 consecutive floats of one k row, lanes 32-63 the
+// next row), the next K tile is fetched into registers while the current
+// one is multiplied (double-buffered LDS, one barrier per K tile), and the
+// workgroup -> tile mapping keeps the workgroups of one XCD on neighbouring
+// tiles so their A and B panels are shared in that XCD's L2.
+//
+// Epilogues (bias, sigmoid, relu) are applied to the accumulators before the
+// single store, so linear / linear_sigmoid are one pass over C.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "internal.h"
+
+namespace silgpu {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// ---- tile mapping -----------------------------------------------------------
+
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup id mod 8).
+// Remap ids so each XCD gets a contiguous range of tiles, then raster that
+// range in groups of kGroupM tile rows so concurrently running tiles share
+// A row panels and B column panels.
+constexpr int kXcds = 8;
+constexpr int kGroupM = 8;
+
+__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int &tm,
+                                            int &tn) {
+  const int nblocks = tiles_m * tiles_n;
+  const int full = (nblocks / kXcds) * kXcds;
+  if (bid < full) bid = (bid % kXcds) * (full / kXcds) + bid / kXcds;
+  const int group_size = kGroupM * tiles_n;
+  const int group = bid / group_size;
+  const int first_m = group * kGroupM;
+  const int gm = min(tiles_m - first_m, kGroupM);
+  const int in_group = bid % group_size;
+  tm = first_m + in_group % gm;
+  tn = in_group / gm;
+}
+
+// ---- SGEMM kernel -----------------------------------------------------------
+
+struct gemm_args {
+  const float *A;
+  const float *B;
+  float *C;
+  const float *bias;
+  int64_t lda, ldb, ldc;
+  int64_t sA, sB, sC;
+  int64_t bias_len;
+  int M, N, K;
+  int tiles_m, tiles_n;
+  int epi;
+};
+
+template <int BM, int BN, int BK, int WM, int WN>
+struct cfg {
+  static constexpr int kThreads = WM * WN * kWave;
+  static constexpr int TM = BM / WM / 32;  // 32x32 MFMA blocks per wave along M
+  static constexpr int TN = BN / WN / 32;
+  static constexpr int LA = BM + 4;        // LDS row pitch (floats), padded
+  static constexpr int LB = BN + 4;
+  static constexpr int kAStage = BK * LA;  // floats per stage
+  static constexpr int kBStage = BK * LB;
+  static constexpr int kLdsBytes = 2 * (kAStage + kBStage) * 4;
+  static constexpr int NA = BM * BK / 4 / kThreads;  // 4-float groups per thread
+  static constexpr int NB = BK * BN / 4 / kThreads;
+  static_assert(TM >= 1 && TN >= 1, "wave tile below 32x32");
+  static_assert(NA >= 1 && NB >= 1 && NA * 4 * kThreads == BM * BK &&
+                    NB * 4 * kThreads == BK * BN,
+                "tile not divisible among threads");
+  static_assert(BK % 4 == 0 && BK % 2 == 0, "BK");
+};
+
+// Loads this thread's share of an R x Cc tile whose *contiguous* global axis
+// has Cc elements (4 per group).  Group f = t + i*NT covers row f / (Cc/4),
+// columns (f % (Cc/4))*4 .. +3.  Out-of-range elements read as 0.
+template <int R, int Cc, int NT, int NG, bool VEC, bool EDGE>
+__device__ __forceinline__ void load_groups(const float *__restrict__ base, int64_t ld,
+                                            int row0, int col0, int rows, int cols, int t,
+                                            float (&g)[NG][4]) {
+  constexpr int GPR = Cc / 4;  // groups per row
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    const int f = t + i * NT;
+    const int r = f / GPR;
+    const int c = (f % GPR) * 4;
+    const int gr = row0 + r, gc = col0 + c;
+    const float *p = base + int64_t(gr) * ld + gc;
+    if constexpr (VEC) {
+      // VEC requires cols % 4 == 0, so a group is entirely in or out.
+      if (!EDGE || (gr < rows && gc < cols)) {
+        float4 v = *reinterpret_cast<const float4 *>(p);
+        g[i][0] = v.x;
+        g[i][1] = v.y;
+        g[i][2] = v.z;
+        g[i][3] = v.w;
+      } else {
+        g[i][0] = g[i][1] = g[i][2] = g[i][3] = 0.0f;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        g[i][j] = (!EDGE || (gr < rows && gc + j < cols)) ? p[j] : 0.0f;
+    }
+  }
+}
+
+// Stores groups into a k-major LDS tile S[k][x] (pitch L).
+//  KMAJOR_GLOBAL = true : the global contiguous axis is x (groups run along
+//                         x within one k row) -> one 16-byte LDS write.
+//  KMAJOR_GLOBAL = false: the global contiguous axis is k (groups run along
+//                         k within one x row) -> four 4-byte writes.
+template <int R, int Cc, int NT, int NG, int L, bool KMAJOR_GLOBAL>
+__device__ __forceinline__ void store_groups(float *__restrict__ S, int t,
+                                             const float (&g)[NG][4]) {
+  constexpr int GPR = Cc / 4;
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    const int f = t + i * NT;
+    const int r = f / GPR;
+    const int c = (f % GPR) * 4;
+    if constexpr (KMAJOR_GLOBAL) {
+      // row r is k, columns c.. are x
+      *reinterpret_cast<float4 *>(S + r * L + c) = make_float4(g[i][0], g[i][1], g[i][2], g[i][3]);
+    } else {
+      // row r is x, columns c.. are k
+#pragma unroll
+      for (int j = 0; j < 4; ++j) S[(c + j) * L + r] = g[i][j];
+    }
+  }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VEC, bool EDGE>
+__global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
+  using C = cfg<BM, BN, BK, WM, WN>;
+  constexpr int NT = C::kThreads;
+  extern __shared__ float lds[];
+  float *As = lds;                    // [2][BK][LA]
+  float *Bs = lds + 2 * C::kAStage;   // [2][BK][LB]
+
+  const int t = threadIdx.x;
+  const int lane = t % kWave;
+  const int wave = t / kWave;
+  const int wm = wave / WN, wn = wave % WN;
+
+  int tm, tn;
+  tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int64_t z = blockIdx.z;
+  const float *__restrict__ A = p.A + z * p.sA;
+  const float *__restrict__ B = p.B + z * p.sB;
+  float *__restrict__ Cp = p.C + z * p.sC;
+  const int M = p.M, N = p.N, K = p.K;
+
+  floatx16 acc[C::TM][C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  float ga[C::NA][4], gb[C::NB][4];
+  // Global views: A non-trans is [M][K] (contiguous K), trans is [K][M].
+  //               B non-trans is [K][N] (contiguous N), trans is [N][K].
+  auto load_a = [&](int k0) {
+    if constexpr (!TA)
+      load_groups<BM, BK, NT, C::NA, VEC, EDGE>(A, p.lda, m0, k0, M, K, t, ga);
+    else
+      load_groups<BK, BM, NT, C::NA, VEC, EDGE>(A, p.lda, k0, m0, K, M, t, ga);
+  };
+  auto load_b = [&](int k0) {
+    if constexpr (!TB)
+      load_groups<BK, BN, NT, C::NB, VEC, EDGE>(B, p.ldb, k0, n0, K, N, t, gb);
+    else
+      load_groups<BN, BK, NT, C::NB, VEC, EDGE>(B, p.ldb, n0, k0, N, K, t, gb);
+  };
+  auto store_a = [&](int stage) {
+    float *S = As + stage * C::kAStage;
+    if constexpr (!TA)
+      store_groups<BM, BK, NT, C::NA, C::LA, false>(S, t, ga);
+    else
+      store_groups<BK, BM, NT, C::NA, C::LA, true>(S, t, ga);
+  };
+  auto store_b = [&](int stage) {
+    float *S = Bs + stage * C::kBStage;
+    if constexpr (!TB)
+      store_groups<BK, BN, NT, C::NB, C::LB, true>(S, t, gb);
+    else
+      store_groups<BN, BK, NT, C::NB, C::LB, false>(S, t, gb);
+  };
+
+  const int KT = (K + BK - 1) / BK;
+  const int khalf = lane / 32;  // which k of the pair this lane supplies
+  const int l32 = lane % 32;
+  const int a_col = wm * C::TM * 32 + l32;
+  const int b_col = wn * C::TN * 32 + l32;
+
+  if (KT > 0) {
+    load_a(0);
+    load_b(0);
+    store_a(0);
+    store_b(0);
+    __syncthreads();
+  }
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < KT;
+    if (more) {
+      load_a((kt + 1) * BK);
+      load_b((kt + 1) * BK);
+    }
+    const float *Sa = As + cur * C::kAStage + khalf * C::LA + a_col;
+    const float *Sb = Bs + cur * C::kBStage + khalf * C::LB + b_col;
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 2) {
+      float a[C::TM], b[C::TN];
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i) a[i] = Sa[kk * C::LA + i * 32];
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j) b[j] = Sb[kk * C::LB + j * 32];
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) {
+      store_a(cur ^ 1);
+      store_b(cur ^ 1);
+    }
+    __syncthreads();
+  }
+
+  // Epilogue.  Accumulator register r of lane l in block (i, j) is
+  // C[row][col] with col = 32j + l%32 and row = 32i + 8*(r/4) + 4*(l/32) + r%4
+  // (relative to the wave tile).
+  const int epi = p.epi;
+#pragma unroll
+  for (int j = 0; j < C::TN; ++j) {
+    const int col = n0 + wn * C::TN * 32 + j * 32 + l32;
+    if (EDGE && col >= N) continue;
+    float bv = 0.0f;
+    if (epi == SILGPU_EPI_BIAS || epi == SILGPU_EPI_BIAS_SIGMOID || epi == SILGPU_EPI_BIAS_RELU)
+      bv = p.bias[col % p.bias_len];
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * C::TM * 32 + i * 32 + 8 * (r / 4) + 4 * khalf + (r % 4);
+        if (EDGE && row >= M) continue;
+        float v = acc[i][j][r] + bv;
+        if (epi == SILGPU_EPI_BIAS_SIGMOID) v = sigmoidf_dev(v);
+        else if (epi == SILGPU_EPI_RELU || epi == SILGPU_EPI_BIAS_RELU) v = fmaxf(v, 0.0f);
+        Cp[int64_t(row) * p.ldc + col] = v;
+      }
+    }
+  }
+}
+
+// ---- GEMV: y[1 x N] = x[1 x K] * B[K x N] -----------------------------------
+//
+// HBM-bound: B (K*N floats) is read once.  Workgroup (ct, ks) covers 256
+// columns (one float4 per lane) and rows [ks*kc, (ks+1)*kc); its four
+// wavefronts take interleaved rows, eight loads in flight per lane.  The
+// split over K gives enough workgroups to fill the GPU; the last workgroup
+// of each column tile adds the K-split partials in a fixed order.
+constexpr int kGemvBlock = 256;
+constexpr int kGemvCols = 256;  // columns per workgroup (64 lanes x float4)
+
+template <bool VEC>
+__global__ __launch_bounds__(kGemvBlock) void gemv_n_k(const float *__restrict__ x,
+                                                       const float *__restrict__ Bm,
+                                                       int64_t ldb, float *__restrict__ y,
+                                                       int64_t N, int64_t K, int64_t kc,
+                                                       float *__restrict__ partial,
+                                                       unsigned int *counters) {
+  __shared__ float4 red[kGemvBlock / kWave][kWave];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int64_t c0 = int64_t(blockIdx.x) * kGemvCols;
+  const int64_t k0 = int64_t(blockIdx.y) * kc;
+  const int64_t k1 = k0 + kc < K ? k0 + kc : K;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if constexpr (VEC) {
+    const int64_t col = c0 + lane * 4;
+    if (col < N) {
+      const float *bp = Bm + col;
+      int64_t k = k0 + wave;
+      constexpr int U = 8;
+      for (; k + (U - 1) * 4 < k1; k += U * 4) {
+        float4 v[U];
+        float xv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          v[u] = *reinterpret_cast<const float4 *>(bp + (k + u * 4) * ldb);
+          xv[u] = x[k + u * 4];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          acc.x += xv[u] * v[u].x;
+          acc.y += xv[u] * v[u].y;
+          acc.z += xv[u] * v[u].z;
+          acc.w += xv[u] * v[u].w;
+        }
+      }
+      for (; k < k1; k += 4) {
+        float4 v = *reinterpret_cast<const float4 *>(bp + k * ldb);
+        float xv = x[k];
+        acc.x += xv * v.x;
+        acc.y += xv * v.y;
+        acc.z += xv * v.z;
+        acc.w += xv * v.w;
+      }
+    }
+  } else {
+    // Lane handles columns c0 + lane + 64*q, q < 4.
+    for (int64_t k = k0 + wave; k < k1; k += 4) {
+      const float xv = x[k];
+      const float *row = Bm + k * ldb;
+      int64_t c = c0 + lane;
+      if (c < N) acc.x += xv * row[c];
+      if (c + 64 < N) acc.y += xv * row[c + 64];
+      if (c + 128 < N) acc.z += xv * row[c + 128];
+      if (c + 192 < N) acc.w += xv * row[c + 192];
+    }
+  }
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  float4 s = red[0][lane];
+#pragma unroll
+  for (int w = 1; w < kGemvBlock / kWave; ++w) {
+    float4 o = red[w][lane];
+    s.x += o.x;
+    s.y += o.y;
+    s.z += o.z;
+    s.w += o.w;
+  }
+  auto col_of = [&](int q) -> int64_t {
+    return VEC ? c0 + lane * 4 + q : c0 + lane + 64 * q;
+  };
+  if (gridDim.y == 1) {
+    float sv[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (col_of(q) < N) y[col_of(q)] = sv[q];
+    return;
+  }
+  // Partial for this K split: partial[ks][ct*256 + lane*4 + q]
+  float4 *pp = reinterpret_cast<float4 *>(partial) +
+               (int64_t(blockIdx.y) * gridDim.x + blockIdx.x) * kWave + lane;
+  *pp = s;
+  __threadfence();  // publish the partial before counting this arrival
+  // Only wavefront 0 is still running: lane 0 counts, the result is
+  // broadcast through a register.
+  unsigned prev = 0;
+  if (lane == 0) prev = atomicAdd(counters + blockIdx.x, 1u);
+  prev = __shfl(prev, 0, kWave);
+  if (prev != gridDim.y - 1) return;
+  if (lane == 0) atomicExch(counters + blockIdx.x, 0u);
+  __threadfence();  // see every other workgroup's partial
+  float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (unsigned ks = 0; ks < gridDim.y; ++ks) {
+    float4 o = reinterpret_cast<const float4 *>(partial)[(int64_t(ks) * gridDim.x + blockIdx.x) *
+                                                           kWave + lane];
+    f.x += o.x;
+    f.y += o.y;
+    f.z += o.z;
+    f.w += o.w;
+  }
+  float fv[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    if (col_of(q) < N) y[col_of(q)] = fv[q];
+}
+
+// y[n] = sum_k x[k] * R[n*ldr + k]: one wavefront per output (rows of R
+// contiguous).  Used for x * B^T (trans_b) and for A * v (N == 1).
+template <bool VEC>
+__global__ __launch_bounds__(256) void gemv_t_k(const float *__restrict__ x,
+                                                int64_t incx,
+                                                const float *__restrict__ R, int64_t ldr,
+                                                float *__restrict__ y, int64_t incy,
+                                                int64_t nrows, int64_t K) {
+  const int64_t n = int64_t(blockIdx.x) * 4 + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  if (n >= nrows) return;
+  const float *row = R + n * ldr;
+  float acc = 0.0f;
+  if (VEC && incx == 1) {
+    const float4 *r4 = reinterpret_cast<const float4 *>(row);
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    for (int64_t k = lane; k < K / 4; k += kWave) {
+      float4 a = r4[k], b = x4[k];
+      acc += a.x * b.x;
+      acc += a.y * b.y;
+      acc += a.z * b.z;
+      acc += a.w * b.w;
+    }
+  } else {
+    for (int64_t k = lane; k < K; k += kWave) acc += row[k] * x[k * incx];
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) y[n * incy] = acc;
+}
+
+// Applies an epilogue to a [M x N] block of C in place (GEMV paths).
+__global__ __launch_bounds__(256) void epilogue_k(float *__restrict__ C, int64_t ldc,
+                                                  int64_t M, int64_t N,
+                                                  const float *__restrict__ bias,
+                                                  int64_t bias_len, int epi) {
+  const int64_t total = M * N;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total;
+       i += int64_t(gridDim.x) * 256) {
+    const int64_t m = i / N, n = i % N;
+    float v = C[m * ldc + n];
+    if (epi == SILGPU_EPI_BIAS || epi == SILGPU_EPI_BIAS_SIGMOID || epi == SILGPU_EPI_BIAS_RELU)
+      v += bias[n % bias_len];
+    if (epi == SILGPU_EPI_BIAS_SIGMOID) v = sigmoidf_dev(v);
+    else if (epi == SILGPU_EPI_RELU || epi == SILGPU_EPI_BIAS_RELU) v = fmaxf(v, 0.0f);
+    C[m * ldc + n] = v;
+  }
+}
+
+// ---- host dispatch ----------------------------------------------------------
+
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VEC, bool EDGE>
+int launch_cfg(const gemm_args &a, int64_t batch, hipStream_t s) {
+  using C = cfg<BM, BN, BK, WM, WN>;
+  auto kern = sgemm_mfma_k<BM, BN, BK, WM, WN, TA, TB, VEC, EDGE>;
+  static bool attr_done = false;
+  if (!attr_done) {
+    SILGPU_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         C::kLdsBytes));
+    attr_done = true;
+  }
+  gemm_args g = a;
+  g.tiles_m = static_cast<int>(cdiv(a.M, BM));
+  g.tiles_n = static_cast<int>(cdiv(a.N, BN));
+  dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), 1, static_cast<unsigned>(batch));
+  kern<<<grid, C::kThreads, C::kLdsBytes, s>>>(g);
+  SILGPU_LAUNCH_CHECK("sgemm_mfma_k");
+  return SILGPU_OK;
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
+int launch_tb(const gemm_args &a, int64_t batch, bool vec, hipStream_t s) {
+  const bool edge = (a.M % BM) || (a.N % BN) || (a.K % BK);
+  if (vec) {
+    return edge ? launch_cfg<BM, BN, BK, WM, WN, TA, TB, true, true>(a, batch, s)
+                : launch_cfg<BM, BN, BK, WM, WN, TA, TB, true, false>(a, batch, s);
+  }
+  return launch_cfg<BM, BN, BK, WM, WN, TA, TB, false, true>(a, batch, s);
+}
+
+template <int BM, int BN, int BK, int WM, int WN>
+int launch_tiles(const gemm_args &a, int64_t batch, bool ta, bool tb, bool vec,
+                 hipStream_t s) {
+  if (!ta && !tb) return launch_tb<BM, BN, BK, WM, WN, false, false>(a, batch, vec, s);
+  if (!ta && tb) return launch_tb<BM, BN, BK, WM, WN, false, true>(a, batch, vec, s);
+  if (ta && !tb) return launch_tb<BM, BN, BK, WM, WN, true, false>(a, batch, vec, s);
+  return launch_tb<BM, BN, BK, WM, WN, true, true>(a, batch, vec, s);
+}
+
+int launch_gemv_n(const float *x, const float *Bm, int64_t ldb, float *y, int64_t N,
+                  int64_t K, context *c) {
+  const bool vec = N % 4 == 0 && ldb % 4 == 0 && aligned16(Bm);
+  const int64_t ct = cdiv(N, kGemvCols);
+  // K splits: aim for ~1024 workgroups, >= 32 rows per split, kc % 4 == 0.
+  int64_t ks = 1024 / ct;
+  if (ks < 1) ks = 1;
+  int64_t max_ks = K / 32;
+  if (ks > max_ks) ks = max_ks;
+  if (ks < 1) ks = 1;
+  if (ks > 65535) ks = 65535;
+  while (ks > 1 && ks * ct * kGemvCols * int64_t(sizeof(float)) > int64_t(kPartialBytes)) ks /= 2;
+  if (ct > kCounterCount) ks = 1;
+  int64_t kc = cdiv(cdiv(K, ks), 4) * 4;
+  ks = cdiv(K, kc);
+  dim3 grid(static_cast<unsigned>(ct), static_cast<unsigned>(ks));
+  if (vec)
+    gemv_n_k<true><<<grid, kGemvBlock, 0, c->stream>>>(
+        x, Bm, ldb, y, N, K, kc, static_cast<float *>(c->partials), c->counters);
+  else
+    gemv_n_k<false><<<grid, kGemvBlock, 0, c->stream>>>(
+        x, Bm, ldb, y, N, K, kc, static_cast<float *>(c->partials), c->counters);
+  SILGPU_LAUNCH_CHECK("gemv_n_k");
+  return SILGPU_OK;
+}
+
+int launch_gemv_t(const float *x, int64_t incx, const float *R, int64_t ldr, float *y,
+                  int64_t incy, int64_t nrows, int64_t K, context *c) {
+  const bool vec = K % 4 == 0 && ldr % 4 == 0 && aligned16(R) && aligned16(x);
+  unsigned grid = static_cast<unsigned>(cdiv(nrows, 4));
+  if (vec)
+    gemv_t_k<true><<<grid, 256, 0, c->stream>>>(x, incx, R, ldr, y, incy, nrows, K);
+  else
+    gemv_t_k<false><<<grid, 256, 0, c->stream>>>(x, incx, R, ldr, y, incy, nrows, K);
+  SILGPU_LAUNCH_CHECK("gemv_t_k");
+  return SILGPU_OK;
+}
+
+int apply_epilogue(float *C, int64_t ldc, int64_t M, int64_t N, const float *bias,
+                   int64_t bias_len, int epi, context *c) {
+  if (epi == SILGPU_EPI_NONE) return SILGPU_OK;
+  int64_t g = cdiv(M * N, 256);
+  if (g > 4096) g = 4096;
+  epilogue_k<<<static_cast<unsigned>(g), 256, 0, c->stream>>>(C, ldc, M, N, bias, bias_len,
+                                                                epi);
+  SILGPU_LAUNCH_CHECK("epilogue_k");
+  return SILGPU_OK;
+}
+
+}  // namespace
+}  // namespace silgpu
+
+using namespace silgpu;
+
+extern "C" {
+
+int silgpu_sgemv(const float *d_x, const float *d_B, int64_t ldb, float *d_y, int64_t N,
+                 int64_t K) {
+  SILGPU_REQUIRE(N >= 0 && K >= 0, "silgpu_sgemv: negative extent");
+  if (N == 0) return SILGPU_OK;
+  SILGPU_REQUIRE(ldb >= N, "silgpu_sgemv: ldb %lld < N %lld", (long long)ldb, (long long)N);
+  SILGPU_REQUIRE(d_y != nullptr, "silgpu_sgemv: null y");
+  SILGPU_CTX(c);
+  if (K == 0) return silgpu_fill_u32(d_y, 0u, N);
+  SILGPU_REQUIRE(d_x && d_B, "silgpu_sgemv: null pointer");
+  return launch_gemv_n(d_x, d_B, ldb, d_y, N, K, c);
+}
+
+int silgpu_sgemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const float *d_A,
+                 int64_t lda, int64_t stride_a, const float *d_B, int64_t ldb,
+                 int64_t stride_b, float *d_C, int64_t ldc, int64_t stride_c, int64_t batch,
+                 const float *d_bias, int64_t bias_len, int epilogue) {
+  SILGPU_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "silgpu_sgemm: negative extent");
+  SILGPU_REQUIRE(M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX,
+                 "silgpu_sgemm: extent exceeds int32");
+  SILGPU_REQUIRE(epilogue >= SILGPU_EPI_NONE && epilogue <= SILGPU_EPI_BIAS_RELU,
+                 "silgpu_sgemm: unknown epilogue %d", epilogue);
+  if (M == 0 || N == 0 || batch == 0) return SILGPU_OK;
+  const bool ta = trans_a != 0, tb = trans_b != 0;
+  SILGPU_REQUIRE(lda >= (ta ? M : K) && lda >= 1, "silgpu_sgemm: lda %lld too small",
+                 (long long)lda);
+  SILGPU_REQUIRE(ldb >= (tb ? K : N) && ldb >= 1, "silgpu_sgemm: ldb %lld too small",
+                 (long long)ldb);
+  SILGPU_REQUIRE(ldc >= N, "silgpu_sgemm: ldc %lld < N %lld", (long long)ldc, (long long)N);
+  SILGPU_REQUIRE(batch <= 65535, "silgpu_sgemm: batch %lld exceeds the grid", (long long)batch);
+  const bool uses_bias = epilogue == SILGPU_EPI_BIAS || epilogue == SILGPU_EPI_BIAS_SIGMOID ||
+                         epilogue == SILGPU_EPI_BIAS_RELU;
+  SILGPU_REQUIRE(!uses_bias || (d_bias && bias_len > 0),
+                 "silgpu_sgemm: bias epilogue without bias");
+  SILGPU_REQUIRE(d_C != nullptr && (K == 0 || (d_A && d_B)), "silgpu_sgemm: null pointer");
+  SILGPU_CTX(c);
+
+  // Vector products (the reference routes M == 1 to sgemv, include/array.h:2675-2676).
+  if (batch == 1 && K > 0 && (M == 1 || N == 1)) {
+    int rc;
+    if (M == 1 && !tb && !ta) {
+      // y = x * B with x = A[0..K) contiguous and B [K][N].
+      rc = launch_gemv_n(d_A, d_B, ldb, d_C, N, K, c);
+      if (rc != SILGPU_OK) return rc;
+      return apply_epilogue(d_C, ldc, 1, N, d_bias, bias_len, epilogue, c);
+    } else if (M == 1 && tb) {
+      // y[n] = sum_k x[k] * B[n*ldb + k]
+      rc = launch_gemv_t(d_A, ta ? lda : 1, d_B, ldb, d_C, 1, N, K, c);
+      if (rc != SILGPU_OK) return rc;
+      return apply_epilogue(d_C, ldc, 1, N, d_bias, bias_len, epilogue, c);
+    } else if (N == 1 && !ta) {
+      // y[m] = sum_k A[m*lda + k] * b[k], b[k] = B[k*ldb] (non-trans) or B[k] (trans)
+      rc = launch_gemv_t(d_B, tb ? 1 : ldb, d_A, lda, d_C, ldc, M, K, c);
+      if (rc != SILGPU_OK) return rc;
+      return apply_epilogue(d_C, ldc, M, 1, d_bias, bias_len, epilogue, c);
+    }
+  }
+
+  gemm_args a{};
+  a.A = d_A;
+  a.B = d_B;
+  a.C = d_C;
+  a.bias = d_bias;
+  a.lda = lda;
+  a.ldb = ldb;
+  a.ldc = ldc;
+  a.sA = stride_a;
+  a.sB = stride_b;
+  a.sC = stride_c;
+  a.bias_len = bias_len > 0 ? bias_len : 1;
+  a.M = static_cast<int>(M);
+  a.N = static_cast<int>(N);
+  a.K = static_cast<int>(K);
+  a.epi = epilogue;
+  const bool vec = aligned16(d_A) && aligned16(d_B) && lda % 4 == 0 && ldb % 4 == 0 &&
+                   (ta ? M % 4 == 0 : K % 4 == 0) && (tb ? K % 4 == 0 : N % 4 == 0) &&
+                   (batch == 1 || (stride_a % 4 == 0 && stride_b % 4 == 0));
+  const int64_t tiles128 = cdiv(M, 128) * cdiv(N, 128) * batch;
+  if (tiles128 >= 1024)
+    return launch_tiles<128, 128, 16, 2, 2>(a, batch, ta, tb, vec, c->stream);
+  return launch_tiles<64, 64, 16, 2, 2>(a, batch, ta, tb, vec, c->stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,103 @@
+// Internal declarations shared by the HIP translation units of libsilgpu.
+// Device code here targets gfx950 (CDNA4) only: 64-lane wavefronts, fp32
+// MFMA, 160 KiB LDS per CU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/silgpu.h"
+
+namespace silgpu {
+
+// ---- error plumbing --------------------------------------------------------
+
+// Records a message for silgpu_last_error() and returns `code`.
+int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+// Library context: device, the single stream, scratch for multi-block
+// reductions.
+struct context {
+  int device = -1;
+  hipStream_t stream = nullptr;
+  int cu_count = 0;
+  int clock_khz = 0;
+  // Scratch: per-workgroup partial results (floats / doubles / (val, idx)
+  // pairs) and completion counters.  Counters are left at zero by every
+  // kernel that uses them (the last workgroup resets its counter), so no
+  // clearing launch is needed between calls on the stream.
+  void *partials = nullptr;      // kPartialBytes
+  unsigned int *counters = nullptr;  // kCounterCount
+};
+
+constexpr size_t kPartialBytes = size_t(16) << 20;  // 16 MiB
+constexpr int kCounterCount = 65536;
+
+// Returns the initialised context, or nullptr after recording an error.
+context *ctx();
+
+// Checks a HIP call; on failure records the error and returns SILGPU_ERR_HIP.
+#define SILGPU_HIP_CHECK(call)                                                       \
+  do {                                                                               \
+    hipError_t e_ = (call);                                                          \
+    if (e_ != hipSuccess)                                                            \
+      return ::silgpu::set_error(SILGPU_ERR_HIP, "%s failed: %s (%s:%d)", #call,     \
+                                 hipGetErrorString(e_), __FILE__, __LINE__);         \
+  } while (0)
+
+// Checks the launch just issued.
+#define SILGPU_LAUNCH_CHECK(name)                                                    \
+  do {                                                                               \
+    hipError_t e_ = hipGetLastError();                                               \
+    if (e_ != hipSuccess)                                                            \
+      return ::silgpu::set_error(SILGPU_ERR_HIP, "launch of %s failed: %s", name,    \
+                                 hipGetErrorString(e_));                             \
+  } while (0)
+
+#define SILGPU_REQUIRE(cond, ...)                                                    \
+  do {                                                                               \
+    if (!(cond)) return ::silgpu::set_error(SILGPU_ERR_INVALID, __VA_ARGS__);        \
+  } while (0)
+
+#define SILGPU_CTX(c)                                                                \
+  ::silgpu::context *c = ::silgpu::ctx();                                            \
+  if (!c) return SILGPU_ERR_NODEVICE
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---- device helpers ---------------------------------------------------------
+
+constexpr int kWave = 64;
+
+// Butterfly reductions across the 64 lanes of a wavefront.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+__device__ __forceinline__ float sigmoidf_dev(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+}  // namespace silgpu

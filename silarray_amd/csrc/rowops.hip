@@ -1,0 +1,329 @@
+// Row softmax and row layer_norm over a contiguous [rows, cols] array.
+//
+// Both are HBM-bound: the optimum is one read and one write of the array
+// (8 bytes per element).  A row of up to 16384 floats is held in registers
+// by one workgroup (256 threads x up to 16 float4) or, for rows up to 2048,
+// by one wavefront, so the row is read from HBM exactly once and every
+// reduction (max, sum, mean, variance) runs over registers with wave64
+// butterflies and one LDS exchange.  Longer rows take a looped variant that
+// reads the row twice.
+//
+// Numerics: softmax subtracts the row maximum and divides by an fp64-
+// accumulated sum; layer_norm uses the two-pass form of cpu::layer_norm
+// (include/cpu.h:352-373): mean, then sum of squared deviations, then
+// 1/sqrtf(ss/cols + eps), then *gamma + beta.
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cmath>
+
+#include "internal.h"
+
+namespace silgpu {
+namespace {
+
+// Reductions over a group of NT threads that own one row.  NT == 64: one
+// wavefront; NT > 64: the whole workgroup (NT threads) through LDS.
+template <int NT>
+struct group {
+  static constexpr int kWaves = NT / kWave;
+
+  template <typename T, typename F>
+  __device__ static T reduce(T v, F op) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = op(v, __shfl_xor(v, o, kWave));
+    if constexpr (NT == kWave) {
+      return v;
+    } else {
+      __shared__ T red[kWaves];
+      const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+      __syncthreads();
+      if (lane == 0) red[wave] = v;
+      __syncthreads();
+      T r = red[0];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) r = op(r, red[w]);
+      return r;
+    }
+  }
+};
+
+struct fmax_op {
+  __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+struct dsum_op {
+  __device__ double operator()(double a, double b) const { return a + b; }
+};
+
+// Loads V float4 (VEC) or 4V scalars (!VEC) of row `row` owned by thread
+// `t` of an NT-thread group: element j of slot k is column
+// (k*NT + t)*4 + j.  Columns >= cols read as `pad`.
+template <int NT, int V, bool VEC>
+__device__ __forceinline__ void load_row(const float *__restrict__ row, int64_t cols, int t,
+                                         float pad, float (&x)[V][4]) {
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    int64_t c = (int64_t(k) * NT + t) * 4;
+    if constexpr (VEC) {
+      if (c < cols) {
+        float4 v = reinterpret_cast<const float4 *>(row)[c / 4];
+        x[k][0] = v.x;
+        x[k][1] = v.y;
+        x[k][2] = v.z;
+        x[k][3] = v.w;
+      } else {
+        x[k][0] = x[k][1] = x[k][2] = x[k][3] = pad;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[k][j] = (c + j < cols) ? row[c + j] : pad;
+    }
+  }
+}
+
+template <int NT, int V, bool VEC>
+__device__ __forceinline__ void store_row(float *__restrict__ row, int64_t cols, int t,
+                                          const float (&y)[V][4]) {
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    int64_t c = (int64_t(k) * NT + t) * 4;
+    if constexpr (VEC) {
+      if (c < cols)
+        reinterpret_cast<float4 *>(row)[c / 4] = make_float4(y[k][0], y[k][1], y[k][2], y[k][3]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (c + j < cols) row[c + j] = y[k][j];
+    }
+  }
+}
+
+// Launch shape: NT threads per row, RPB rows per workgroup (NT * RPB <= 256).
+template <int NT, int V, bool VEC>
+__global__ __launch_bounds__(256) void softmax_reg_k(const float *__restrict__ in,
+                                                     float *__restrict__ out, int64_t rows,
+                                                     int64_t cols) {
+  constexpr int RPB = 256 / NT;
+  const int64_t r = int64_t(blockIdx.x) * RPB + threadIdx.x / NT;
+  const int t = threadIdx.x % NT;
+  if (NT == kWave && r >= rows) return;  // whole wavefronts exit together
+  const float *src = in + r * cols;
+  float x[V][4];
+  load_row<NT, V, VEC>(src, cols, t, -INFINITY, x);
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < V; ++k)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m = fmaxf(m, x[k][j]);
+  m = group<NT>::reduce(m, fmax_op{});
+  double s = 0.0;
+#pragma unroll
+  for (int k = 0; k < V; ++k)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float e = expf(x[k][j] - m);  // padding: exp(-inf) = 0
+      x[k][j] = e;
+      s += static_cast<double>(e);
+    }
+  s = group<NT>::reduce(s, dsum_op{});
+  const float sf = static_cast<float>(s);
+#pragma unroll
+  for (int k = 0; k < V; ++k)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[k][j] = x[k][j] / sf;
+  store_row<NT, V, VEC>(out + r * cols, cols, t, x);
+}
+
+template <int NT, int V, bool VEC>
+__global__ __launch_bounds__(256) void layer_norm_reg_k(const float *__restrict__ in,
+                                                        float *__restrict__ out,
+                                                        const float *__restrict__ gamma,
+                                                        const float *__restrict__ beta,
+                                                        int64_t rows, int64_t cols,
+                                                        float eps) {
+  constexpr int RPB = 256 / NT;
+  const int64_t r = int64_t(blockIdx.x) * RPB + threadIdx.x / NT;
+  const int t = threadIdx.x % NT;
+  if (NT == kWave && r >= rows) return;
+  float x[V][4];
+  load_row<NT, V, VEC>(in + r * cols, cols, t, 0.0f, x);
+  double s = 0.0;
+#pragma unroll
+  for (int k = 0; k < V; ++k)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s += static_cast<double>(x[k][j]);
+  s = group<NT>::reduce(s, dsum_op{});
+  const float mu = static_cast<float>(s / static_cast<double>(cols));
+  double ss = 0.0;
+#pragma unroll
+  for (int k = 0; k < V; ++k)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int64_t c = (int64_t(k) * NT + t) * 4 + j;
+      float d = x[k][j] - mu;
+      x[k][j] = d;
+      if (c < cols) ss += static_cast<double>(d) * static_cast<double>(d);
+    }
+  ss = group<NT>::reduce(ss, dsum_op{});
+  const float var = static_cast<float>(ss / static_cast<double>(cols));
+  const float inv_std = 1.0f / sqrtf(var + eps);
+  float g[V][4], b[V][4];
+  load_row<NT, V, VEC>(gamma, cols, t, 0.0f, g);
+  load_row<NT, V, VEC>(beta, cols, t, 0.0f, b);
+#pragma unroll
+  for (int k = 0; k < V; ++k)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[k][j] = (x[k][j] * inv_std) * g[k][j] + b[k][j];
+  store_row<NT, V, VEC>(out + r * cols, cols, t, x);
+}
+
+// Rows longer than the register path: one workgroup per row, two reads.
+constexpr int kLoopBlock = 256;
+
+__global__ __launch_bounds__(kLoopBlock) void softmax_loop_k(const float *__restrict__ in,
+                                                             float *__restrict__ out,
+                                                             int64_t cols) {
+  const float *src = in + int64_t(blockIdx.x) * cols;
+  float *dst = out + int64_t(blockIdx.x) * cols;
+  // Online (max, sum) per thread, rescaling the sum when the max grows.
+  float m = -INFINITY;
+  double s = 0.0;
+  for (int64_t c = threadIdx.x; c < cols; c += kLoopBlock) {
+    float v = src[c];
+    if (v > m) {
+      s = s * static_cast<double>(expf(m - v)) + 1.0;
+      m = v;
+    } else {
+      s += static_cast<double>(expf(v - m));
+    }
+  }
+  const float gm = group<kLoopBlock>::reduce(m, fmax_op{});
+  double part = (m == -INFINITY) ? 0.0 : s * static_cast<double>(expf(m - gm));
+  const float sf = static_cast<float>(group<kLoopBlock>::reduce(part, dsum_op{}));
+  for (int64_t c = threadIdx.x; c < cols; c += kLoopBlock) dst[c] = expf(src[c] - gm) / sf;
+}
+
+__global__ __launch_bounds__(kLoopBlock) void layer_norm_loop_k(
+    const float *__restrict__ in, float *__restrict__ out, const float *__restrict__ gamma,
+    const float *__restrict__ beta, int64_t cols, float eps) {
+  const float *src = in + int64_t(blockIdx.x) * cols;
+  float *dst = out + int64_t(blockIdx.x) * cols;
+  double s = 0.0;
+  for (int64_t c = threadIdx.x; c < cols; c += kLoopBlock) s += static_cast<double>(src[c]);
+  s = group<kLoopBlock>::reduce(s, dsum_op{});
+  const float mu = static_cast<float>(s / static_cast<double>(cols));
+  double ss = 0.0;
+  for (int64_t c = threadIdx.x; c < cols; c += kLoopBlock) {
+    float d = src[c] - mu;
+    ss += static_cast<double>(d) * static_cast<double>(d);
+  }
+  ss = group<kLoopBlock>::reduce(ss, dsum_op{});
+  const float inv_std = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(cols)) + eps);
+  for (int64_t c = threadIdx.x; c < cols; c += kLoopBlock)
+    dst[c] = ((src[c] - mu) * inv_std) * gamma[c] + beta[c];
+}
+
+// ---- dispatch ---------------------------------------------------------------
+
+struct row_launch {
+  int nt;      // threads per row
+  int v;       // float4 slots per thread
+};
+
+// Smallest register configuration that covers `cols`, or {0,0} for the
+// looped kernels.
+row_launch pick(int64_t cols) {
+  if (cols <= 256) return {64, 1};
+  if (cols <= 512) return {64, 2};
+  if (cols <= 1024) return {64, 4};
+  if (cols <= 2048) return {64, 8};
+  if (cols <= 4096) return {256, 4};
+  if (cols <= 8192) return {256, 8};
+  if (cols <= 16384) return {256, 16};
+  return {0, 0};
+}
+
+template <int NT, int V, bool VEC>
+void go_softmax(const float *in, float *out, int64_t rows, int64_t cols, hipStream_t s) {
+  constexpr int RPB = 256 / NT;
+  softmax_reg_k<NT, V, VEC><<<static_cast<unsigned>(cdiv(rows, RPB)), 256, 0, s>>>(in, out,
+                                                                                  rows, cols);
+}
+
+template <int NT, int V, bool VEC>
+void go_ln(const float *in, float *out, const float *g, const float *b, int64_t rows,
+           int64_t cols, float eps, hipStream_t s) {
+  constexpr int RPB = 256 / NT;
+  layer_norm_reg_k<NT, V, VEC><<<static_cast<unsigned>(cdiv(rows, RPB)), 256, 0, s>>>(
+      in, out, g, b, rows, cols, eps);
+}
+
+#define SILGPU_ROW_DISPATCH(FN, VEC, ...)                                               \
+  switch (L.nt * 100 + L.v) {                                                           \
+    case 6401: FN<64, 1, VEC>(__VA_ARGS__); break;                                      \
+    case 6402: FN<64, 2, VEC>(__VA_ARGS__); break;                                      \
+    case 6404: FN<64, 4, VEC>(__VA_ARGS__); break;                                      \
+    case 6408: FN<64, 8, VEC>(__VA_ARGS__); break;                                      \
+    case 25604: FN<256, 4, VEC>(__VA_ARGS__); break;                                    \
+    case 25608: FN<256, 8, VEC>(__VA_ARGS__); break;                                    \
+    default: FN<256, 16, VEC>(__VA_ARGS__); break;                                      \
+  }
+
+}  // namespace
+}  // namespace silgpu
+
+using namespace silgpu;
+
+extern "C" {
+
+int silgpu_softmax_rows_f32(const float *d_in, float *d_out, int64_t rows, int64_t cols) {
+  SILGPU_REQUIRE(rows >= 0 && cols >= 0, "silgpu_softmax_rows_f32: negative extent");
+  if (rows == 0 || cols == 0) return SILGPU_OK;
+  SILGPU_REQUIRE(d_in && d_out, "silgpu_softmax_rows_f32: null pointer");
+  SILGPU_REQUIRE(rows <= (int64_t(1) << 31) - 1, "silgpu_softmax_rows_f32: too many rows");
+  SILGPU_CTX(c);
+  row_launch L = pick(cols);
+  if (L.nt == 0) {
+    softmax_loop_k<<<static_cast<unsigned>(rows), kLoopBlock, 0, c->stream>>>(d_in, d_out,
+                                                                              cols);
+    SILGPU_LAUNCH_CHECK("softmax_loop_k");
+    return SILGPU_OK;
+  }
+  bool vec = cols % 4 == 0 && aligned16(d_in) && aligned16(d_out);
+  if (vec) {
+    SILGPU_ROW_DISPATCH(go_softmax, true, d_in, d_out, rows, cols, c->stream);
+  } else {
+    SILGPU_ROW_DISPATCH(go_softmax, false, d_in, d_out, rows, cols, c->stream);
+  }
+  SILGPU_LAUNCH_CHECK("softmax_reg_k");
+  return SILGPU_OK;
+}
+
+int silgpu_layer_norm_rows_f32(const float *d_in, float *d_out, const float *d_gamma,
+                               const float *d_beta, int64_t rows, int64_t cols, float eps) {
+  SILGPU_REQUIRE(rows >= 0 && cols >= 0, "silgpu_layer_norm_rows_f32: negative extent");
+  if (rows == 0 || cols == 0) return SILGPU_OK;
+  SILGPU_REQUIRE(d_in && d_out && d_gamma && d_beta,
+                 "silgpu_layer_norm_rows_f32: null pointer");
+  SILGPU_CTX(c);
+  row_launch L = pick(cols);
+  if (L.nt == 0) {
+    layer_norm_loop_k<<<static_cast<unsigned>(rows), kLoopBlock, 0, c->stream>>>(
+        d_in, d_out, d_gamma, d_beta, cols, eps);
+    SILGPU_LAUNCH_CHECK("layer_norm_loop_k");
+    return SILGPU_OK;
+  }
+  bool vec = cols % 4 == 0 && aligned16(d_in) && aligned16(d_out) && aligned16(d_gamma) &&
+             aligned16(d_beta);
+  if (vec) {
+    SILGPU_ROW_DISPATCH(go_ln, true, d_in, d_out, d_gamma, d_beta, rows, cols, eps,
+                        c->stream);
+  } else {
+    SILGPU_ROW_DISPATCH(go_ln, false, d_in, d_out, d_gamma, d_beta, rows, cols, eps,
+                        c->stream);
+  }
+  SILGPU_LAUNCH_CHECK("layer_norm_reg_k");
+  return SILGPU_OK;
+}
+
+}  // extern "C"

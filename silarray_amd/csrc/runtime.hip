@@ -1,0 +1,295 @@
+// Context, error reporting, pooled device memory, copies and events.
+//
+// Stands in for the reference's gpu_context (include/gpu.h:49-260: one Metal
+// queue, one lazily created command buffer, blocking flush) and its
+// unified-memory buffer_pool (include/unified_memory.h:29-62).  On MI355X the
+// equivalents are one HIP stream (issue order = execution order, like the
+// single command buffer), hipStreamSynchronize for flush, and a size-class
+// pool of hipMalloc'd HBM blocks.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "internal.h"
+
+namespace silgpu {
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+std::mutex g_init_mu;
+context g_ctx;
+bool g_ready = false;
+
+int init_locked() {
+  if (g_ready) return SILGPU_OK;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= 0)
+    return set_error(SILGPU_ERR_NODEVICE, "no HIP device visible (%s)",
+                     e == hipSuccess ? "count 0" : hipGetErrorString(e));
+  SILGPU_HIP_CHECK(hipSetDevice(0));
+  hipDeviceProp_t prop;
+  SILGPU_HIP_CHECK(hipGetDeviceProperties(&prop, 0));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return set_error(SILGPU_ERR_UNSUPPORTED,
+                     "device 0 is %s; this library is built for gfx950 only",
+                     prop.gcnArchName);
+  g_ctx.device = 0;
+  g_ctx.cu_count = prop.multiProcessorCount;
+  g_ctx.clock_khz = prop.clockRate;
+  // Default priority on purpose: streams of mixed priority are avoided.
+  SILGPU_HIP_CHECK(hipStreamCreateWithFlags(&g_ctx.stream, hipStreamNonBlocking));
+  SILGPU_HIP_CHECK(hipMalloc(&g_ctx.partials, kPartialBytes));
+  SILGPU_HIP_CHECK(hipMalloc(reinterpret_cast<void **>(&g_ctx.counters),
+                             sizeof(unsigned int) * kCounterCount));
+  SILGPU_HIP_CHECK(hipMemset(g_ctx.counters, 0, sizeof(unsigned int) * kCounterCount));
+  SILGPU_HIP_CHECK(hipDeviceSynchronize());
+  g_ready = true;
+  return SILGPU_OK;
+}
+
+// ---- size-class pool --------------------------------------------------------
+
+// Size classes: multiples of 256 B up to 64 KiB, then four classes per power
+// of two (waste <= 25%).  The reference keeps exact-byte free lists
+// (include/unified_memory.h:38-51); classes let nearby sizes share blocks.
+size_t size_class(size_t bytes) {
+  if (bytes == 0) bytes = 1;
+  if (bytes <= 65536) return (bytes + 255) & ~size_t(255);
+  size_t p = size_t(1) << (63 - __builtin_clzll(bytes));  // floor pow2
+  size_t step = p / 4;
+  return (bytes + step - 1) / step * step;
+}
+
+struct pool {
+  std::mutex mu;
+  std::unordered_map<size_t, std::vector<void *>> free_lists;
+  std::unordered_map<void *, size_t> live;  // ptr -> class bytes
+  size_t in_use = 0;
+  size_t cached = 0;
+};
+
+pool &the_pool() {
+  static pool *p = new pool();  // never destroyed: blocks outlive static dtors
+  return *p;
+}
+
+}  // namespace
+
+int set_error(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+void clear_error() { g_err[0] = '\0'; }
+
+context *ctx() {
+  if (g_ready) return &g_ctx;
+  std::lock_guard<std::mutex> lk(g_init_mu);
+  if (init_locked() != SILGPU_OK) return nullptr;
+  return &g_ctx;
+}
+
+}  // namespace silgpu
+
+using namespace silgpu;
+
+extern "C" {
+
+const char *silgpu_last_error(void) { return g_err; }
+
+int silgpu_init(void) {
+  std::lock_guard<std::mutex> lk(g_init_mu);
+  return init_locked();
+}
+
+int silgpu_sync(void) {
+  SILGPU_CTX(c);
+  SILGPU_HIP_CHECK(hipStreamSynchronize(c->stream));
+  return SILGPU_OK;
+}
+
+int silgpu_device_info(int *cu_count, int *clock_khz, int *lds_bytes, char *arch,
+                       size_t arch_len) {
+  SILGPU_CTX(c);
+  hipDeviceProp_t prop;
+  SILGPU_HIP_CHECK(hipGetDeviceProperties(&prop, c->device));
+  if (cu_count) *cu_count = prop.multiProcessorCount;
+  if (clock_khz) *clock_khz = prop.clockRate;
+  if (lds_bytes) *lds_bytes = static_cast<int>(prop.sharedMemPerBlock);
+  if (arch && arch_len) {
+    std::strncpy(arch, prop.gcnArchName, arch_len - 1);
+    arch[arch_len - 1] = '\0';
+  }
+  return SILGPU_OK;
+}
+
+int silgpu_alloc(size_t bytes, void **d_ptr) {
+  SILGPU_REQUIRE(d_ptr != nullptr, "silgpu_alloc: d_ptr is null");
+  SILGPU_CTX(c);
+  (void)c;
+  size_t cls = size_class(bytes);
+  pool &p = the_pool();
+  {
+    std::lock_guard<std::mutex> lk(p.mu);
+    auto it = p.free_lists.find(cls);
+    if (it != p.free_lists.end() && !it->second.empty()) {
+      void *ptr = it->second.back();
+      it->second.pop_back();
+      p.live[ptr] = cls;
+      p.in_use += cls;
+      p.cached -= cls;
+      *d_ptr = ptr;
+      return SILGPU_OK;
+    }
+  }
+  void *ptr = nullptr;
+  hipError_t e = hipMalloc(&ptr, cls);
+  if (e != hipSuccess) {
+    // Release cached blocks and retry once before giving up.
+    silgpu_pool_trim();
+    e = hipMalloc(&ptr, cls);
+    if (e != hipSuccess)
+      return set_error(SILGPU_ERR_NOMEM, "hipMalloc(%zu) failed: %s", cls,
+                       hipGetErrorString(e));
+  }
+  std::lock_guard<std::mutex> lk(p.mu);
+  p.live[ptr] = cls;
+  p.in_use += cls;
+  *d_ptr = ptr;
+  return SILGPU_OK;
+}
+
+int silgpu_free(void *d_ptr) {
+  if (!d_ptr) return SILGPU_OK;
+  pool &p = the_pool();
+  std::lock_guard<std::mutex> lk(p.mu);
+  auto it = p.live.find(d_ptr);
+  if (it == p.live.end())
+    return set_error(SILGPU_ERR_INVALID, "silgpu_free: %p was not allocated by silgpu_alloc",
+                     d_ptr);
+  size_t cls = it->second;
+  p.live.erase(it);
+  p.in_use -= cls;
+  p.cached += cls;
+  // Work already issued on the stream may still read this block; any later
+  // user is ordered after it on the same stream, so reuse is safe.
+  p.free_lists[cls].push_back(d_ptr);
+  return SILGPU_OK;
+}
+
+int silgpu_pool_trim(void) {
+  SILGPU_CTX(c);
+  SILGPU_HIP_CHECK(hipStreamSynchronize(c->stream));
+  pool &p = the_pool();
+  std::lock_guard<std::mutex> lk(p.mu);
+  for (auto &kv : p.free_lists) {
+    for (void *ptr : kv.second) (void)hipFree(ptr);
+    kv.second.clear();
+  }
+  p.cached = 0;
+  return SILGPU_OK;
+}
+
+int silgpu_pool_stats(size_t *in_use, size_t *cached) {
+  pool &p = the_pool();
+  std::lock_guard<std::mutex> lk(p.mu);
+  if (in_use) *in_use = p.in_use;
+  if (cached) *cached = p.cached;
+  return SILGPU_OK;
+}
+
+int silgpu_host_alloc(size_t bytes, void **h_ptr) {
+  SILGPU_REQUIRE(h_ptr != nullptr, "silgpu_host_alloc: h_ptr is null");
+  SILGPU_CTX(c);
+  (void)c;
+  hipError_t e = hipHostMalloc(h_ptr, bytes ? bytes : 1, hipHostMallocDefault);
+  if (e != hipSuccess)
+    return set_error(SILGPU_ERR_NOMEM, "hipHostMalloc(%zu) failed: %s", bytes,
+                     hipGetErrorString(e));
+  return SILGPU_OK;
+}
+
+int silgpu_host_free(void *h_ptr) {
+  if (!h_ptr) return SILGPU_OK;
+  SILGPU_HIP_CHECK(hipHostFree(h_ptr));
+  return SILGPU_OK;
+}
+
+int silgpu_memcpy_h2d(void *d_dst, const void *h_src, size_t bytes) {
+  if (bytes == 0) return SILGPU_OK;
+  SILGPU_REQUIRE(d_dst && h_src, "silgpu_memcpy_h2d: null pointer");
+  SILGPU_CTX(c);
+  SILGPU_HIP_CHECK(hipMemcpyAsync(d_dst, h_src, bytes, hipMemcpyHostToDevice, c->stream));
+  // The caller may overwrite h_src as soon as this returns.
+  SILGPU_HIP_CHECK(hipStreamSynchronize(c->stream));
+  return SILGPU_OK;
+}
+
+int silgpu_memcpy_d2h(void *h_dst, const void *d_src, size_t bytes) {
+  if (bytes == 0) return SILGPU_OK;
+  SILGPU_REQUIRE(h_dst && d_src, "silgpu_memcpy_d2h: null pointer");
+  SILGPU_CTX(c);
+  SILGPU_HIP_CHECK(hipMemcpyAsync(h_dst, d_src, bytes, hipMemcpyDeviceToHost, c->stream));
+  SILGPU_HIP_CHECK(hipStreamSynchronize(c->stream));
+  return SILGPU_OK;
+}
+
+int silgpu_memcpy_d2d(void *d_dst, const void *d_src, size_t bytes) {
+  if (bytes == 0) return SILGPU_OK;
+  SILGPU_REQUIRE(d_dst && d_src, "silgpu_memcpy_d2d: null pointer");
+  SILGPU_CTX(c);
+  SILGPU_HIP_CHECK(
+      hipMemcpyAsync(d_dst, d_src, bytes, hipMemcpyDeviceToDevice, c->stream));
+  return SILGPU_OK;
+}
+
+int silgpu_event_create(void **ev) {
+  SILGPU_REQUIRE(ev != nullptr, "silgpu_event_create: ev is null");
+  SILGPU_CTX(c);
+  (void)c;
+  hipEvent_t e;
+  SILGPU_HIP_CHECK(hipEventCreate(&e));
+  *ev = e;
+  return SILGPU_OK;
+}
+
+int silgpu_event_destroy(void *ev) {
+  if (!ev) return SILGPU_OK;
+  SILGPU_HIP_CHECK(hipEventDestroy(static_cast<hipEvent_t>(ev)));
+  return SILGPU_OK;
+}
+
+int silgpu_event_record(void *ev) {
+  SILGPU_REQUIRE(ev != nullptr, "silgpu_event_record: ev is null");
+  SILGPU_CTX(c);
+  SILGPU_HIP_CHECK(hipEventRecord(static_cast<hipEvent_t>(ev), c->stream));
+  return SILGPU_OK;
+}
+
+int silgpu_event_elapsed_ms(void *ev_start, void *ev_end, float *ms) {
+  SILGPU_REQUIRE(ev_start && ev_end && ms, "silgpu_event_elapsed_ms: null argument");
+  SILGPU_HIP_CHECK(hipEventSynchronize(static_cast<hipEvent_t>(ev_end)));
+  SILGPU_HIP_CHECK(hipEventElapsedTime(ms, static_cast<hipEvent_t>(ev_start),
+                                       static_cast<hipEvent_t>(ev_end)));
+  return SILGPU_OK;
+}
+
+int silgpu_get_stream(void **stream) {
+  SILGPU_REQUIRE(stream != nullptr, "silgpu_get_stream: stream is null");
+  SILGPU_CTX(c);
+  *stream = c->stream;
+  return SILGPU_OK;
+}
+
+}  // extern "C"

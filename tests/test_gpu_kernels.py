@@ -1,0 +1,518 @@
+"""GPU parity of every C ABI entry point against the CPU oracle.
+
+Bars (stated per test): bit-exact for integer/index results, min/max,
+add/sub/mul/div, affine and fused affine chains; <= a few float32 ulps for
+functions built on exp/pow (the GPU's and glibc's expf/powf differ by up to
+1-2 ulp); relative 1e-5 for softmax, layer_norm and sums; SGEMM/GEMV
+normwise 1e-5*sqrt(K) plus a per-element bound 1e-5*sqrt(K)*sum|a||b|.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+from conftest import rng
+from gpu_util import announce, down, empty, gemm_tolerance_ok, ulp_diff, up
+
+pytestmark = pytest.mark.gpu
+
+ADD, SUB, MUL, DIV, POW = range(5)
+
+
+# ---- elementwise --------------------------------------------------------------
+
+@pytest.mark.parametrize("op", [ADD, SUB, MUL, DIV])
+@pytest.mark.parametrize("n,a_len,b_len", [(4096, 4096, 4096), (4099, 4099, 4099),
+                                           (4096, 4096, 1), (4096, 1, 4096),
+                                           (4096, 4096, 256), (4096, 512, 4096),
+                                           (1000, 1000, 7), (13, 1, 1)])
+def test_binary_f32_exact(native, oracle, op, n, a_len, b_len):
+    announce(f"binary_f32 op={op} n={n} a_len={a_len} b_len={b_len}")
+    g = rng(100 + op)
+    a = g.uniform(-2, 2, a_len).astype(np.float32)
+    b = g.uniform(0.25, 2, b_len).astype(np.float32) * np.where(g.random(b_len) < 0.5, -1, 1).astype(np.float32)
+    da, db, do = up(native, a), up(native, b), empty(native, n)
+    native.binary_f32(op, da, a_len, db, b_len, do, n)
+    out = down(native, do, n)
+    ref = oracle.binary_mod_f32(op, a, b, n)
+    assert np.array_equal(out, ref)
+
+
+def test_binary_f32_pow_ulps(native, oracle):
+    announce("binary_f32 pow")
+    g = rng(7)
+    a = g.uniform(0.1, 3, 5000).astype(np.float32)
+    b = g.uniform(-3, 3, 5000).astype(np.float32)
+    da, db, do = up(native, a), up(native, b), empty(native, 5000)
+    native.binary_f32(POW, da, 5000, db, 5000, do, 5000)
+    out = down(native, do, 5000)
+    assert np.max(ulp_diff(out, oracle.binary_mod_f32(POW, a, b, 5000))) <= 2
+
+
+def test_binary_reference_goldens(native, ref_vectors):
+    announce("binary goldens")
+    v = ref_vectors["vector_arith"]
+    a, b = np.array(v["a"], np.float32), np.array(v["b"], np.float32)
+    da, db, do = up(native, a), up(native, b), empty(native, 16)
+    for op, key in [(ADD, "add"), (SUB, "sub"), (MUL, "mul"), (DIV, "div")]:
+        native.binary_f32(op, da, 16, db, 16, do, 16)
+        assert np.max(np.abs(down(native, do, 16) - v[key])) <= v["tol_abs"], key
+    m = ref_vectors["msl_add"]
+    da, db, do = up(native, np.float32(m["bcast_a"])), up(native, np.float32(m["bcast_b"])), empty(native, 4)
+    native.binary_f32(ADD, da, 4, db, 1, do, 4)
+    assert np.array_equal(down(native, do, 4), m["bcast_out"])
+    ia, ib, io = up(native, np.int32(m["int_a"])), up(native, np.int32(m["int_b"])), empty(native, 4, np.int32)
+    native.binary_i32(ADD, ia, 4, ib, 4, io, 4)
+    assert np.array_equal(down(native, io, 4, np.int32), m["int_out"])
+
+
+@pytest.mark.parametrize("op", [ADD, SUB, MUL, DIV, POW])
+def test_binary_i32_exact(native, oracle, op):
+    announce(f"binary_i32 op={op}")
+    g = rng(200 + op)
+    n = 3001
+    a = g.integers(-50, 50, n).astype(np.int32)
+    b = g.integers(1, 6, 97).astype(np.int32) if op != SUB else g.integers(-9, 9, 97).astype(np.int32)
+    if op == POW:
+        a = g.integers(-6, 6, n).astype(np.int32)
+        b = g.integers(0, 5, 97).astype(np.int32)
+    da, db, do = up(native, a), up(native, b), empty(native, n, np.int32)
+    native.binary_i32(op, da, n, db, 97, do, n)
+    assert np.array_equal(down(native, do, n, np.int32), oracle.binary_mod_i32(op, a, b, n))
+
+
+@pytest.mark.parametrize("shape,sa_shape,sb_shape", [
+    ((2, 2, 3), (2, 2, 3), (2, 1, 3)),     # middle-axis broadcast
+    ((3, 3), (3, 1), (1, 3)),              # two-sided
+    ((4, 5, 6, 7), (4, 1, 6, 1), (1, 5, 1, 7)),
+    ((64, 300), (64, 300), (300,)),
+])
+def test_binary_strided(native, oracle, shape, sa_shape, sb_shape):
+    announce(f"binary_strided {shape}")
+    g = rng(300)
+    a = g.uniform(-1, 1, sa_shape).astype(np.float32)
+    b = g.uniform(-1, 1, sb_shape).astype(np.float32)
+    ab = np.broadcast_to(a, shape)
+    bb = np.broadcast_to(b.reshape((1,) * (len(shape) - b.ndim) + b.shape), shape)
+    sa = [s // 4 for s in ab.strides]
+    sb = [s // 4 for s in bb.strides]
+    da, db, do = up(native, a), up(native, b), empty(native, int(np.prod(shape)))
+    native.binary_strided_f32(MUL, shape, da, sa, db, sb, do)
+    out = down(native, do, shape)
+    assert np.array_equal(out, oracle.binary_strided_f32(MUL, shape, a, sa, b, sb))
+    assert np.array_equal(out, ab * bb)
+
+
+@pytest.mark.parametrize("n", [1, 5, 4096, 100003])
+def test_unary(native, oracle, n):
+    announce(f"unary n={n}")
+    x = rng(400).normal(0, 4, n).astype(np.float32)
+    dx, do = up(native, x), empty(native, n)
+    native.unary_f32(native.SIGMOID, dx, do, n)
+    assert np.max(ulp_diff(down(native, do, n), oracle.sigmoid(x))) <= 4
+    native.unary_f32(native.RELU, dx, do, n)
+    assert np.array_equal(down(native, do, n), oracle.relu(x))
+
+
+def test_unary_goldens(native, ref_vectors):
+    announce("unary goldens")
+    s = ref_vectors["sigmoid"]
+    dx, do = up(native, np.float32(s["x"])), empty(native, 5)
+    native.unary_f32(native.SIGMOID, dx, do, 5)
+    out = down(native, do, 5)
+    assert np.max(np.abs(out[:3] - s["expected_first3"])) <= s["tol_abs"]
+    assert out[3] > s["x3_gt"] and out[4] < s["x4_lt"]
+
+
+def test_bias_sigmoid_and_backward(native, oracle):
+    announce("bias_sigmoid / sigmoid_backward")
+    g = rng(500)
+    d = g.normal(0, 1, (33, 70)).astype(np.float32)
+    b = g.normal(0, 1, 70).astype(np.float32)
+    dd, db = up(native, d), up(native, b)
+    native.bias_sigmoid_f32(dd, db, d.size, 70)
+    assert np.max(ulp_diff(down(native, dd, d.shape), oracle.bias_sigmoid(d, b))) <= 4
+    dout = g.normal(0, 1, 999).astype(np.float32)
+    x = g.normal(0, 2, 999).astype(np.float32)
+    ddo, dxx, do = up(native, dout), up(native, x), empty(native, 999)
+    native.sigmoid_backward_f32(ddo, dxx, do, 999)
+    ref = oracle.sigmoid_backward(dout, x)
+    assert np.max(np.abs(down(native, do, 999) - ref) / (np.abs(ref) + 1e-30)) < 2e-6
+
+
+@pytest.mark.parametrize("n", [4096, 4097, 3])
+def test_affine_exact(native, oracle, n):
+    announce(f"affine n={n}")
+    x = rng(600).uniform(-1, 1, n).astype(np.float32)
+    dx, do = up(native, x), empty(native, n)
+    native.affine_f32(dx, do, n, 1.7, -0.3)
+    assert np.array_equal(down(native, do, n), oracle.affine(x, 1.7, -0.3))
+
+
+# ---- fused program ----------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [1 << 20, 1001])
+def test_program_affine_chain_exact(native, oracle, n):
+    announce(f"program chain n={n}")
+    g = rng(700)
+    x = g.uniform(-1, 1, n).astype(np.float32)
+    sc = g.uniform(0.9, 1.1, 20).astype(np.float32)
+    of = g.uniform(-0.1, 0.1, 20).astype(np.float32)
+    dx, do = up(native, x), empty(native, n)
+    instrs = [(native.PI_LOAD, 0, 0, 0, 0.0, 0.0)] + \
+             [(native.PI_FMAI, 0, 0, 0, float(a), float(b)) for a, b in zip(sc, of)]
+    prog = native.make_program((n,), [(dx, (1,))], instrs)
+    native.program_f32(prog, do)
+    assert np.array_equal(down(native, do, n), oracle.affine_chain(x, sc, of))
+
+
+def test_program_general_graph(native, oracle):
+    """relu(x*w + b) - sigmoid(y) / 3 with b broadcast over rows, y full."""
+    announce("program general")
+    g = rng(710)
+    R, Cc = 37, 129
+    x = g.normal(0, 1, (R, Cc)).astype(np.float32)
+    y = g.normal(0, 1, (R, Cc)).astype(np.float32)
+    b = g.normal(0, 1, Cc).astype(np.float32)
+    dx, dy, dbb, do = up(native, x), up(native, y), up(native, b), empty(native, R * Cc)
+    P = native
+    instrs = [(P.PI_LOAD, 0, 0), (P.PI_MULI, 0, 0, 0, 0.75), (P.PI_LOAD, 1, 2),
+              (P.PI_ADD, 0, 0, 1), (P.PI_RELU, 0, 0), (P.PI_LOAD, 2, 1), (P.PI_SIGMOID, 2, 2),
+              (P.PI_CONST, 3, 0, 0, 3.0), (P.PI_DIV, 2, 2, 3), (P.PI_SUB, 0, 0, 2)]
+    prog = P.make_program((R, Cc), [(dx, (Cc, 1)), (dy, (Cc, 1)), (dbb, (0, 1))], instrs)
+    P.program_f32(prog, do)
+    out = down(native, do, (R, Cc))
+    t = oracle.relu(oracle.binary_mod_f32(ADD, oracle.binary_mod_f32(MUL, x.ravel(), [0.75], x.size),
+                                          b, x.size))
+    s = oracle.binary_mod_f32(DIV, oracle.sigmoid(y.ravel()), [3.0], y.size)
+    ref = oracle.binary_mod_f32(SUB, t, s, x.size).reshape(R, Cc)
+    assert np.max(ulp_diff(out, ref)[np.abs(ref) > 1e-6]) <= 4
+    assert np.max(np.abs(out - ref)) < 1e-6
+
+
+# ---- reductions ------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,offset", [(1, 0), (7, 0), (1000, 1), (65536, 0), (1 << 22, 3),
+                                      (12345679, 2)])
+def test_sum_min_max(native, oracle, n, offset):
+    announce(f"sum/min/max n={n} offset={offset}")
+    g = rng(800 + n % 97)
+    x = g.uniform(-1, 1, n + offset).astype(np.float32)
+    dx, do = up(native, x), empty(native, 1)
+    view = dx.ptr + 4 * offset
+    native.sum_f32(view, n, do)
+    s = float(down(native, do, 1)[0])
+    s64 = oracle.sum_f64(x[offset:])
+    assert abs(s - s64) <= 1e-5 * abs(s64) + 1e-6, (s, s64)
+    native.min_f32(view, n, do)
+    assert down(native, do, 1)[0] == oracle.fmin(x[offset:])
+    native.max_f32(view, n, do)
+    assert down(native, do, 1)[0] == oracle.fmax(x[offset:])
+
+
+def test_sum_empty_and_min_empty(native):
+    announce("sum empty")
+    do = empty(native, 1)
+    native.sum_f32(do, 0, do)
+    assert down(native, do, 1)[0] == 0.0
+    with pytest.raises(native.SilGpuError):
+        native.min_f32(do, 0, do)
+
+
+def test_reduction_goldens(native, ref_vectors):
+    announce("reduction goldens")
+    ag = ref_vectors["aggregates"]
+    t = np.array(ag["t_3_2_3"], np.float32)
+    dt, do = up(native, t), empty(native, 16)
+    native.sum_f32(dt, t.size, do)
+    assert down(native, do, 1)[0] == ag["sum"]
+    for ax in range(3):
+        outer = int(np.prod(t.shape[:ax]))
+        inner = int(np.prod(t.shape[ax + 1:]))
+        native.sum_axis_f32(dt, outer, t.shape[ax], inner, do)
+        got = down(native, do, outer * inner)
+        assert np.array_equal(got, np.ravel(ag[f"sum{ax}"])), ax
+    ones = up(native, np.ones((256, 128), np.float32))
+    native.sum_f32(ones, 256 * 128, do)
+    assert down(native, do, 1)[0] == ag["ones_256x128_sum"]
+    native.sum_axis_f32(ones, 1, 256, 128, do)
+    assert down(native, do, 1)[0] == ag["ones_256x128_sum0_first"]
+
+
+@pytest.mark.parametrize("shape,axis", [((4096, 8192), 1), ((4096, 8192), 0), ((3, 100000), 1),
+                                        ((100, 3), 1), ((7, 300, 9), 1), ((5, 4, 3, 2), 2),
+                                        ((1, 5000000), 1), ((20000, 4), 0), ((70000, 2), 1)])
+def test_sum_axis(native, oracle, shape, axis):
+    announce(f"sum_axis {shape} axis={axis}")
+    x = rng(900).normal(0, 3, shape).astype(np.float32)
+    outer = int(np.prod(shape[:axis]))
+    inner = int(np.prod(shape[axis + 1:]))
+    dx, do = up(native, x), empty(native, outer * inner)
+    native.sum_axis_f32(dx, outer, shape[axis], inner, do)
+    got = down(native, do, outer * inner).astype(np.float64)
+    ref = oracle.sum_axis_f64(x, axis).ravel()
+    absref = oracle.sum_axis_f64(np.abs(x), axis).ravel()
+    # relative 1e-5 of the exact sum, with the fp32 output rounding (2^-24 of
+    # the magnitude) as a floor for sums that cancel to near zero
+    assert np.all(np.abs(got - ref) <= 1e-5 * np.abs(ref) + 6e-8 * absref + 1e-30)
+
+
+@pytest.mark.parametrize("rows,cols", [(2, 3), (4096, 256), (1024, 2048), (1, 67108864),
+                                       (64, 100003), (3, 1 << 20), (70000, 5)])
+def test_argmax_rows(native, oracle, rows, cols):
+    announce(f"argmax {rows}x{cols}")
+    g = rng(1000 + rows)
+    x = g.uniform(-1, 1, (rows, cols)).astype(np.float32)
+    # a unique planted maximum not aligned to 4 or to a workgroup chunk, and ties
+    x[:, (cols * 7) // 9] = 2.0
+    if cols > 10:
+        x[rows // 2, 3] = 2.0  # tie with the later column: first index must win
+    dx, do = up(native, x), empty(native, rows, np.int32)
+    native.argmax_rows_f32(dx, rows, cols, do)
+    assert np.array_equal(down(native, do, rows, np.int32), oracle.argmax_rows(x))
+
+
+def test_argmax_golden_nan_negative(native, oracle, ref_vectors):
+    announce("argmax goldens")
+    a = np.array(ref_vectors["argmax"]["x"], np.float32)
+    dx, do = up(native, a), empty(native, 2, np.int32)
+    native.argmax_rows_f32(dx, 2, 3, do)
+    assert list(down(native, do, 2, np.int32)) == ref_vectors["argmax"]["out"]
+    z = np.array([[np.nan, 1.0, 3.0, np.nan, -1.0, 3.0], [-5, -4, -3, -2, -1, -9]], np.float32)
+    dz, do = up(native, z), empty(native, 2, np.int32)
+    native.argmax_rows_f32(dz, 2, 6, do)
+    assert list(down(native, do, 2, np.int32)) == list(oracle.argmax_rows(z)) == [2, 4]
+
+
+# ---- row ops ----------------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,cols", [(2, 3), (64, 32), (4096, 8192), (300, 512), (100, 1000),
+                                       (50, 2048), (33, 3000), (16, 16384), (5, 40000),
+                                       (7, 4097), (1, 1)])
+def test_softmax_rows(native, oracle, rows, cols):
+    announce(f"softmax {rows}x{cols}")
+    x = rng(1100 + cols).normal(0, 3, (rows, cols)).astype(np.float32)
+    dx, do = up(native, x), empty(native, rows * cols)
+    native.softmax_rows_f32(dx, do, rows, cols)
+    out = down(native, do, (rows, cols)).astype(np.float64)
+    ref = oracle.softmax_rows_f64(x)
+    # relative 1e-5 per element (entries below 1e-30 compared absolutely)
+    assert np.all(np.abs(out - ref) <= 1e-5 * ref + 1e-30)
+
+
+def test_softmax_golden(native, ref_vectors):
+    announce("softmax golden")
+    s = ref_vectors["softmax"]
+    dx, do = up(native, np.float32([s["x"]])), empty(native, 3)
+    native.softmax_rows_f32(dx, do, 1, 3)
+    assert np.max(np.abs(down(native, do, 3) - s["expected"])) <= s["tol_abs"]
+
+
+@pytest.mark.parametrize("rows,cols", [(2, 3), (64, 256), (4096, 8192), (2048, 768), (9, 1001),
+                                       (16, 16384), (3, 50000), (1, 1)])
+def test_layer_norm_rows(native, oracle, rows, cols):
+    announce(f"layer_norm {rows}x{cols}")
+    g = rng(1200 + cols)
+    x = g.normal(0, 3, (rows, cols)).astype(np.float32)
+    if rows * cols <= 1 << 20:
+        gamma = g.uniform(0.5, 1.5, cols).astype(np.float32)
+        beta = g.uniform(-1, 1, cols).astype(np.float32)
+    else:
+        gamma = np.ones(cols, np.float32)
+        beta = np.zeros(cols, np.float32)
+    dx, dg, db, do = up(native, x), up(native, gamma), up(native, beta), empty(native, rows * cols)
+    native.layer_norm_rows_f32(dx, do, dg, db, rows, cols, 1e-5)
+    out = down(native, do, (rows, cols)).astype(np.float64)
+    ref = oracle.layer_norm_f64(x, gamma, beta, 1e-5)
+    # |y - y64| <= 1e-5 * max(1, |y64|): relative 1e-5 at the unit scale the
+    # normalisation produces
+    assert np.all(np.abs(out - ref) <= 1e-5 * np.maximum(1.0, np.abs(ref)))
+
+
+def test_layer_norm_golden(native, ref_vectors):
+    announce("layer_norm golden")
+    ln = ref_vectors["layer_norm"]
+    x = np.array(ln["x"], np.float32)
+    dx, do = up(native, x), empty(native, 6)
+    native.layer_norm_rows_f32(dx, do, up(native, np.float32(ln["gamma"])),
+                               up(native, np.float32(ln["beta"])), 2, 3, 1e-5)
+    assert np.max(np.abs(down(native, do, (2, 3))[0] - ln["row0"])) <= ln["tol_abs"]
+
+
+# ---- GEMM / GEMV ------------------------------------------------------------------
+
+def _gemm_case(native, oracle, M, N, K, ta=False, tb=False, epi=0, bias_len=0, seed=0,
+               dist="uniform"):
+    g = rng(seed + 7 * M + 3 * N + K)
+    if dist == "uniform":
+        A = g.uniform(-1, 1, (K, M) if ta else (M, K)).astype(np.float32)
+        B = g.uniform(-1, 1, (N, K) if tb else (K, N)).astype(np.float32)
+    else:
+        A = g.normal(0, 0.02, (K, M) if ta else (M, K)).astype(np.float32)
+        B = g.normal(0, 0.02, (N, K) if tb else (K, N)).astype(np.float32)
+    dA, dB, dC = up(native, A), up(native, B), empty(native, M * N)
+    bias = g.normal(0, 1, max(bias_len, 1)).astype(np.float32)
+    dbias = up(native, bias) if bias_len else None
+    native.sgemm(ta, tb, M, N, K, dA, A.shape[1], 0, dB, B.shape[1], 0, dC, N, 0, 1,
+                 dbias, bias_len, epi)
+    Cg = down(native, dC, (M, N))
+    C64, Cabs = oracle.sgemm_f64(A, B, ta=ta, tb=tb, with_abs=True)
+    if epi in (native.EPI_BIAS, native.EPI_BIAS_SIGMOID, native.EPI_BIAS_RELU):
+        bb = bias[np.arange(N) % bias_len].astype(np.float64)
+        C64 = C64 + bb
+        Cabs = Cabs + np.abs(bb)
+    if epi == native.EPI_BIAS_SIGMOID:
+        # sigmoid is 1/4-Lipschitz: the pre-activation bound carries over
+        C64 = 1 / (1 + np.exp(-C64))
+        Cabs = Cabs / 4 + 1e-7
+    if epi in (native.EPI_RELU, native.EPI_BIAS_RELU):
+        C64 = np.maximum(C64, 0)
+    return Cg, C64, Cabs
+
+
+ROUTING_SHAPES = [(1, 16, 3), (15, 16, 16), (16, 16, 16), (17, 50, 17), (32, 768, 4096),
+                  (33, 65, 15), (63, 64, 784), (64, 64, 64), (96, 4096, 8), (97, 1, 17),
+                  (100, 768, 784), (128, 128, 16), (256, 512, 130), (1, 4096, 4096),
+                  (64, 1, 300), (3, 5, 1)]
+
+
+@pytest.mark.parametrize("M,N,K", ROUTING_SHAPES)
+def test_sgemm_routing_shapes(native, oracle, M, N, K):
+    announce(f"sgemm NN {M}x{N}x{K}")
+    Cg, C64, Cabs = _gemm_case(native, oracle, M, N, K)
+    ok, nw, el = gemm_tolerance_ok(Cg, C64, Cabs, K)
+    assert ok, (nw, el)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(4, 3, 2), (17, 33, 65), (128, 256, 64), (200, 130, 70),
+                                   (1, 300, 200), (300, 1, 200)])
+def test_sgemm_transposed(native, oracle, ta, tb, M, N, K):
+    announce(f"sgemm ta={ta} tb={tb} {M}x{N}x{K}")
+    Cg, C64, Cabs = _gemm_case(native, oracle, M, N, K, ta=ta, tb=tb)
+    ok, nw, el = gemm_tolerance_ok(Cg, C64, Cabs, K)
+    assert ok, (nw, el)
+
+
+@pytest.mark.parametrize("epi,bias_len", [(1, 96), (2, 96), (3, 0), (4, 96), (1, 32)])
+@pytest.mark.parametrize("M,N,K", [(100, 96, 48), (256, 384, 256), (1, 96, 64)])
+def test_sgemm_epilogues(native, oracle, epi, bias_len, M, N, K):
+    announce(f"sgemm epi={epi} {M}x{N}x{K}")
+    Cg, C64, Cabs = _gemm_case(native, oracle, M, N, K, epi=epi, bias_len=bias_len)
+    ok, nw, el = gemm_tolerance_ok(Cg, C64, Cabs, K)
+    assert ok, (nw, el)
+
+
+def test_sgemm_reference_goldens(native, ref_vectors):
+    announce("sgemm goldens")
+    d = ref_vectors["dot"]
+    a = np.float32(d["mm_a_3x4_iota1"])
+    b = np.float32(d["mm_b_4x2_iota1"])
+    dA, dB, dC = up(native, a), up(native, b), empty(native, 6)
+    native.sgemm(0, 0, 3, 2, 4, dA, 4, 0, dB, 2, 0, dC, 2, 0)
+    assert np.array_equal(down(native, dC, (3, 2)), d["mm_out"])
+    lin = ref_vectors["linear"]
+    dX, dW, dbias, dO = (up(native, np.float32(lin["x"])), up(native, np.float32(lin["W"])),
+                         up(native, np.float32(lin["b"])), empty(native, 4))
+    native.sgemm(0, 0, 2, 2, 3, dX, 3, 0, dW, 2, 0, dO, 2, 0, 1, dbias, 2, native.EPI_BIAS)
+    assert np.array_equal(down(native, dO, (2, 2)), lin["out"])
+    e = ref_vectors["dot_example"]
+    dx, dW, dy = up(native, np.float32(e["x"])), up(native, np.float32(e["W"])), empty(native, 2)
+    native.sgemm(0, 0, 1, 2, 3, dx, 3, 0, dW, 2, 0, dy, 2, 0)
+    assert np.array_equal(down(native, dy, 2), e["y"])
+    t = ref_vectors["dot_transposed"]
+    dd, dW2, dxo = up(native, np.ones((4, 2), np.float32)), up(native, np.full((3, 2), 0.5, np.float32)), empty(native, 12)
+    native.sgemm(0, 1, 4, 3, 2, dd, 2, 0, dW2, 2, 0, dxo, 3, 0)
+    assert np.allclose(down(native, dxo, (4, 3)), t["dx"]["value"], rtol=t["eps_rel"])
+
+
+def test_sgemm_batched(native, oracle):
+    announce("sgemm batched 48x512x64x512")
+    g = rng(1300)
+    Bt, M, N, K = 48, 512, 512, 64
+    A = g.normal(0, 1, (Bt, M, K)).astype(np.float32)
+    B = g.normal(0, 1, (Bt, K, N)).astype(np.float32)
+    dA, dB, dC = up(native, A), up(native, B), empty(native, Bt * M * N)
+    native.sgemm(0, 0, M, N, K, dA, K, M * K, dB, N, K * N, dC, N, M * N, Bt)
+    Cg = down(native, dC, (Bt, M, N))
+    for b in (0, 17, 47):
+        C64, Cabs = oracle.sgemm_f64(A[b], B[b], with_abs=True)
+        ok, nw, el = gemm_tolerance_ok(Cg[b], C64, Cabs, K)
+        assert ok, (b, nw, el)
+
+
+@pytest.mark.parametrize("S", [2048, 8192])
+def test_sgemm_large_sampled(native, oracle, S):
+    """Full-size square SGEMM (configs 4): fp64 dot products at 4096 sampled
+    entries plus the closed form ones * ones = K on a second run."""
+    announce(f"sgemm {S}^3 sampled")
+    g = rng(1400 + S)
+    A = g.uniform(-1, 1, (S, S)).astype(np.float32)
+    B = g.uniform(-1, 1, (S, S)).astype(np.float32)
+    dA, dB, dC = up(native, A), up(native, B), empty(native, S * S)
+    native.sgemm(0, 0, S, S, S, dA, S, 0, dB, S, 0, dC, S, 0)
+    Cg = down(native, dC, (S, S))
+    rows = g.integers(0, S, 4096)
+    cols = g.integers(0, S, 4096)
+    rows[:4] = [0, S - 1, 0, S - 1]
+    cols[:4] = [0, S - 1, S - 1, 0]
+    ref, refabs = oracle.sgemm_sampled_f64(A, B, rows, cols)
+    tol = 1e-5 * math.sqrt(S)
+    diff = np.abs(Cg[rows, cols] - ref)
+    assert np.all(diff <= tol * refabs), float(np.max(diff / refabs))
+    assert np.linalg.norm(diff) / np.linalg.norm(ref) <= tol
+    del A, B
+    ones = up(native, np.ones((S, S), np.float32))
+    native.sgemm(0, 0, S, S, S, ones, S, 0, ones, S, 0, dC, S, 0)
+    assert np.all(down(native, dC, (S, S)) == S)
+
+
+def test_gemv_config(native, oracle):
+    """configs[1](a): 1x4096 . 4096x4096, N(0, 0.02)."""
+    announce("gemv 1x4096x4096")
+    g = rng(1500)
+    x = g.normal(0, 0.02, 4096).astype(np.float32)
+    B = g.normal(0, 0.02, (4096, 4096)).astype(np.float32)
+    dx, dB, dy = up(native, x), up(native, B), empty(native, 4096)
+    native.sgemv(dx, dB, 4096, dy, 4096, 4096)
+    y = down(native, dy, 4096)
+    C64, Cabs = oracle.sgemm_f64(x[None, :], B, with_abs=True)
+    ok, nw, el = gemm_tolerance_ok(y[None, :], C64, Cabs, 4096)
+    assert ok, (nw, el)
+    # the sgemm entry routes M == 1 to the same kernel
+    dy2 = empty(native, 4096)
+    native.sgemm(0, 0, 1, 4096, 4096, dx, 4096, 0, dB, 4096, 0, dy2, 4096, 0)
+    assert np.array_equal(down(native, dy2, 4096), y)
+
+
+@pytest.mark.parametrize("N,K,ldb", [(4093, 1000, 4093), (100, 5, 128), (4096, 4096, 4100),
+                                     (1, 1, 1)])
+def test_gemv_ragged(native, oracle, N, K, ldb):
+    announce(f"gemv N={N} K={K} ldb={ldb}")
+    g = rng(1600 + N)
+    x = g.normal(0, 1, K).astype(np.float32)
+    Bfull = g.normal(0, 1, (K, ldb)).astype(np.float32)
+    dx, dB, dy = up(native, x), up(native, Bfull), empty(native, N)
+    native.sgemv(dx, dB, ldb, dy, N, K)
+    y = down(native, dy, N)
+    C64, Cabs = oracle.sgemm_f64(x[None, :], Bfull[:, :N], with_abs=True)
+    ok, nw, el = gemm_tolerance_ok(y[None, :], C64, Cabs, K)
+    assert ok, (nw, el)
+
+
+def test_linear_sigmoid_config(native, oracle):
+    """configs[1](c): sigmoid(X . W + b), X 256x4096, W 4096x4096, N(0, 0.02)."""
+    announce("linear_sigmoid 256x4096x4096")
+    Cg, C64, Cabs = _gemm_case(native, oracle, 256, 4096, 4096, epi=native.EPI_BIAS_SIGMOID,
+                               bias_len=4096, dist="normal")
+    ok, nw, el = gemm_tolerance_ok(Cg, C64, Cabs, 4096)
+    assert ok, (nw, el)
+
+
+def test_small_batch_config(native, oracle):
+    """configs[1](b): 32x4096 . 4096x768."""
+    announce("sgemm 32x768x4096")
+    Cg, C64, Cabs = _gemm_case(native, oracle, 32, 768, 4096, dist="normal")
+    ok, nw, el = gemm_tolerance_ok(Cg, C64, Cabs, 4096)
+    assert ok, (nw, el)
