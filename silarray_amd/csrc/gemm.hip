@@ -271,22 +271,38 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
 
 // ---- GEMV: y[1 x N] = x[1 x K] * B[K x N] -----------------------------------
 //
-// HBM-bound: B (K*N floats) is read once.  Workgroup (ct, ks) covers 256
-// columns (one float4 per lane) and rows [ks*kc, (ks+1)*kc); its four
-// wavefronts take interleaved rows, eight loads in flight per lane.  The
-// split over K gives enough workgroups to fill the GPU; the last workgroup
-// of each column tile adds the K-split partials in a fixed order.
+// HBM-bound: B (K*N floats) is read once.  Pass 1: workgroup (ct, ks) covers
+// 256 columns (one float4 per lane) and rows [ks*kc, (ks+1)*kc); its four
+// wavefronts take interleaved rows with eight 16-byte non-temporal loads in
+// flight per lane, add their results in LDS and write one partial row
+// partial[ks][ct*256 ..] to scratch.  The K split gives ~1024 workgroups to
+// fill the GPU.  Pass 2 adds the partials per column in split order.  (An
+// in-kernel finish needs agent-scope fences or device-coherent stores and
+// measured slower on MI355X than the second launch.)
 constexpr int kGemvBlock = 256;
+constexpr int kGemvWaves = kGemvBlock / kWave;
 constexpr int kGemvCols = 256;  // columns per workgroup (64 lanes x float4)
+constexpr int kGemvUnroll = 8;
 
+__device__ __forceinline__ float4 load_nt4(const float *p) {
+  const float4 *q = reinterpret_cast<const float4 *>(p);
+  float4 v;
+  v.x = __builtin_nontemporal_load(&q->x);
+  v.y = __builtin_nontemporal_load(&q->y);
+  v.z = __builtin_nontemporal_load(&q->z);
+  v.w = __builtin_nontemporal_load(&q->w);
+  return v;
+}
+
+// VEC: N % 4 == 0, ldb % 4 == 0, B 16-byte aligned; lane owns 4 adjacent
+// columns.  !VEC: lane owns columns c0 + lane + 64*q, q < 4.
 template <bool VEC>
-__global__ __launch_bounds__(kGemvBlock) void gemv_n_k(const float *__restrict__ x,
-                                                       const float *__restrict__ Bm,
-                                                       int64_t ldb, float *__restrict__ y,
-                                                       int64_t N, int64_t K, int64_t kc,
-                                                       float *__restrict__ partial,
-                                                       unsigned int *counters) {
-  __shared__ float4 red[kGemvBlock / kWave][kWave];
+__global__ __launch_bounds__(kGemvBlock) void gemv_part_k(const float *__restrict__ x,
+                                                          const float *__restrict__ Bm,
+                                                          int64_t ldb, int64_t N, int64_t K,
+                                                          int64_t kc,
+                                                          float *__restrict__ partial) {
+  __shared__ float4 red[kGemvWaves][kWave];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int64_t c0 = int64_t(blockIdx.x) * kGemvCols;
   const int64_t k0 = int64_t(blockIdx.y) * kc;
@@ -297,14 +313,14 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_n_k(const float *__restrict__
     if (col < N) {
       const float *bp = Bm + col;
       int64_t k = k0 + wave;
-      constexpr int U = 8;
-      for (; k + (U - 1) * 4 < k1; k += U * 4) {
+      constexpr int U = kGemvUnroll, W = kGemvWaves;
+      for (; k + (U - 1) * W < k1; k += U * W) {
         float4 v[U];
         float xv[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          v[u] = *reinterpret_cast<const float4 *>(bp + (k + u * 4) * ldb);
-          xv[u] = x[k + u * 4];
+          v[u] = load_nt4(bp + (k + u * W) * ldb);
+          xv[u] = x[k + u * W];
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -314,8 +330,8 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_n_k(const float *__restrict__
           acc.w += xv[u] * v[u].w;
         }
       }
-      for (; k < k1; k += 4) {
-        float4 v = *reinterpret_cast<const float4 *>(bp + k * ldb);
+      for (; k < k1; k += W) {
+        float4 v = load_nt4(bp + k * ldb);
         float xv = x[k];
         acc.x += xv * v.x;
         acc.y += xv * v.y;
@@ -324,11 +340,10 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_n_k(const float *__restrict__
       }
     }
   } else {
-    // Lane handles columns c0 + lane + 64*q, q < 4.
-    for (int64_t k = k0 + wave; k < k1; k += 4) {
+    for (int64_t k = k0 + wave; k < k1; k += kGemvWaves) {
       const float xv = x[k];
       const float *row = Bm + k * ldb;
-      int64_t c = c0 + lane;
+      const int64_t c = c0 + lane;
       if (c < N) acc.x += xv * row[c];
       if (c + 64 < N) acc.y += xv * row[c + 64];
       if (c + 128 < N) acc.z += xv * row[c + 128];
@@ -338,51 +353,51 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_n_k(const float *__restrict__
   red[wave][lane] = acc;
   __syncthreads();
   if (wave != 0) return;
-  float4 s = red[0][lane];
 #pragma unroll
-  for (int w = 1; w < kGemvBlock / kWave; ++w) {
+  for (int w = 1; w < kGemvWaves; ++w) {
     float4 o = red[w][lane];
-    s.x += o.x;
-    s.y += o.y;
-    s.z += o.z;
-    s.w += o.w;
+    acc.x += o.x;
+    acc.y += o.y;
+    acc.z += o.z;
+    acc.w += o.w;
   }
-  auto col_of = [&](int q) -> int64_t {
-    return VEC ? c0 + lane * 4 + q : c0 + lane + 64 * q;
-  };
-  if (gridDim.y == 1) {
-    float sv[4] = {s.x, s.y, s.z, s.w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (col_of(q) < N) y[col_of(q)] = sv[q];
-    return;
+  // partial row ks holds N floats in the same per-lane order as the columns.
+  float *prow = partial + int64_t(blockIdx.y) * (int64_t(gridDim.x) * kGemvCols) + c0;
+  reinterpret_cast<float4 *>(prow)[lane] = acc;
+}
+
+// Pass 2: 64 columns per workgroup, the four wavefronts split the K splits.
+// Partial slot q of lane l in tile ct maps to column c0 + 4l + q (VEC) or
+// c0 + l + 64q (!VEC).
+template <bool VEC>
+__global__ __launch_bounds__(kGemvBlock) void gemv_finish_k(const float *__restrict__ partial,
+                                                            int64_t ks, int64_t pitch,
+                                                            int64_t N, float *__restrict__ y) {
+  __shared__ float red[kGemvWaves][kWave];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int64_t slot = int64_t(blockIdx.x) * kWave + lane;  // index into a partial row
+  float s = 0.0f;
+  if (slot < pitch) {
+    int64_t j = wave;
+    for (; j + 3 * kGemvWaves < ks; j += 4 * kGemvWaves) {
+      float o0 = partial[j * pitch + slot];
+      float o1 = partial[(j + kGemvWaves) * pitch + slot];
+      float o2 = partial[(j + 2 * kGemvWaves) * pitch + slot];
+      float o3 = partial[(j + 3 * kGemvWaves) * pitch + slot];
+      s += o0;
+      s += o1;
+      s += o2;
+      s += o3;
+    }
+    for (; j < ks; j += kGemvWaves) s += partial[j * pitch + slot];
   }
-  // Partial for this K split: partial[ks][ct*256 + lane*4 + q]
-  float4 *pp = reinterpret_cast<float4 *>(partial) +
-               (int64_t(blockIdx.y) * gridDim.x + blockIdx.x) * kWave + lane;
-  *pp = s;
-  __threadfence();  // publish the partial before counting this arrival
-  // Only wavefront 0 is still running: lane 0 counts, the result is
-  // broadcast through a register.
-  unsigned prev = 0;
-  if (lane == 0) prev = atomicAdd(counters + blockIdx.x, 1u);
-  prev = __shfl(prev, 0, kWave);
-  if (prev != gridDim.y - 1) return;
-  if (lane == 0) atomicExch(counters + blockIdx.x, 0u);
-  __threadfence();  // see every other workgroup's partial
-  float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (unsigned ks = 0; ks < gridDim.y; ++ks) {
-    float4 o = reinterpret_cast<const float4 *>(partial)[(int64_t(ks) * gridDim.x + blockIdx.x) *
-                                                           kWave + lane];
-    f.x += o.x;
-    f.y += o.y;
-    f.z += o.z;
-    f.w += o.w;
-  }
-  float fv[4] = {f.x, f.y, f.z, f.w};
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-    if (col_of(q) < N) y[col_of(q)] = fv[q];
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave != 0 || slot >= pitch) return;
+  s = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+  const int64_t ct = slot / kGemvCols, within = slot % kGemvCols;
+  const int64_t col = VEC ? slot : ct * kGemvCols + (within % 4) * 64 + within / 4;
+  if (col < N) y[col] = s;
 }
 
 // y[n] = sum_k x[k] * R[n*ldr + k]: one wavefront per output (rows of R
@@ -478,25 +493,30 @@ int launch_gemv_n(const float *x, const float *Bm, int64_t ldb, float *y, int64_
                   int64_t K, context *c) {
   const bool vec = N % 4 == 0 && ldb % 4 == 0 && aligned16(Bm);
   const int64_t ct = cdiv(N, kGemvCols);
-  // K splits: aim for ~1024 workgroups, >= 32 rows per split, kc % 4 == 0.
+  const int64_t pitch = ct * kGemvCols;
+  // K splits: ~1024 workgroups, >= 32 rows per split, partials fit scratch.
   int64_t ks = 1024 / ct;
-  if (ks < 1) ks = 1;
-  int64_t max_ks = K / 32;
-  if (ks > max_ks) ks = max_ks;
+  if (ks > K / 32) ks = K / 32;
   if (ks < 1) ks = 1;
   if (ks > 65535) ks = 65535;
-  while (ks > 1 && ks * ct * kGemvCols * int64_t(sizeof(float)) > int64_t(kPartialBytes)) ks /= 2;
-  if (ct > kCounterCount) ks = 1;
-  int64_t kc = cdiv(cdiv(K, ks), 4) * 4;
+  while (ks > 1 && ks * pitch * int64_t(sizeof(float)) > int64_t(kPartialBytes)) ks /= 2;
+  SILGPU_REQUIRE(pitch * int64_t(sizeof(float)) <= int64_t(kPartialBytes),
+                 "silgpu_sgemv: N %lld exceeds the scratch area", (long long)N);
+  const int64_t kc = cdiv(K, ks);
   ks = cdiv(K, kc);
+  float *partial = static_cast<float *>(c->partials);
   dim3 grid(static_cast<unsigned>(ct), static_cast<unsigned>(ks));
   if (vec)
-    gemv_n_k<true><<<grid, kGemvBlock, 0, c->stream>>>(
-        x, Bm, ldb, y, N, K, kc, static_cast<float *>(c->partials), c->counters);
+    gemv_part_k<true><<<grid, kGemvBlock, 0, c->stream>>>(x, Bm, ldb, N, K, kc, partial);
   else
-    gemv_n_k<false><<<grid, kGemvBlock, 0, c->stream>>>(
-        x, Bm, ldb, y, N, K, kc, static_cast<float *>(c->partials), c->counters);
-  SILGPU_LAUNCH_CHECK("gemv_n_k");
+    gemv_part_k<false><<<grid, kGemvBlock, 0, c->stream>>>(x, Bm, ldb, N, K, kc, partial);
+  SILGPU_LAUNCH_CHECK("gemv_part_k");
+  const unsigned fgrid = static_cast<unsigned>(cdiv(pitch, kWave));
+  if (vec)
+    gemv_finish_k<true><<<fgrid, kGemvBlock, 0, c->stream>>>(partial, ks, pitch, N, y);
+  else
+    gemv_finish_k<false><<<fgrid, kGemvBlock, 0, c->stream>>>(partial, ks, pitch, N, y);
+  SILGPU_LAUNCH_CHECK("gemv_finish_k");
   return SILGPU_OK;
 }
 

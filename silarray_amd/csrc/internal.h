@@ -20,23 +20,21 @@ namespace silgpu {
 int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 void clear_error();
 
-// Library context: device, the single stream, scratch for multi-block
+// Library context: device, the single stream, scratch for multi-pass
 // reductions.
 struct context {
   int device = -1;
   hipStream_t stream = nullptr;
   int cu_count = 0;
   int clock_khz = 0;
-  // Scratch: per-workgroup partial results (floats / doubles / (val, idx)
-  // pairs) and completion counters.  Counters are left at zero by every
-  // kernel that uses them (the last workgroup resets its counter), so no
-  // clearing launch is needed between calls on the stream.
-  void *partials = nullptr;      // kPartialBytes
-  unsigned int *counters = nullptr;  // kCounterCount
+  // Scratch: per-workgroup partial results (floats / doubles / (value,
+  // index) pairs) written by a reduction's first pass and read by its
+  // second.  Launches on the one stream run in order, so every call may
+  // reuse the whole area.
+  void *partials = nullptr;  // kPartialBytes
 };
 
 constexpr size_t kPartialBytes = size_t(16) << 20;  // 16 MiB
-constexpr int kCounterCount = 65536;
 
 // Returns the initialised context, or nullptr after recording an error.
 context *ctx();

@@ -2,15 +2,19 @@
 //
 // The reference reduces with one pass that writes up to 256 per-threadgroup
 // partials, a blocking host round trip, and a host finish over the partials
-// (include/array.h:1535-1545; include/gpu.h:323-354).  Here one launch does
-// both stages: every workgroup writes its partial to scratch, publishes it
-// with an agent-scope fence and a counter increment, and the workgroup that
-// arrives last reduces all partials in a fixed order.  The result never
-// leaves HBM unless the caller asks, and the fixed order makes results
+// (include/array.h:1535-1545; include/gpu.h:323-354).  Here the whole
+// reduction stays on the device and never synchronises with the host:
+//   pass 1: each workgroup streams one contiguous chunk of the input with
+//           16-byte non-temporal loads (eight in flight per thread) and
+//           writes one partial to scratch;
+//   pass 2: a small kernel reduces the partials in a fixed order.
+// The kernel boundary orders pass 2 after pass 1; an in-kernel "last
+// workgroup finishes" scheme needs agent-scope release/acquire fences
+// (L2 write-back + invalidate on every XCD), which on MI355X cost far more
+// than the second launch.  The fixed partial order makes every result
 // deterministic run to run.
 //
-// All kernels are HBM-bound (4 bytes read per element).  Loads are 16-byte
-// vectors, four in flight per thread.
+// All kernels are HBM-bound (4 bytes read per element).
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
@@ -23,8 +27,8 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
-constexpr int kUnroll = 4;
-constexpr int kMaxFullBlocks = 2048;
+constexpr int kUnroll = 8;          // 16-byte loads in flight per thread
+constexpr int kFullBlocks = 2048;   // pass-1 workgroups for a full reduction
 
 enum { R_SUM = 0, R_MIN = 1, R_MAX = 2 };
 
@@ -35,6 +39,10 @@ struct racc<R_SUM> {
   using T = double;  // fp64 accumulation: free on an HBM-bound pass
   __device__ static T init() { return 0.0; }
   __device__ static T add(T a, float x) { return a + static_cast<double>(x); }
+  __device__ static T add4(T a, float4 v) {
+    return a + (static_cast<double>(v.x) + static_cast<double>(v.y)) +
+           (static_cast<double>(v.z) + static_cast<double>(v.w));
+  }
   __device__ static T merge(T a, T b) { return a + b; }
 };
 template <>
@@ -42,6 +50,7 @@ struct racc<R_MIN> {
   using T = float;
   __device__ static T init() { return INFINITY; }
   __device__ static T add(T a, float x) { return fminf(a, x); }
+  __device__ static T add4(T a, float4 v) { return fminf(fminf(a, fminf(v.x, v.y)), fminf(v.z, v.w)); }
   __device__ static T merge(T a, T b) { return fminf(a, b); }
 };
 template <>
@@ -49,8 +58,18 @@ struct racc<R_MAX> {
   using T = float;
   __device__ static T init() { return -INFINITY; }
   __device__ static T add(T a, float x) { return fmaxf(a, x); }
+  __device__ static T add4(T a, float4 v) { return fmaxf(fmaxf(a, fmaxf(v.x, v.y)), fmaxf(v.z, v.w)); }
   __device__ static T merge(T a, T b) { return fmaxf(a, b); }
 };
+
+__device__ __forceinline__ float4 load_nt(const float4 *p) {
+  float4 v;
+  v.x = __builtin_nontemporal_load(&p->x);
+  v.y = __builtin_nontemporal_load(&p->y);
+  v.z = __builtin_nontemporal_load(&p->z);
+  v.w = __builtin_nontemporal_load(&p->w);
+  return v;
+}
 
 template <int R>
 __device__ __forceinline__ typename racc<R>::T wave_merge(typename racc<R>::T v) {
@@ -75,187 +94,142 @@ __device__ __forceinline__ typename racc<R>::T block_merge(typename racc<R>::T v
   return r;
 }
 
-// Returns true in every thread of the workgroup that arrives last at
-// `counter` (expected arrivals: `total`), and resets the counter for the
-// next kernel on the stream.  Before calling, each workgroup has written its
-// partial; the fences publish it across the XCDs' L2s and make the last
-// workgroup's later reads see every partial.
-__device__ __forceinline__ bool last_arrival(unsigned int *counter, unsigned int total) {
-  __shared__ bool last;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned int prev = atomicAdd(counter, 1u);
-    last = (prev == total - 1);
-    if (last) atomicExch(counter, 0u);
-  }
-  __syncthreads();
-  if (last) __threadfence();
-  return last;
-}
-
-// Full reduction of x[0..n).  x4 = x + head (16-byte aligned), n4 float4s
-// after the `head` leading scalars; `tail` trailing scalars follow.
+// Accumulates float4s [c0, c1) of x4 owned by this thread (stride kBlock).
 template <int R>
-__global__ __launch_bounds__(kBlock) void reduce_full_k(
-    const float *__restrict__ x, int head, const float4 *__restrict__ x4, int64_t n4,
-    const float *__restrict__ tail_ptr, int tail, typename racc<R>::T *__restrict__ partial,
-    unsigned int *counter, float *__restrict__ out) {
-  using T = typename racc<R>::T;
-  T acc = racc<R>::init();
-  const int64_t step = int64_t(gridDim.x) * kBlock;
-  int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
-  for (; i + (kUnroll - 1) * step < n4; i += kUnroll * step) {
+__device__ __forceinline__ typename racc<R>::T stream4(const float4 *__restrict__ x4,
+                                                      int64_t c0, int64_t c1,
+                                                      typename racc<R>::T acc) {
+  int64_t i = c0 + threadIdx.x;
+  for (; i + (kUnroll - 1) * kBlock < c1; i += kUnroll * kBlock) {
     float4 v[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) v[u] = x4[i + u * step];
+    for (int u = 0; u < kUnroll; ++u) v[u] = load_nt(x4 + i + u * kBlock);
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      acc = racc<R>::add(acc, v[u].x);
-      acc = racc<R>::add(acc, v[u].y);
-      acc = racc<R>::add(acc, v[u].z);
-      acc = racc<R>::add(acc, v[u].w);
-    }
+    for (int u = 0; u < kUnroll; ++u) acc = racc<R>::add4(acc, v[u]);
   }
-  for (; i < n4; i += step) {
-    float4 v = x4[i];
-    acc = racc<R>::add(acc, v.x);
-    acc = racc<R>::add(acc, v.y);
-    acc = racc<R>::add(acc, v.z);
-    acc = racc<R>::add(acc, v.w);
-  }
+  for (; i < c1; i += kBlock) acc = racc<R>::add4(acc, load_nt(x4 + i));
+  return acc;
+}
+
+// Pass 1 of a full reduction.  Workgroup b streams float4s
+// [b*chunk4, (b+1)*chunk4) of x4; workgroup 0 also takes the `head` scalars
+// before x4 and the `tail` scalars after the last float4.
+template <int R>
+__global__ __launch_bounds__(kBlock) void reduce_part_k(
+    const float *__restrict__ head_ptr, int head, const float4 *__restrict__ x4, int64_t n4,
+    int64_t chunk4, const float *__restrict__ tail_ptr, int tail,
+    typename racc<R>::T *__restrict__ partial) {
+  using T = typename racc<R>::T;
+  const int64_t c0 = int64_t(blockIdx.x) * chunk4;
+  const int64_t c1 = c0 + chunk4 < n4 ? c0 + chunk4 : n4;
+  T acc = stream4<R>(x4, c0, c1, racc<R>::init());
   if (blockIdx.x == 0) {
-    if (threadIdx.x < head) acc = racc<R>::add(acc, x[threadIdx.x]);
+    if (threadIdx.x < head) acc = racc<R>::add(acc, head_ptr[threadIdx.x]);
     if (threadIdx.x < tail) acc = racc<R>::add(acc, tail_ptr[threadIdx.x]);
   }
   T b = block_merge<R>(acc);
-  if (gridDim.x == 1) {
-    if (threadIdx.x == 0) out[0] = static_cast<float>(b);
-    return;
-  }
   if (threadIdx.x == 0) partial[blockIdx.x] = b;
-  if (!last_arrival(counter, gridDim.x)) return;
-  T f = racc<R>::init();
-  for (int j = threadIdx.x; j < static_cast<int>(gridDim.x); j += kBlock)
-    f = racc<R>::merge(f, partial[j]);
-  f = block_merge<R>(f);
-  if (threadIdx.x == 0) out[0] = static_cast<float>(f);
 }
 
+// Inputs that are not 4-byte aligned (never produced by the allocator; kept
+// so every pointer is accepted): scalar loads, same partial layout.
 template <int R>
-int launch_full(const float *x, int64_t n, float *out) {
-  SILGPU_REQUIRE(n >= 0, "reduce: negative n");
-  SILGPU_REQUIRE(n > 0 || R == R_SUM, "reduce: min/max of an empty array");
-  SILGPU_REQUIRE(out != nullptr && (n == 0 || x != nullptr), "reduce: null pointer");
-  SILGPU_CTX(c);
-  if (n == 0) {
-    float zero = 0.0f;
-    SILGPU_HIP_CHECK(hipMemcpyAsync(out, &zero, sizeof(float), hipMemcpyHostToDevice,
-                                    c->stream));
-    SILGPU_HIP_CHECK(hipStreamSynchronize(c->stream));
-    return SILGPU_OK;
-  }
-  int head = static_cast<int>(((16 - (reinterpret_cast<uintptr_t>(x) & 15)) & 15) / 4);
-  if (reinterpret_cast<uintptr_t>(x) & 3) head = 0;  // not even 4-aligned: scalar only
-  if (head > n) head = static_cast<int>(n);
-  int64_t body = n - head;
-  int64_t n4 = (reinterpret_cast<uintptr_t>(x) & 3) ? 0 : body / 4;
-  int64_t rest = body - n4 * 4;
-  const float *tail_ptr = x + head + n4 * 4;
-  int64_t g = cdiv(n4, int64_t(kBlock) * kUnroll);
-  if (g < 1) g = 1;
-  if (g > kMaxFullBlocks) g = kMaxFullBlocks;
+__global__ __launch_bounds__(kBlock) void reduce_part_scalar_k(
+    const float *__restrict__ x, int64_t n, int64_t chunk,
+    typename racc<R>::T *__restrict__ partial) {
   using T = typename racc<R>::T;
-  reduce_full_k<R><<<static_cast<unsigned>(g), kBlock, 0, c->stream>>>(
-      x, head, reinterpret_cast<const float4 *>(x + head), n4, tail_ptr, static_cast<int>(rest),
-      static_cast<T *>(c->partials), c->counters, out);
-  SILGPU_LAUNCH_CHECK("reduce_full_k");
-  return SILGPU_OK;
-}
-
-// Scalar fallback for inputs that are not 4-byte aligned (never produced by
-// the allocator; kept so every pointer is accepted).
-template <int R>
-__global__ __launch_bounds__(kBlock) void reduce_scalar_k(const float *__restrict__ x,
-                                                          int64_t n,
-                                                          typename racc<R>::T *partial,
-                                                          unsigned int *counter,
-                                                          float *__restrict__ out) {
-  using T = typename racc<R>::T;
+  const int64_t c0 = int64_t(blockIdx.x) * chunk;
+  const int64_t c1 = c0 + chunk < n ? c0 + chunk : n;
   T acc = racc<R>::init();
-  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n;
-       i += int64_t(gridDim.x) * kBlock)
-    acc = racc<R>::add(acc, x[i]);
+  for (int64_t i = c0 + threadIdx.x; i < c1; i += kBlock) acc = racc<R>::add(acc, x[i]);
   T b = block_merge<R>(acc);
   if (threadIdx.x == 0) partial[blockIdx.x] = b;
-  if (!last_arrival(counter, gridDim.x)) return;
+}
+
+// Pass 2: one workgroup reduces np partials in a fixed order.
+template <int R>
+__global__ __launch_bounds__(kBlock) void reduce_finish_k(
+    const typename racc<R>::T *__restrict__ partial, int np, float *__restrict__ out) {
+  using T = typename racc<R>::T;
   T f = racc<R>::init();
-  for (int j = threadIdx.x; j < static_cast<int>(gridDim.x); j += kBlock)
-    f = racc<R>::merge(f, partial[j]);
+  for (int j = threadIdx.x; j < np; j += kBlock) f = racc<R>::merge(f, partial[j]);
   f = block_merge<R>(f);
   if (threadIdx.x == 0) out[0] = static_cast<float>(f);
 }
 
 template <int R>
 int launch_reduce(const float *x, int64_t n, float *out) {
-  if (n > 0 && x && (reinterpret_cast<uintptr_t>(x) & 3)) {
-    SILGPU_CTX(c);
-    int64_t g = cdiv(n, int64_t(kBlock) * 16);
-    if (g > kMaxFullBlocks) g = kMaxFullBlocks;
-    using T = typename racc<R>::T;
-    reduce_scalar_k<R><<<static_cast<unsigned>(g), kBlock, 0, c->stream>>>(
-        x, n, static_cast<T *>(c->partials), c->counters, out);
-    SILGPU_LAUNCH_CHECK("reduce_scalar_k");
-    return SILGPU_OK;
+  SILGPU_REQUIRE(n >= 0, "reduce: negative n");
+  SILGPU_REQUIRE(n > 0 || R == R_SUM, "reduce: min/max of an empty array");
+  SILGPU_REQUIRE(out != nullptr && (n == 0 || x != nullptr), "reduce: null pointer");
+  SILGPU_CTX(c);
+  using T = typename racc<R>::T;
+  T *partial = static_cast<T *>(c->partials);
+  if (n == 0) return silgpu_fill_u32(out, 0u, 1);  // sum of nothing: +0.0f
+  int64_t blocks;
+  if (reinterpret_cast<uintptr_t>(x) & 3) {
+    blocks = cdiv(n, int64_t(kBlock) * 64);
+    if (blocks > kFullBlocks) blocks = kFullBlocks;
+    int64_t chunk = cdiv(n, blocks);
+    blocks = cdiv(n, chunk);
+    reduce_part_scalar_k<R><<<static_cast<unsigned>(blocks), kBlock, 0, c->stream>>>(
+        x, n, chunk, partial);
+    SILGPU_LAUNCH_CHECK("reduce_part_scalar_k");
+  } else {
+    int head = static_cast<int>(((16 - (reinterpret_cast<uintptr_t>(x) & 15)) & 15) / 4);
+    if (head > n) head = static_cast<int>(n);
+    const int64_t n4 = (n - head) / 4;
+    const int tail = static_cast<int>(n - head - 4 * n4);
+    // Chunks of whole kUnroll*kBlock float4 groups, at most kFullBlocks of them.
+    const int64_t group = int64_t(kUnroll) * kBlock;
+    int64_t chunk4 = cdiv(cdiv(n4 > 0 ? n4 : 1, kFullBlocks), group) * group;
+    blocks = n4 > 0 ? cdiv(n4, chunk4) : 1;
+    reduce_part_k<R><<<static_cast<unsigned>(blocks), kBlock, 0, c->stream>>>(
+        x, head, reinterpret_cast<const float4 *>(x + head), n4, chunk4, x + head + 4 * n4,
+        tail, partial);
+    SILGPU_LAUNCH_CHECK("reduce_part_k");
   }
-  return launch_full<R>(x, n, out);
+  reduce_finish_k<R><<<1, kBlock, 0, c->stream>>>(partial, static_cast<int>(blocks), out);
+  SILGPU_LAUNCH_CHECK("reduce_finish_k");
+  return SILGPU_OK;
 }
 
 // ---- sum over the last axis (rows of a [rows, cols] view) -------------------
 //
 // grid = (chunks, rows).  Workgroup (c, r) sums columns
-// [c*chunk, min(cols, (c+1)*chunk)) of row r in fp64.  With one chunk the
-// workgroup writes out[r]; otherwise partials go to scratch and the last
-// arrival for row r finishes in chunk order.
-__global__ __launch_bounds__(kBlock) void row_sum_k(const float *__restrict__ x,
-                                                    int64_t cols, int64_t chunk,
-                                                    bool vec, double *__restrict__ partial,
-                                                    unsigned int *counters,
+// [c*chunk, min(cols, (c+1)*chunk)) of row r in fp64.  With one chunk it
+// writes out[r]; otherwise it writes partial[r*chunks + c] and
+// row_sum_finish_k adds each row's partials in chunk order.
+__global__ __launch_bounds__(kBlock) void row_sum_k(const float *__restrict__ x, int64_t cols,
+                                                    int64_t chunk, bool vec,
+                                                    double *__restrict__ partial,
                                                     float *__restrict__ out) {
   const int64_t r = blockIdx.y;
   const float *row = x + r * cols;
   const int64_t c0 = int64_t(blockIdx.x) * chunk;
   const int64_t c1 = c0 + chunk < cols ? c0 + chunk : cols;
   double acc = 0.0;
-  if (vec) {  // cols % 4 == 0, row 16-byte aligned, chunk % 4 == 0
-    const float4 *r4 = reinterpret_cast<const float4 *>(row);
-    int64_t i = c0 / 4 + threadIdx.x, e4 = c1 / 4;
-    for (; i + 3 * kBlock < e4; i += 4 * kBlock) {
-      float4 v0 = r4[i], v1 = r4[i + kBlock], v2 = r4[i + 2 * kBlock], v3 = r4[i + 3 * kBlock];
-      acc += (double)v0.x + (double)v0.y + (double)v0.z + (double)v0.w;
-      acc += (double)v1.x + (double)v1.y + (double)v1.z + (double)v1.w;
-      acc += (double)v2.x + (double)v2.y + (double)v2.z + (double)v2.w;
-      acc += (double)v3.x + (double)v3.y + (double)v3.z + (double)v3.w;
-    }
-    for (; i < e4; i += kBlock) {
-      float4 v = r4[i];
-      acc += (double)v.x + (double)v.y + (double)v.z + (double)v.w;
-    }
-  } else {
+  if (vec)  // cols % 4 == 0, row 16-byte aligned, chunk % 4 == 0
+    acc = stream4<R_SUM>(reinterpret_cast<const float4 *>(row), c0 / 4, c1 / 4, acc);
+  else
     for (int64_t i = c0 + threadIdx.x; i < c1; i += kBlock) acc += (double)row[i];
-  }
   double b = block_merge<R_SUM>(acc);
-  if (gridDim.x == 1) {
-    if (threadIdx.x == 0) out[r] = static_cast<float>(b);
-    return;
-  }
-  if (threadIdx.x == 0) partial[r * gridDim.x + blockIdx.x] = b;
-  if (!last_arrival(counters + r, gridDim.x)) return;
-  if (threadIdx.x == 0) {
-    double f = 0.0;
-    for (unsigned j = 0; j < gridDim.x; ++j) f += partial[r * gridDim.x + j];
-    out[r] = static_cast<float>(f);
-  }
+  if (threadIdx.x != 0) return;
+  if (gridDim.x == 1)
+    out[r] = static_cast<float>(b);
+  else
+    partial[r * gridDim.x + blockIdx.x] = b;
+}
+
+// One thread per row adds that row's `chunks` partials in order.
+__global__ __launch_bounds__(kBlock) void row_sum_finish_k(const double *__restrict__ partial,
+                                                           int64_t rows, int64_t chunks,
+                                                           float *__restrict__ out) {
+  const int64_t r = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (r >= rows) return;
+  double f = 0.0;
+  for (int64_t j = 0; j < chunks; ++j) f += partial[r * chunks + j];
+  out[r] = static_cast<float>(f);
 }
 
 // Short rows: one wavefront per row, four rows per workgroup.
@@ -275,54 +249,55 @@ __global__ __launch_bounds__(kBlock) void row_sum_wave_k(const float *__restrict
 // ---- sum over a middle axis: out[o, i] = sum_a x[o, a, i], inner > 1 -------
 //
 // grid = (ceil(inner / kBlock), splits, outer).  Threads walk inner
-// (coalesced), each sums its share of the axis.  With splits > 1 partials
-// go to scratch and the last arrival per (o, inner-tile) finishes in split
-// order.
+// (coalesced), each sums its share of the axis.  With splits > 1 the
+// partials go to scratch as partial[(o*inner + i)*splits + s] and
+// axis_sum_finish_k adds them in split order.
 __global__ __launch_bounds__(kBlock) void axis_sum_k(const float *__restrict__ x,
                                                      int64_t axis_len, int64_t inner,
                                                      int64_t per_split,
                                                      double *__restrict__ partial,
-                                                     unsigned int *counters,
                                                      float *__restrict__ out) {
   const int64_t o = blockIdx.z;
   const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= inner) return;
   const int64_t a0 = int64_t(blockIdx.y) * per_split;
   const int64_t a1 = a0 + per_split < axis_len ? a0 + per_split : axis_len;
+  const float *p = x + o * axis_len * inner + i;
   double acc = 0.0;
-  if (i < inner) {
-    const float *p = x + o * axis_len * inner + i;
-    int64_t a = a0;
-    for (; a + 3 < a1; a += 4) {
-      float v0 = p[a * inner], v1 = p[(a + 1) * inner], v2 = p[(a + 2) * inner],
-            v3 = p[(a + 3) * inner];
-      acc += (double)v0;
-      acc += (double)v1;
-      acc += (double)v2;
-      acc += (double)v3;
-    }
-    for (; a < a1; ++a) acc += (double)p[a * inner];
+  int64_t a = a0;
+  for (; a + 7 < a1; a += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(p + (a + u) * inner);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc += (double)v[u];
   }
-  if (gridDim.y == 1) {
-    if (i < inner) out[o * inner + i] = static_cast<float>(acc);
-    return;
-  }
-  const int64_t tile = o * gridDim.x + blockIdx.x;
-  const int64_t nsplit = gridDim.y;
-  if (i < inner) partial[(tile * nsplit + blockIdx.y) * kBlock + threadIdx.x] = acc;
-  if (!last_arrival(counters + tile, gridDim.y)) return;
-  if (i < inner) {
-    double f = 0.0;
-    for (int64_t s = 0; s < nsplit; ++s) f += partial[(tile * nsplit + s) * kBlock + threadIdx.x];
-    out[o * inner + i] = static_cast<float>(f);
-  }
+  for (; a < a1; ++a) acc += (double)p[a * inner];
+  if (gridDim.y == 1)
+    out[o * inner + i] = static_cast<float>(acc);
+  else
+    partial[(o * inner + i) * gridDim.y + blockIdx.y] = acc;
+}
+
+__global__ __launch_bounds__(kBlock) void axis_sum_finish_k(const double *__restrict__ partial,
+                                                            int64_t count, int64_t splits,
+                                                            float *__restrict__ out) {
+  const int64_t j = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (j >= count) return;
+  double f = 0.0;
+  for (int64_t s = 0; s < splits; ++s) f += partial[j * splits + s];
+  out[j] = static_cast<float>(f);
 }
 
 // ---- argmax per row ---------------------------------------------------------
 
 struct vi {
   float v;
+  int32_t pad;
   int64_t i;
 };
+
+constexpr int64_t kNoIndex = INT64_MAX;
 
 // Larger value wins; equal values keep the smaller index; NaN never wins.
 __device__ __forceinline__ vi better(vi a, vi b) {
@@ -352,52 +327,70 @@ __device__ __forceinline__ vi block_best(vi x) {
     si[wave] = x.i;
   }
   __syncthreads();
-  vi r{sv[0], si[0]};
+  vi r{sv[0], 0, si[0]};
 #pragma unroll
-  for (int w = 1; w < kWaves; ++w) r = better(r, vi{sv[w], si[w]});
+  for (int w = 1; w < kWaves; ++w) r = better(r, vi{sv[w], 0, si[w]});
   return r;
 }
 
-constexpr int64_t kNoIndex = INT64_MAX;
+// Within one thread indices only increase, so a strict > keeps the first
+// maximum; NaN is replaced by any number.
+__device__ __forceinline__ void scan1(vi &best, float v, int64_t i) {
+  if (v > best.v || (best.v != best.v && v == v)) best = vi{v, 0, i};
+}
 
 // grid = (chunks, rows); workgroup (c, r) scans columns of chunk c of row r.
 __global__ __launch_bounds__(kBlock) void argmax_k(const float *__restrict__ x, int64_t cols,
                                                    int64_t chunk, bool vec,
                                                    vi *__restrict__ partial,
-                                                   unsigned int *counters,
                                                    int32_t *__restrict__ out) {
   const int64_t r = blockIdx.y;
   const float *row = x + r * cols;
   const int64_t c0 = int64_t(blockIdx.x) * chunk;
   const int64_t c1 = c0 + chunk < cols ? c0 + chunk : cols;
-  vi best{NAN, kNoIndex};
+  vi best{NAN, 0, kNoIndex};
   if (vec) {
     const float4 *r4 = reinterpret_cast<const float4 *>(row);
-    for (int64_t i = c0 / 4 + threadIdx.x; i < c1 / 4; i += kBlock) {
-      float4 v = r4[i];
-      int64_t b = i * 4;
-      // Within a thread indices increase, so strict > keeps the first max.
-      if (v.x > best.v || (best.v != best.v && v.x == v.x)) best = vi{v.x, b};
-      if (v.y > best.v || (best.v != best.v && v.y == v.y)) best = vi{v.y, b + 1};
-      if (v.z > best.v || (best.v != best.v && v.z == v.z)) best = vi{v.z, b + 2};
-      if (v.w > best.v || (best.v != best.v && v.w == v.w)) best = vi{v.w, b + 3};
+    int64_t i = c0 / 4 + threadIdx.x;
+    const int64_t e4 = c1 / 4;
+    for (; i + (kUnroll - 1) * kBlock < e4; i += kUnroll * kBlock) {
+      float4 v[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) v[u] = load_nt(r4 + i + u * kBlock);
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t b = (i + u * kBlock) * 4;
+        scan1(best, v[u].x, b);
+        scan1(best, v[u].y, b + 1);
+        scan1(best, v[u].z, b + 2);
+        scan1(best, v[u].w, b + 3);
+      }
+    }
+    for (; i < e4; i += kBlock) {
+      float4 v = load_nt(r4 + i);
+      scan1(best, v.x, i * 4);
+      scan1(best, v.y, i * 4 + 1);
+      scan1(best, v.z, i * 4 + 2);
+      scan1(best, v.w, i * 4 + 3);
     }
   } else {
-    for (int64_t i = c0 + threadIdx.x; i < c1; i += kBlock) {
-      float v = row[i];
-      if (v > best.v || (best.v != best.v && v == v)) best = vi{v, i};
-    }
+    for (int64_t i = c0 + threadIdx.x; i < c1; i += kBlock) scan1(best, row[i], i);
   }
   vi b = block_best(best);
-  if (gridDim.x == 1) {
-    if (threadIdx.x == 0) out[r] = static_cast<int32_t>(b.i == kNoIndex ? 0 : b.i);
-    return;
-  }
-  if (threadIdx.x == 0) partial[r * gridDim.x + blockIdx.x] = b;
-  if (!last_arrival(counters + r, gridDim.x)) return;
-  vi f{NAN, kNoIndex};
-  for (int64_t j = threadIdx.x; j < gridDim.x; j += kBlock)
-    f = better(f, partial[r * gridDim.x + j]);
+  if (threadIdx.x != 0) return;
+  if (gridDim.x == 1)
+    out[r] = static_cast<int32_t>(b.i == kNoIndex ? 0 : b.i);
+  else
+    partial[r * gridDim.x + blockIdx.x] = b;
+}
+
+// One workgroup per row merges that row's chunk results.
+__global__ __launch_bounds__(kBlock) void argmax_finish_k(const vi *__restrict__ partial,
+                                                          int64_t chunks,
+                                                          int32_t *__restrict__ out) {
+  const int64_t r = blockIdx.x;
+  vi f{NAN, 0, kNoIndex};
+  for (int64_t j = threadIdx.x; j < chunks; j += kBlock) f = better(f, partial[r * chunks + j]);
   f = block_best(f);
   if (threadIdx.x == 0) out[r] = static_cast<int32_t>(f.i == kNoIndex ? 0 : f.i);
 }
@@ -410,25 +403,26 @@ __global__ __launch_bounds__(kBlock) void argmax_wave_k(const float *__restrict_
   const int lane = threadIdx.x % kWave;
   if (r >= rows) return;
   const float *row = x + r * cols;
-  vi best{NAN, kNoIndex};
-  for (int64_t i = lane; i < cols; i += kWave) {
-    float v = row[i];
-    if (v > best.v || (best.v != best.v && v == v)) best = vi{v, i};
-  }
+  vi best{NAN, 0, kNoIndex};
+  for (int64_t i = lane; i < cols; i += kWave) scan1(best, row[i], i);
   best = wave_best(best);
   if (lane == 0) out[r] = static_cast<int32_t>(best.i == kNoIndex ? 0 : best.i);
 }
 
-// Chunks per row so that rows * chunks fills the GPU, each chunk >= 4096
-// elements and a multiple of 4 * kBlock.
-int64_t pick_chunks(int64_t rows, int64_t cols, int64_t max_chunks) {
+// Chunks per row: enough workgroups (rows * chunks ~ 2048) to fill the GPU,
+// each chunk >= 16384 elements and a whole number of kUnroll*kBlock float4
+// groups; the partials must fit the scratch area.
+int64_t chunk_len(int64_t rows, int64_t cols, size_t partial_bytes, int64_t &chunks) {
   int64_t target = 2048 / (rows > 0 ? rows : 1);
   if (target < 1) target = 1;
-  int64_t by_size = cols / 4096;
+  int64_t by_size = cols / 16384;
   if (by_size < 1) by_size = 1;
-  int64_t ch = target < by_size ? target : by_size;
-  if (ch > max_chunks) ch = max_chunks;
-  return ch;
+  chunks = target < by_size ? target : by_size;
+  while (chunks > 1 && rows * chunks * int64_t(partial_bytes) > int64_t(kPartialBytes)) chunks /= 2;
+  const int64_t group = int64_t(kUnroll) * kBlock * 4;
+  int64_t chunk = cdiv(cdiv(cols, chunks), group) * group;
+  chunks = cdiv(cols, chunk);
+  return chunk;
 }
 
 }  // namespace
@@ -457,9 +451,16 @@ int silgpu_sum_axis_f32(const float *d_in, int64_t outer, int64_t axis_len, int6
   SILGPU_CTX(c);
   if (axis_len == 0) return silgpu_fill_u32(d_out, 0u, outer * inner);
   SILGPU_REQUIRE(d_in != nullptr, "silgpu_sum_axis_f32: d_in is null");
+  double *partial = static_cast<double *>(c->partials);
   if (inner == 1) {
     const int64_t rows = outer, cols = axis_len;
-    if (rows > 65535 && cols > 2048) {  // grid.y limit: issue batches of rows
+    if (cols <= 2048) {
+      row_sum_wave_k<<<static_cast<unsigned>(cdiv(rows, kWaves)), kBlock, 0, c->stream>>>(
+          d_in, rows, cols, d_out);
+      SILGPU_LAUNCH_CHECK("row_sum_wave_k");
+      return SILGPU_OK;
+    }
+    if (rows > 65535) {  // grid.y limit: issue batches of rows
       for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
         int64_t nr = rows - r0 < 65535 ? rows - r0 : 65535;
         int rc = silgpu_sum_axis_f32(d_in + r0 * cols, nr, cols, 1, d_out + r0);
@@ -467,29 +468,23 @@ int silgpu_sum_axis_f32(const float *d_in, int64_t outer, int64_t axis_len, int6
       }
       return SILGPU_OK;
     }
-    if (cols <= 2048) {
-      row_sum_wave_k<<<static_cast<unsigned>(cdiv(rows, kWaves)), kBlock, 0, c->stream>>>(
-          d_in, rows, cols, d_out);
-      SILGPU_LAUNCH_CHECK("row_sum_wave_k");
-      return SILGPU_OK;
-    }
-    bool vec = cols % 4 == 0 && aligned16(d_in);
-    int64_t chunks = pick_chunks(rows, cols, kCounterCount / (rows > 0 ? rows : 1));
-    if (chunks > 1 && rows * chunks * int64_t(sizeof(double)) > int64_t(kPartialBytes))
-      chunks = 1;
-    int64_t chunk = cdiv(cdiv(cols, chunks), 4 * kBlock) * 4 * kBlock;
-    chunks = cdiv(cols, chunk);
+    const bool vec = cols % 4 == 0 && aligned16(d_in);
+    int64_t chunks;
+    const int64_t chunk = chunk_len(rows, cols, sizeof(double), chunks);
     dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(rows));
-    row_sum_k<<<grid, kBlock, 0, c->stream>>>(d_in, cols, chunk, vec,
-                                              static_cast<double *>(c->partials),
-                                              c->counters, d_out);
+    row_sum_k<<<grid, kBlock, 0, c->stream>>>(d_in, cols, chunk, vec, partial, d_out);
     SILGPU_LAUNCH_CHECK("row_sum_k");
+    if (chunks > 1) {
+      row_sum_finish_k<<<static_cast<unsigned>(cdiv(rows, kBlock)), kBlock, 0, c->stream>>>(
+          partial, rows, chunks, d_out);
+      SILGPU_LAUNCH_CHECK("row_sum_finish_k");
+    }
     return SILGPU_OK;
   }
   SILGPU_REQUIRE(outer <= 65535, "silgpu_sum_axis_f32: outer %lld exceeds the grid",
                  (long long)outer);
-  int64_t tiles_x = cdiv(inner, kBlock);
-  int64_t tiles = tiles_x * outer;
+  const int64_t tiles_x = cdiv(inner, kBlock);
+  const int64_t tiles = tiles_x * outer;
   int64_t splits = 1;
   if (tiles < 1024) {
     splits = 2048 / tiles;
@@ -498,18 +493,21 @@ int silgpu_sum_axis_f32(const float *d_in, int64_t outer, int64_t axis_len, int6
     if (splits < 1) splits = 1;
     if (splits > 65535) splits = 65535;
     while (splits > 1 &&
-           tiles * splits * kBlock * int64_t(sizeof(double)) > int64_t(kPartialBytes))
+           outer * inner * splits * int64_t(sizeof(double)) > int64_t(kPartialBytes))
       splits /= 2;
-    if (tiles > kCounterCount) splits = 1;
   }
   int64_t per_split = cdiv(axis_len, splits);
   splits = cdiv(axis_len, per_split);
   dim3 grid(static_cast<unsigned>(tiles_x), static_cast<unsigned>(splits),
             static_cast<unsigned>(outer));
-  axis_sum_k<<<grid, kBlock, 0, c->stream>>>(d_in, axis_len, inner, per_split,
-                                             static_cast<double *>(c->partials), c->counters,
-                                             d_out);
+  axis_sum_k<<<grid, kBlock, 0, c->stream>>>(d_in, axis_len, inner, per_split, partial, d_out);
   SILGPU_LAUNCH_CHECK("axis_sum_k");
+  if (splits > 1) {
+    const int64_t count = outer * inner;
+    axis_sum_finish_k<<<static_cast<unsigned>(cdiv(count, kBlock)), kBlock, 0, c->stream>>>(
+        partial, count, splits, d_out);
+    SILGPU_LAUNCH_CHECK("axis_sum_finish_k");
+  }
   return SILGPU_OK;
 }
 
@@ -536,15 +534,18 @@ int silgpu_argmax_rows_f32(const float *d_in, int64_t rows, int64_t cols, int32_
     }
     return SILGPU_OK;
   }
-  bool vec = cols % 4 == 0 && aligned16(d_in);
-  int64_t chunks = pick_chunks(rows, cols, kCounterCount / rows);
-  if (chunks > 1 && rows * chunks * int64_t(sizeof(vi)) > int64_t(kPartialBytes)) chunks = 1;
-  int64_t chunk = cdiv(cdiv(cols, chunks), 4 * kBlock) * 4 * kBlock;
-  chunks = cdiv(cols, chunk);
+  const bool vec = cols % 4 == 0 && aligned16(d_in);
+  int64_t chunks;
+  const int64_t chunk = chunk_len(rows, cols, sizeof(vi), chunks);
+  vi *partial = static_cast<vi *>(c->partials);
   dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(rows));
-  argmax_k<<<grid, kBlock, 0, c->stream>>>(d_in, cols, chunk, vec,
-                                           static_cast<vi *>(c->partials), c->counters, d_out);
+  argmax_k<<<grid, kBlock, 0, c->stream>>>(d_in, cols, chunk, vec, partial, d_out);
   SILGPU_LAUNCH_CHECK("argmax_k");
+  if (chunks > 1) {
+    argmax_finish_k<<<static_cast<unsigned>(rows), kBlock, 0, c->stream>>>(partial, chunks,
+                                                                           d_out);
+    SILGPU_LAUNCH_CHECK("argmax_finish_k");
+  }
   return SILGPU_OK;
 }
 

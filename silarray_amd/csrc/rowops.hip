@@ -57,8 +57,10 @@ struct dsum_op {
 
 // Loads V float4 (VEC) or 4V scalars (!VEC) of row `row` owned by thread
 // `t` of an NT-thread group: element j of slot k is column
-// (k*NT + t)*4 + j.  Columns >= cols read as `pad`.
-template <int NT, int V, bool VEC>
+// (k*NT + t)*4 + j.  Columns >= cols read as `pad`.  STREAM: the data is read
+// once (input rows), so non-temporal loads keep it out of the caches;
+// gamma/beta are re-read by every row and use ordinary loads.
+template <int NT, int V, bool VEC, bool STREAM = true>
 __device__ __forceinline__ void load_row(const float *__restrict__ row, int64_t cols, int t,
                                          float pad, float (&x)[V][4]) {
 #pragma unroll
@@ -66,7 +68,16 @@ __device__ __forceinline__ void load_row(const float *__restrict__ row, int64_t 
     int64_t c = (int64_t(k) * NT + t) * 4;
     if constexpr (VEC) {
       if (c < cols) {
-        float4 v = reinterpret_cast<const float4 *>(row)[c / 4];
+        const float4 *q = reinterpret_cast<const float4 *>(row) + c / 4;
+        float4 v;
+        if constexpr (STREAM) {
+          v.x = __builtin_nontemporal_load(&q->x);
+          v.y = __builtin_nontemporal_load(&q->y);
+          v.z = __builtin_nontemporal_load(&q->z);
+          v.w = __builtin_nontemporal_load(&q->w);
+        } else {
+          v = *q;
+        }
         x[k][0] = v.x;
         x[k][1] = v.y;
         x[k][2] = v.z;
@@ -168,8 +179,8 @@ __global__ __launch_bounds__(256) void layer_norm_reg_k(const float *__restrict_
   const float var = static_cast<float>(ss / static_cast<double>(cols));
   const float inv_std = 1.0f / sqrtf(var + eps);
   float g[V][4], b[V][4];
-  load_row<NT, V, VEC>(gamma, cols, t, 0.0f, g);
-  load_row<NT, V, VEC>(beta, cols, t, 0.0f, b);
+  load_row<NT, V, VEC, false>(gamma, cols, t, 0.0f, g);
+  load_row<NT, V, VEC, false>(beta, cols, t, 0.0f, b);
 #pragma unroll
   for (int k = 0; k < V; ++k)
 #pragma unroll

@@ -47,9 +47,6 @@ int init_locked() {
   // Default priority on purpose: streams of mixed priority are avoided.
   SILGPU_HIP_CHECK(hipStreamCreateWithFlags(&g_ctx.stream, hipStreamNonBlocking));
   SILGPU_HIP_CHECK(hipMalloc(&g_ctx.partials, kPartialBytes));
-  SILGPU_HIP_CHECK(hipMalloc(reinterpret_cast<void **>(&g_ctx.counters),
-                             sizeof(unsigned int) * kCounterCount));
-  SILGPU_HIP_CHECK(hipMemset(g_ctx.counters, 0, sizeof(unsigned int) * kCounterCount));
   SILGPU_HIP_CHECK(hipDeviceSynchronize());
   g_ready = true;
   return SILGPU_OK;

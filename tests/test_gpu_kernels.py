@@ -187,8 +187,12 @@ def test_program_general_graph(native, oracle):
                                           b, x.size))
     s = oracle.binary_mod_f32(DIV, oracle.sigmoid(y.ravel()), [3.0], y.size)
     ref = oracle.binary_mod_f32(SUB, t, s, x.size).reshape(R, Cc)
-    assert np.max(ulp_diff(out, ref)[np.abs(ref) > 1e-6]) <= 4
-    assert np.max(np.abs(out - ref)) < 1e-6
+    # Every op but sigmoid is correctly rounded on both sides, and the GPU's
+    # expf may differ from glibc's by 1-2 ulp.  The final subtraction can
+    # cancel, so the bound is 4 ulp of the operands' magnitude, not of the
+    # result.
+    scale = (np.abs(t) + np.abs(s)).reshape(R, Cc)
+    assert np.all(np.abs(out - ref) <= 4 * np.finfo(np.float32).eps * scale + 1e-30)
 
 
 # ---- reductions ------------------------------------------------------------------
