@@ -232,6 +232,19 @@ def bench_affine_chain(nat, g, reps=20):
     return {"gbs": 8 * n / (ms / 1e3) / 1e9, "us": ms * 1e3, "bytes": 8 * n, "ops": 20}
 
 
+def bench_copy(nat, g, reps=20):
+    """Plain device copy of 256 MiB (hipMemcpyAsync D2D), the calibration
+    kernel for the FETCH_SIZE / WRITE_SIZE counters: it reads and writes
+    exactly 268,435,456 bytes per launch."""
+    n = 64 * 1024 * 1024
+    src = nat.DeviceBuffer.from_array(uniform(g, n))
+    dst = nat.DeviceBuffer(4 * n)
+    t = Timer(nat)
+    ms = t.ms_per_launch(lambda i: nat.call("silgpu_memcpy_d2d", nat.vp(dst), nat.vp(src), 4 * n),
+                         reps)
+    return {"gbs": 8 * n / (ms / 1e3) / 1e9, "us": ms * 1e3, "bytes": 8 * n}
+
+
 def cpu_baseline(seconds: float) -> dict:
     """cblas_sgemm (OpenBLAS) 2048^3 fp32 on this host's cores, repeated for
     about `seconds`; TFLOP/s of the same SGEMM shape family as the headline."""
@@ -329,6 +342,11 @@ def main():
                                            "us": round(r["us"], 2),
                                            "roofline": roofline("hbm", r["gbs"],
                                                                 load_traffic("affine_chain20_64M"))}
+    if only and "copy" in only:
+        r = bench_copy(nat, g)
+        log(f"copy {r}")
+        secondary["copy_256MiB"] = {"value": round(r["gbs"], 1), "unit": "GB/s",
+                                    "us": round(r["us"], 2)}
     if want("sgemm_sweep"):
         for s in (2048, 4096):
             r = bench_sgemm(nat, s, 10, 3, g)

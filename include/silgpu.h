@@ -254,6 +254,16 @@ int silgpu_sgemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
                  int64_t stride_c, int64_t batch, const float *d_bias,
                  int64_t bias_len, int epilogue);
 
+/* silgpu_sgemm with a forced kernel configuration, for tile sweeps.  No
+ * reference counterpart.  tile: 1 = 128x128, 2 = 64x64, 3 = 32x128,
+ * 4 = 128x64 (workgroup tile of C); splits: K splits (>= 1; batch must be 1
+ * for splits > 1).  Never routes to the GEMV kernels. */
+int silgpu_sgemm_tuned(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                       const float *d_A, int64_t lda, int64_t stride_a, const float *d_B,
+                       int64_t ldb, int64_t stride_b, float *d_C, int64_t ldc,
+                       int64_t stride_c, int64_t batch, const float *d_bias,
+                       int64_t bias_len, int epilogue, int tile, int splits);
+
 /* y[1 x N] = x[1 x K] * B[K x N] (B row-major, ldb >= N).  Replaces gpu::sgemv
  * (include/gpu.h:549-574).  silgpu_sgemm routes M == 1 here as well. */
 int silgpu_sgemv(const float *d_x, const float *d_B, int64_t ldb, float *d_y, int64_t N,

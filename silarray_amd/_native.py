@@ -104,6 +104,8 @@ _SIGS = {
     "silgpu_layer_norm_rows_f32": (_i, [_vp, _vp, _vp, _vp, _i64, _i64, _f]),
     "silgpu_sgemm": (_i, [_i, _i, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp,
                           _i64, _i64, _i64, _vp, _i64, _i]),
+    "silgpu_sgemm_tuned": (_i, [_i, _i, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
+                                _vp, _i64, _i64, _i64, _vp, _i64, _i, _i, _i]),
     "silgpu_sgemv": (_i, [_vp, _vp, _i64, _vp, _i64, _i64]),
     "silgpu_event_create": (_i, [C.POINTER(_vp)]),
     "silgpu_event_destroy": (_i, [_vp]),
@@ -292,6 +294,16 @@ def sgemm(ta, tb, M, N, K, A, lda, sA, B, ldb, sB, Cm, ldc, sC, batch=1, bias=No
           bias_len=0, epi=EPI_NONE):
     call("silgpu_sgemm", int(ta), int(tb), M, N, K, vp(A), lda, sA, vp(B), ldb, sB, vp(Cm),
          ldc, sC, batch, vp(bias) if bias is not None else _vp(None), bias_len, epi)
+
+
+TILE_128x128, TILE_64x64, TILE_32x128, TILE_128x64 = 1, 2, 3, 4
+
+
+def sgemm_tuned(ta, tb, M, N, K, A, lda, sA, B, ldb, sB, Cm, ldc, sC, batch=1, bias=None,
+                bias_len=0, epi=EPI_NONE, tile=TILE_128x128, splits=1):
+    call("silgpu_sgemm_tuned", int(ta), int(tb), M, N, K, vp(A), lda, sA, vp(B), ldb, sB,
+         vp(Cm), ldc, sC, batch, vp(bias) if bias is not None else _vp(None), bias_len, epi,
+         tile, splits)
 
 
 def sgemv(x, B, ldb, y, N, K):

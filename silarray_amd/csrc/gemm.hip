@@ -61,6 +61,11 @@ struct gemm_args {
   int M, N, K;
   int tiles_m, tiles_n;
   int epi;
+  // Split K: workgroup row blockIdx.y covers K range [y*klen, (y+1)*klen)
+  // (klen a multiple of BK).  With gridDim.y > 1 raw accumulators go to
+  // ws[y][M][N] and splitk_reduce_k applies the epilogue.
+  int klen;
+  float *ws;
 };
 
 template <int BM, int BN, int BK, int WM, int WN>
@@ -201,15 +206,17 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
       store_groups<BN, BK, NT, C::NB, C::LB, false>(S, t, gb);
   };
 
-  const int KT = (K + BK - 1) / BK;
+  const int kbeg = blockIdx.y * p.klen;
+  const int kend = min(K, kbeg + p.klen);
+  const int KT = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
   const int khalf = lane / 32;  // which k of the pair this lane supplies
   const int l32 = lane % 32;
   const int a_col = wm * C::TM * 32 + l32;
   const int b_col = wn * C::TN * 32 + l32;
 
   if (KT > 0) {
-    load_a(0);
-    load_b(0);
+    load_a(kbeg);
+    load_b(kbeg);
     store_a(0);
     store_b(0);
     __syncthreads();
@@ -218,8 +225,8 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
     const int cur = kt & 1;
     const bool more = kt + 1 < KT;
     if (more) {
-      load_a((kt + 1) * BK);
-      load_b((kt + 1) * BK);
+      load_a(kbeg + (kt + 1) * BK);
+      load_b(kbeg + (kt + 1) * BK);
     }
     const float *Sa = As + cur * C::kAStage + khalf * C::LA + a_col;
     const float *Sb = Bs + cur * C::kBStage + khalf * C::LB + b_col;
@@ -247,6 +254,23 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
   // C[row][col] with col = 32j + l%32 and row = 32i + 8*(r/4) + 4*(l/32) + r%4
   // (relative to the wave tile).
   const int epi = p.epi;
+  if (gridDim.y > 1) {
+    float *W = p.ws + int64_t(blockIdx.y) * M * N;
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) {
+      const int col = n0 + wn * C::TN * 32 + j * 32 + l32;
+      if (EDGE && col >= N) continue;
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm * C::TM * 32 + i * 32 + 8 * (r / 4) + 4 * khalf + (r % 4);
+          if (EDGE && row >= M) continue;
+          W[int64_t(row) * N + col] = acc[i][j][r];
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < C::TN; ++j) {
     const int col = n0 + wn * C::TN * 32 + j * 32 + l32;
@@ -451,7 +475,7 @@ __global__ __launch_bounds__(256) void epilogue_k(float *__restrict__ C, int64_t
 // ---- host dispatch ----------------------------------------------------------
 
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VEC, bool EDGE>
-int launch_cfg(const gemm_args &a, int64_t batch, hipStream_t s) {
+int launch_cfg(const gemm_args &a, int64_t batch, int splits, hipStream_t s) {
   using C = cfg<BM, BN, BK, WM, WN>;
   auto kern = sgemm_mfma_k<BM, BN, BK, WM, WN, TA, TB, VEC, EDGE>;
   static bool attr_done = false;
@@ -464,29 +488,177 @@ int launch_cfg(const gemm_args &a, int64_t batch, hipStream_t s) {
   gemm_args g = a;
   g.tiles_m = static_cast<int>(cdiv(a.M, BM));
   g.tiles_n = static_cast<int>(cdiv(a.N, BN));
-  dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), 1, static_cast<unsigned>(batch));
+  g.klen = static_cast<int>(cdiv(cdiv(a.K, splits), BK) * BK);
+  if (g.klen < BK) g.klen = BK;
+  splits = static_cast<int>(a.K > 0 ? cdiv(a.K, g.klen) : 1);
+  dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(splits),
+            static_cast<unsigned>(batch));
   kern<<<grid, C::kThreads, C::kLdsBytes, s>>>(g);
   SILGPU_LAUNCH_CHECK("sgemm_mfma_k");
-  return SILGPU_OK;
+  return splits;  // >= 1: the number of K splits actually launched
 }
 
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
-int launch_tb(const gemm_args &a, int64_t batch, bool vec, hipStream_t s) {
+int launch_tb(const gemm_args &a, int64_t batch, int splits, bool vec, hipStream_t s) {
+  // Every split's K range is a multiple of BK except possibly the last, and
+  // that one is too when K is.
   const bool edge = (a.M % BM) || (a.N % BN) || (a.K % BK);
   if (vec) {
-    return edge ? launch_cfg<BM, BN, BK, WM, WN, TA, TB, true, true>(a, batch, s)
-                : launch_cfg<BM, BN, BK, WM, WN, TA, TB, true, false>(a, batch, s);
+    return edge ? launch_cfg<BM, BN, BK, WM, WN, TA, TB, true, true>(a, batch, splits, s)
+                : launch_cfg<BM, BN, BK, WM, WN, TA, TB, true, false>(a, batch, splits, s);
   }
-  return launch_cfg<BM, BN, BK, WM, WN, TA, TB, false, true>(a, batch, s);
+  return launch_cfg<BM, BN, BK, WM, WN, TA, TB, false, true>(a, batch, splits, s);
 }
 
 template <int BM, int BN, int BK, int WM, int WN>
-int launch_tiles(const gemm_args &a, int64_t batch, bool ta, bool tb, bool vec,
+int launch_tiles(const gemm_args &a, int64_t batch, int splits, bool ta, bool tb, bool vec,
                  hipStream_t s) {
-  if (!ta && !tb) return launch_tb<BM, BN, BK, WM, WN, false, false>(a, batch, vec, s);
-  if (!ta && tb) return launch_tb<BM, BN, BK, WM, WN, false, true>(a, batch, vec, s);
-  if (ta && !tb) return launch_tb<BM, BN, BK, WM, WN, true, false>(a, batch, vec, s);
-  return launch_tb<BM, BN, BK, WM, WN, true, true>(a, batch, vec, s);
+  if (!ta && !tb) return launch_tb<BM, BN, BK, WM, WN, false, false>(a, batch, splits, vec, s);
+  if (!ta && tb) return launch_tb<BM, BN, BK, WM, WN, false, true>(a, batch, splits, vec, s);
+  if (ta && !tb) return launch_tb<BM, BN, BK, WM, WN, true, false>(a, batch, splits, vec, s);
+  return launch_tb<BM, BN, BK, WM, WN, true, true>(a, batch, splits, vec, s);
+}
+
+// Sums the K-split partials ws[s][M][N] in split order and applies the
+// epilogue: C[m*ldc + n] = epi(sum_s ws[s][m][n]).  One element (or one
+// float4 when rows allow) per thread.
+template <bool VEC>
+__global__ __launch_bounds__(256) void splitk_reduce_k(const float *__restrict__ ws, int splits,
+                                                       int64_t M, int64_t N,
+                                                       float *__restrict__ C, int64_t ldc,
+                                                       const float *__restrict__ bias,
+                                                       int64_t bias_len, int epi) {
+  const int64_t per = VEC ? 4 : 1;
+  const int64_t total = M * N / per;
+  const int64_t plane = M * N;
+  for (int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x; t < total;
+       t += int64_t(gridDim.x) * 256) {
+    const int64_t e = t * per;
+    const int64_t m = e / N, n = e % N;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < splits; ++sp) {
+      if constexpr (VEC) {
+        float4 q = *reinterpret_cast<const float4 *>(ws + sp * plane + e);
+        v[0] += q.x;
+        v[1] += q.y;
+        v[2] += q.z;
+        v[3] += q.w;
+      } else {
+        v[0] += ws[sp * plane + e];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < (VEC ? 4 : 1); ++j) {
+      float x = v[j];
+      if (epi == SILGPU_EPI_BIAS || epi == SILGPU_EPI_BIAS_SIGMOID || epi == SILGPU_EPI_BIAS_RELU)
+        x += bias[(n + j) % bias_len];
+      if (epi == SILGPU_EPI_BIAS_SIGMOID) x = sigmoidf_dev(x);
+      else if (epi == SILGPU_EPI_RELU || epi == SILGPU_EPI_BIAS_RELU) x = fmaxf(x, 0.0f);
+      v[j] = x;
+    }
+    if constexpr (VEC)
+      *reinterpret_cast<float4 *>(C + m * ldc + n) = make_float4(v[0], v[1], v[2], v[3]);
+    else
+      C[m * ldc + n] = v[0];
+  }
+}
+
+// Tile configurations (BM x BN, waves WM x WN; BK = 16, 32 for 32x128).
+enum tile_cfg { TILE_AUTO = 0, TILE_128x128 = 1, TILE_64x64 = 2, TILE_32x128 = 3, TILE_128x64 = 4 };
+
+struct plan {
+  int tile;
+  int splits;
+};
+
+// Shape heuristic: a cost model calibrated on MI355X sweeps of the 8192^3,
+// 4096^3, 2048^3, linear_sigmoid 256x4096x4096 and transformer-projection
+// shapes.  For each candidate (tile, K splits):
+//   time = flops / (peak * eff[tile] * fill * klen / (klen + k0[tile]))
+//          + splits > 1 ? (splits * M * N * 8 bytes) / 5 TB/s + 4 us : 0
+// eff is the tile's sustained fraction of fp32 MFMA peak on large shapes,
+// fill = min(1, workgroups / full[tile]) (two waves per SIMD are needed to
+// hide load and barrier latency; the 64x64 tile, one 32x32 accumulator per
+// wave, needs twice the workgroups), use = the share of the padded tile area
+// that lies inside C, k0 the per-workgroup fixed cost expressed in units of
+// K, and the split term the partial tiles' HBM round trip plus the reduce
+// launch.  M <= 32 uses the 32x128 tile with enough K splits for
+// ~256 workgroups.
+plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch) {
+  auto tiles = [&](int bm, int bn) { return cdiv(M, bm) * cdiv(N, bn) * batch; };
+  if (M <= 32) {
+    plan p{TILE_32x128, 1};
+    if (batch == 1) {
+      int64_t sp = cdiv(256, tiles(32, 128));
+      if (sp > K / 256) sp = K / 256;
+      if (sp > 64) sp = 64;
+      if (sp > 1) p.splits = static_cast<int>(sp);
+    }
+    return p;
+  }
+  struct cand {
+    int tile, bm, bn;
+    double eff, k0, full;
+  };
+  static const cand cands[] = {{TILE_128x128, 128, 128, 0.79, 256.0, 512.0},
+                               {TILE_128x64, 128, 64, 0.79, 400.0, 512.0},
+                               {TILE_64x64, 64, 64, 0.70, 128.0, 1024.0}};
+  const double flops = 2.0 * double(M) * double(N) * double(K) * double(batch);
+  plan best{TILE_128x128, 1};
+  double best_t = 1e30;
+  for (const cand &cd : cands) {
+    for (int sp : {1, 2, 4, 8}) {
+      if (sp > 1 && (batch != 1 || K / sp < 384)) continue;
+      const double wg = double(tiles(cd.bm, cd.bn)) * sp;
+      const double klen = double(cdiv(K, sp));
+      const double fill = wg >= cd.full ? 1.0 : wg / cd.full;
+      const double use = double(M) * double(N) /
+                         (double(cdiv(M, cd.bm) * cd.bm) * double(cdiv(N, cd.bn) * cd.bn));
+      const double rate = 157.3e12 * cd.eff * fill * use * (klen / (klen + cd.k0));
+      double t = flops / rate;
+      if (sp > 1) t += double(sp) * double(M) * double(N) * 8.0 / 5.0e12 + 4.0e-6;
+      if (t < best_t * 0.999) {
+        best_t = t;
+        best = plan{cd.tile, sp};
+      }
+    }
+  }
+  return best;
+}
+
+int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, bool vec,
+              context *c) {
+  gemm_args a = a0;
+  int splits = pl.splits;
+  if (batch != 1 || a.K == 0) splits = 1;
+  if (splits > 1) {
+    size_t need = size_t(splits) * size_t(a.M) * size_t(a.N) * sizeof(float);
+    int rc = ensure_workspace(c, need);
+    if (rc != SILGPU_OK) return rc;
+    a.ws = static_cast<float *>(c->workspace);
+  }
+  int launched;
+  switch (pl.tile) {
+    case TILE_64x64: launched = launch_tiles<64, 64, 16, 2, 2>(a, batch, splits, ta, tb, vec, c->stream); break;
+    case TILE_32x128: launched = launch_tiles<32, 128, 32, 1, 4>(a, batch, splits, ta, tb, vec, c->stream); break;
+    case TILE_128x64: launched = launch_tiles<128, 64, 16, 2, 2>(a, batch, splits, ta, tb, vec, c->stream); break;
+    default: launched = launch_tiles<128, 128, 16, 2, 2>(a, batch, splits, ta, tb, vec, c->stream); break;
+  }
+  if (launched < 0) return launched;
+  if (launched > 1) {
+    const bool v4 = a.N % 4 == 0 && a.ldc % 4 == 0 && aligned16(a.C);
+    const int64_t work = a.M * int64_t(a.N) / (v4 ? 4 : 1);
+    int64_t g = cdiv(work, 256);
+    if (g > 65536) g = 65536;
+    if (v4)
+      splitk_reduce_k<true><<<static_cast<unsigned>(g), 256, 0, c->stream>>>(
+          a.ws, launched, a.M, a.N, a.C, a.ldc, a.bias, a.bias_len, a.epi);
+    else
+      splitk_reduce_k<false><<<static_cast<unsigned>(g), 256, 0, c->stream>>>(
+          a.ws, launched, a.M, a.N, a.C, a.ldc, a.bias, a.bias_len, a.epi);
+    SILGPU_LAUNCH_CHECK("splitk_reduce_k");
+  }
+  return SILGPU_OK;
 }
 
 int launch_gemv_n(const float *x, const float *Bm, int64_t ldb, float *y, int64_t N,
@@ -562,10 +734,16 @@ int silgpu_sgemv(const float *d_x, const float *d_B, int64_t ldb, float *d_y, in
   return launch_gemv_n(d_x, d_B, ldb, d_y, N, K, c);
 }
 
-int silgpu_sgemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const float *d_A,
-                 int64_t lda, int64_t stride_a, const float *d_B, int64_t ldb,
-                 int64_t stride_b, float *d_C, int64_t ldc, int64_t stride_c, int64_t batch,
-                 const float *d_bias, int64_t bias_len, int epilogue) {
+}  // extern "C"
+
+namespace {
+
+// Shared body of silgpu_sgemm / silgpu_sgemm_tuned.  `forced` (tuning only)
+// skips the vector-product routing and the shape heuristic.
+int sgemm_impl(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const float *d_A,
+               int64_t lda, int64_t stride_a, const float *d_B, int64_t ldb, int64_t stride_b,
+               float *d_C, int64_t ldc, int64_t stride_c, int64_t batch, const float *d_bias,
+               int64_t bias_len, int epilogue, const plan *forced) {
   SILGPU_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "silgpu_sgemm: negative extent");
   SILGPU_REQUIRE(M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX,
                  "silgpu_sgemm: extent exceeds int32");
@@ -587,7 +765,7 @@ int silgpu_sgemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, cons
   SILGPU_CTX(c);
 
   // Vector products (the reference routes M == 1 to sgemv, include/array.h:2675-2676).
-  if (batch == 1 && K > 0 && (M == 1 || N == 1)) {
+  if (!forced && batch == 1 && K > 0 && (M == 1 || N == 1)) {
     int rc;
     if (M == 1 && !tb && !ta) {
       // y = x * B with x = A[0..K) contiguous and B [K][N].
@@ -626,10 +804,34 @@ int silgpu_sgemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, cons
   const bool vec = aligned16(d_A) && aligned16(d_B) && lda % 4 == 0 && ldb % 4 == 0 &&
                    (ta ? M % 4 == 0 : K % 4 == 0) && (tb ? K % 4 == 0 : N % 4 == 0) &&
                    (batch == 1 || (stride_a % 4 == 0 && stride_b % 4 == 0));
-  const int64_t tiles128 = cdiv(M, 128) * cdiv(N, 128) * batch;
-  if (tiles128 >= 1024)
-    return launch_tiles<128, 128, 16, 2, 2>(a, batch, ta, tb, vec, c->stream);
-  return launch_tiles<64, 64, 16, 2, 2>(a, batch, ta, tb, vec, c->stream);
+  return run_sgemm(a, batch, forced ? *forced : choose_plan(M, N, K, batch), ta, tb, vec, c);
 }
+
+}  // namespace
+
+extern "C" {
+
+int silgpu_sgemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const float *d_A,
+                 int64_t lda, int64_t stride_a, const float *d_B, int64_t ldb,
+                 int64_t stride_b, float *d_C, int64_t ldc, int64_t stride_c, int64_t batch,
+                 const float *d_bias, int64_t bias_len, int epilogue) {
+  return sgemm_impl(trans_a, trans_b, M, N, K, d_A, lda, stride_a, d_B, ldb, stride_b, d_C, ldc,
+                    stride_c, batch, d_bias, bias_len, epilogue, nullptr);
+}
+
+int silgpu_sgemm_tuned(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                       const float *d_A, int64_t lda, int64_t stride_a, const float *d_B,
+                       int64_t ldb, int64_t stride_b, float *d_C, int64_t ldc, int64_t stride_c,
+                       int64_t batch, const float *d_bias, int64_t bias_len, int epilogue,
+                       int tile, int splits) {
+  SILGPU_REQUIRE(tile >= TILE_128x128 && tile <= TILE_128x64,
+                 "silgpu_sgemm_tuned: unknown tile configuration %d", tile);
+  SILGPU_REQUIRE(splits >= 1 && splits <= 256, "silgpu_sgemm_tuned: splits %d not in [1, 256]",
+                 splits);
+  plan pl{tile, splits};
+  return sgemm_impl(trans_a, trans_b, M, N, K, d_A, lda, stride_a, d_B, ldb, stride_b, d_C, ldc,
+                    stride_c, batch, d_bias, bias_len, epilogue, &pl);
+}
+
 
 }  // extern "C"

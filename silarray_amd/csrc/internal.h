@@ -32,9 +32,16 @@ struct context {
   // second.  Launches on the one stream run in order, so every call may
   // reuse the whole area.
   void *partials = nullptr;  // kPartialBytes
+  // GEMM split-K workspace: grown to the largest request seen, never shrunk.
+  void *workspace = nullptr;
+  size_t workspace_bytes = 0;
 };
 
 constexpr size_t kPartialBytes = size_t(16) << 20;  // 16 MiB
+
+// Makes c->workspace hold at least `bytes` (synchronises the stream before
+// replacing a smaller block).
+int ensure_workspace(context *c, size_t bytes);
 
 // Returns the initialised context, or nullptr after recording an error.
 context *ctx();

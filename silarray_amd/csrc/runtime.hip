@@ -90,6 +90,21 @@ int set_error(int code, const char *fmt, ...) {
 
 void clear_error() { g_err[0] = '\0'; }
 
+int ensure_workspace(context *c, size_t bytes) {
+  if (bytes <= c->workspace_bytes) return SILGPU_OK;
+  size_t grow = (bytes + (size_t(64) << 20) - 1) & ~((size_t(64) << 20) - 1);  // 64 MiB steps
+  SILGPU_HIP_CHECK(hipStreamSynchronize(c->stream));
+  if (c->workspace) SILGPU_HIP_CHECK(hipFree(c->workspace));
+  c->workspace = nullptr;
+  c->workspace_bytes = 0;
+  hipError_t e = hipMalloc(&c->workspace, grow);
+  if (e != hipSuccess)
+    return set_error(SILGPU_ERR_NOMEM, "GEMM workspace of %zu bytes: %s", grow,
+                     hipGetErrorString(e));
+  c->workspace_bytes = grow;
+  return SILGPU_OK;
+}
+
 context *ctx() {
   if (g_ready) return &g_ctx;
   std::lock_guard<std::mutex> lk(g_init_mu);

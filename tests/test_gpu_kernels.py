@@ -520,3 +520,31 @@ def test_small_batch_config(native, oracle):
     Cg, C64, Cabs = _gemm_case(native, oracle, 32, 768, 4096, dist="normal")
     ok, nw, el = gemm_tolerance_ok(Cg, C64, Cabs, 4096)
     assert ok, (nw, el)
+
+
+@pytest.mark.parametrize("tile", [1, 2, 3, 4])
+@pytest.mark.parametrize("splits", [1, 3, 8])
+@pytest.mark.parametrize("M,N,K,ta,tb,epi", [(33, 70, 200, 0, 0, 0), (128, 256, 512, 0, 0, 2),
+                                             (100, 130, 1000, 1, 0, 1), (64, 96, 777, 0, 1, 4)])
+def test_sgemm_tuned_configs(native, oracle, tile, splits, M, N, K, ta, tb, epi):
+    """Every forced tile configuration and K split against the oracle."""
+    announce(f"sgemm_tuned tile={tile} splits={splits} {M}x{N}x{K} ta={ta} tb={tb} epi={epi}")
+    g = rng(1700 + M + N + K)
+    A = g.uniform(-1, 1, (K, M) if ta else (M, K)).astype(np.float32)
+    B = g.uniform(-1, 1, (N, K) if tb else (K, N)).astype(np.float32)
+    bias_len = N if epi in (1, 2, 4) else 0
+    bias = g.normal(0, 1, max(bias_len, 1)).astype(np.float32)
+    dA, dB, dC = up(native, A), up(native, B), empty(native, M * N)
+    dbias = up(native, bias) if bias_len else None
+    native.sgemm_tuned(ta, tb, M, N, K, dA, A.shape[1], 0, dB, B.shape[1], 0, dC, N, 0, 1,
+                       dbias, bias_len, epi, tile=tile, splits=splits)
+    Cg = down(native, dC, (M, N))
+    C64, Cabs = oracle.sgemm_f64(A, B, ta=ta, tb=tb, with_abs=True)
+    if bias_len:
+        C64, Cabs = C64 + bias, Cabs + np.abs(bias)
+    if epi == 2:
+        C64, Cabs = 1 / (1 + np.exp(-C64)), Cabs / 4 + 1e-7
+    if epi in (3, 4):
+        C64 = np.maximum(C64, 0)
+    ok, nw, el = gemm_tolerance_ok(Cg, C64, Cabs, K)
+    assert ok, (nw, el)
