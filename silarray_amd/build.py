@@ -74,5 +74,22 @@ def build_library(jobs: int = 5) -> Path:
     return LIB
 
 
+CXX = os.environ.get("SIL_CXX", "/opt/rocm/llvm/bin/clang++")
+CPP_TESTS = ROOT / "tests" / "cpp"
+
+
+def build_cpp_tests() -> Path:
+    """Compiles the C++ front-end tests (tests/cpp/test_array.cpp) against the
+    headers in silarray_amd/include, linked to the in-tree libsilgpu.so."""
+    out = CPP_TESTS / "test_array"
+    tmp = out.with_suffix(".tmp")
+    _run([CXX, "-std=c++23", "-O2", "-ffp-contract=off", "-Wall", "-Wno-unused-function",
+          f"-I{PKG / 'include'}", str(CPP_TESTS / "test_array.cpp"), "-o", str(tmp),
+          f"-L{PKG}", "-lsilgpu", "-Wl,-rpath,$ORIGIN/../../silarray_amd"])
+    os.replace(tmp, out)
+    return out
+
+
 if __name__ == "__main__":
     print(build_library())
+    print(build_cpp_tests())

@@ -1,0 +1,1710 @@
+#pragma once
+// sil::array — the reference's C++23 numerical-array front end
+// (include/array.h) over the MI355X backend.  The public API follows the
+// reference: constructors, views, lazy float arithmetic, dot/linear/
+// linear_sigmoid/softmax/layer_norm/sum/min/max/argmax, and sil::eval().
+// The implementation is this build's own:
+//   * float arrays build a lazy graph (detail::node); evaluation lowers it
+//     (detail::evaluate): maximal single-consumer elementwise subgraphs become
+//     one fused program launch (one HBM pass for a chain of scalar ops, with
+//     the reference's own per-node rounding), everything else one library
+//     call per node;
+//   * storage is device-resident HBM with a host mirror made current only
+//     when the host reads or writes elements (storage.h);
+//   * int and bool arrays are handled as in the reference: int elementwise
+//     arithmetic on the GPU, the rest on the host.
+
+#include <algorithm>
+#include <array>
+#include <cmath>
+#include <concepts>
+#include <cstring>
+#include <functional>
+#include <initializer_list>
+#include <iostream>
+#include <iterator>
+#include <limits>
+#include <memory>
+#include <numeric>
+#include <random>
+#include <ranges>
+#include <span>
+#include <sstream>
+#include <stdexcept>
+#include <string>
+#include <tuple>
+#include <unordered_map>
+#include <unordered_set>
+#include <utility>
+#include <vector>
+
+#include "gpu.h"
+
+namespace sil {
+
+template <typename T>
+concept arithmetic = std::is_arithmetic_v<T>;
+
+using shape_type = std::vector<size_t>;
+using strides_type = shape_type;
+
+// Row-major contiguous strides (a scalar has the single stride {1}).
+inline strides_type contiguous_strides(const shape_type &shape) {
+  if (shape.empty()) return {1};
+  strides_type st(shape.size());
+  st.back() = 1;
+  for (size_t i = shape.size() - 1; i-- > 0;) st[i] = st[i + 1] * shape[i + 1];
+  return st;
+}
+
+// numpy-style broadcast of two shapes, aligned at the trailing axis
+// (include/array.h:38-59).
+inline shape_type broadcast_shape(const shape_type &ls, const shape_type &rs) {
+  if (ls == rs) return ls;
+  if (ls.empty()) return rs;
+  if (rs.empty()) return ls;
+  const size_t n = std::max(ls.size(), rs.size());
+  shape_type out(n);
+  for (size_t i = 0; i < n; i++) {
+    const size_t a = i + ls.size() >= n ? ls[i + ls.size() - n] : 1;
+    const size_t b = i + rs.size() >= n ? rs[i + rs.size() - n] : 1;
+    if (a != b && a != 1 && b != 1) throw std::runtime_error("array: invalid operation.");
+    out[i] = std::max(a, b);
+  }
+  return out;
+}
+
+inline size_t shape_count(const shape_type &s) {
+  size_t n = 1;
+  for (auto d : s) n *= d;
+  return n;
+}
+
+//------------------------------------------------------------------------------
+// Lazy graph
+//------------------------------------------------------------------------------
+
+namespace detail {
+
+enum class op : uint8_t {
+  leaf,
+  add, sub, mul, div, pow,           // binary elementwise
+  sigmoid, relu, sigmoid_backward,   // unary elementwise (+ dout)
+  softmax, layer_norm,               // row ops
+  dot, batched_dot, linear, linear_sigmoid,
+  sum_axis,
+};
+
+inline bool is_elementwise(op o) { return o >= op::add && o <= op::sigmoid_backward; }
+inline bool is_binary(op o) { return o >= op::add && o <= op::pow; }
+
+struct node {
+  op operation = op::leaf;
+  std::array<std::shared_ptr<node>, 3> inputs{};
+  uint8_t num_inputs = 0;
+
+  storage data;  // valid once evaluated
+  shape_type shape;
+  strides_type strides;
+  bool evaluated = false;
+
+  float eps = 0.0f;   // layer_norm
+  size_t axis = 0;    // sum_axis
+
+  static std::shared_ptr<node> leaf(const storage &s, const shape_type &sh, const strides_type &st) {
+    auto n = std::make_shared<node>();
+    n->data = s;
+    n->shape = sh;
+    n->strides = st;
+    n->evaluated = true;
+    return n;
+  }
+
+  static std::shared_ptr<node> make(op o, std::initializer_list<std::shared_ptr<node>> ins,
+                                    const shape_type &sh) {
+    auto n = std::make_shared<node>();
+    n->operation = o;
+    for (auto &i : ins) n->inputs[n->num_inputs++] = i;
+    n->shape = sh;
+    n->strides = contiguous_strides(sh);
+    return n;
+  }
+};
+
+inline void evaluate(const std::vector<node *> &roots);
+
+}  // namespace detail
+
+using lazy_node = detail::node;
+
+//------------------------------------------------------------------------------
+// Nested initializer lists (array{{1,2},{3,4}})
+//------------------------------------------------------------------------------
+
+template <value_type T, size_t I>
+struct nested_initializer_list_ {
+  using type = std::initializer_list<typename nested_initializer_list_<T, I - 1>::type>;
+};
+template <value_type T>
+struct nested_initializer_list_<T, 0> {
+  using type = T;
+};
+template <value_type T, size_t I>
+using nested_initializer_list = typename nested_initializer_list_<T, I>::type;
+
+namespace detail {
+
+template <typename L>
+void nested_shape(const L &l, shape_type &s, size_t depth) {
+  if constexpr (requires { l.begin(); l.size(); }) {
+    if (s.size() <= depth) s.push_back(l.size());
+    if (l.size() > 0) nested_shape(*l.begin(), s, depth + 1);
+  }
+}
+
+template <typename L>
+size_t nested_count(const L &l) {
+  if constexpr (requires { l.begin(); l.size(); }) {
+    size_t n = 0;
+    for (const auto &x : l) n += nested_count(x);
+    return n;
+  } else {
+    return 1;
+  }
+}
+
+template <typename T, typename L>
+void nested_copy(T *&dst, const L &l) {
+  if constexpr (requires { l.begin(); l.size(); }) {
+    for (const auto &x : l) nested_copy(dst, x);
+  } else {
+    *dst++ = static_cast<T>(l);
+  }
+}
+
+}  // namespace detail
+
+//------------------------------------------------------------------------------
+
+template <value_type T>
+class array;
+
+template <value_type T, bool IsConst>
+class element_iterator_;
+template <value_type T, bool IsConst>
+class row_iterator_;
+
+template <value_type T>
+class array {
+  template <value_type U>
+  friend class array;
+
+ public:
+  using value_t = T;
+
+  array() = default;
+  array(const array &) = default;
+  array(array &&) = default;
+  array &operator=(const array &) = default;
+  array &operator=(array &&) = default;
+
+  array(const shape_type &shape, T val) {
+    reshape_raw_(shape);
+    allocate_();
+    constants(val);
+  }
+  template <std::input_iterator It>
+  array(const shape_type &shape, It it) {
+    reshape_raw_(shape);
+    allocate_();
+    set(it);
+  }
+  template <std::ranges::input_range R>
+    requires(!std::is_same_v<std::remove_cvref_t<R>, array>)
+  array(const shape_type &shape, R &&r) {
+    reshape_raw_(shape);
+    allocate_();
+    set(std::ranges::begin(r));
+  }
+  template <std::ranges::input_range R>
+    requires(!std::is_same_v<std::remove_cvref_t<R>, array> &&
+             !std::is_same_v<std::remove_cvref_t<R>, shape_type>)
+  explicit array(R &&r) {
+    std::vector<T> tmp;
+    for (auto &&x : r) tmp.push_back(static_cast<T>(x));
+    reshape_raw_({tmp.size()});
+    allocate_();
+    set(tmp.begin());
+  }
+  array(T val) : array(shape_type{}, val) {}
+
+  array(nested_initializer_list<T, 1> l) { init_list_(l); }
+  array(nested_initializer_list<T, 2> l) { init_list_(l); }
+  array(nested_initializer_list<T, 3> l) { init_list_(l); }
+  array(nested_initializer_list<T, 4> l) { init_list_(l); }
+
+  //----------------------------------------------------------------------------
+
+  template <value_type U = T>
+  array<U> clone() const {
+    array<U> tmp(shape_, U{});
+    for (size_t i = 0; i < element_count(); i++) tmp.at(i) = static_cast<U>(at(i));
+    return tmp;
+  }
+
+  void eval() const { ensure_evaluated_(); }
+  std::shared_ptr<lazy_node> lazy_node_ptr() const { return node_; }
+
+  //----------------------------------------------------------------------------
+
+  array<bool> operator==(const array &rhs) const { return compare_(rhs, std::equal_to<>{}); }
+  array<bool> operator!=(const array &rhs) const { return compare_(rhs, std::not_equal_to<>{}); }
+  array<bool> operator>(const array &rhs) const { return compare_(rhs, std::greater<>{}); }
+  array<bool> operator<(const array &rhs) const { return compare_(rhs, std::less<>{}); }
+  array<bool> operator>=(const array &rhs) const { return compare_(rhs, std::greater_equal<>{}); }
+  array<bool> operator<=(const array &rhs) const { return compare_(rhs, std::less_equal<>{}); }
+
+  //----------------------------------------------------------------------------
+
+  size_t buffer_element_count() const {
+    ensure_evaluated_();
+    return storage_.len;
+  }
+  size_t buffer_bytes() const { return buffer_element_count() * sizeof(T); }
+
+  // Host pointer to the first element of this array's window; waits for the
+  // GPU when the data is still being computed (include/array.h:951-958).
+  T *buffer_data() {
+    ensure_evaluated_();
+    return storage_.template host_out<T>();
+  }
+  const T *buffer_data() const {
+    ensure_evaluated_();
+    return storage_.template host_in<T>();
+  }
+  std::span<T> buffer_span() { return std::span<T>(buffer_data(), buffer_element_count()); }
+  std::span<const T> buffer_span() const {
+    return std::span<const T>(buffer_data(), buffer_element_count());
+  }
+
+  //----------------------------------------------------------------------------
+
+  size_t element_count() const { return shape_count(shape_); }
+  size_t length() const {
+    if (shape_.empty()) throw std::runtime_error("array: cannot call with a scalar value.");
+    return shape_[0];
+  }
+  size_t dimension() const { return shape_.size(); }
+  const shape_type &shape() const { return shape_; }
+  const strides_type &strides() const { return strides_; }
+
+  void reshape(const shape_type &shape) {
+    ensure_evaluated_();
+    if (storage_ && shape_count(shape) != element_count() && storage_.len < shape_count(shape))
+      throw std::runtime_error("array: invalid shape for reshape.");
+    if (storage_ && !is_contiguous_()) *this = materialize_();
+    reshape_raw_(shape);
+  }
+
+  // Zero-copy broadcast view to `target_shape` (include/array.h:1008-1049).
+  array broadcast(const shape_type &target_shape) const {
+    ensure_evaluated_();
+    if (target_shape.size() < dimension())
+      throw std::runtime_error("array: invalid shape for broadcast.");
+    const size_t diff = target_shape.size() - dimension();
+    for (size_t i = 0; i < dimension(); i++)
+      if (shape_[i] != target_shape[i + diff] && shape_[i] != 1)
+        throw std::runtime_error("array: invalid shape for broadcast.");
+    if (target_shape == shape_) return *this;
+    array tmp = *this;
+    tmp.node_.reset();
+    tmp.shape_ = target_shape;
+    tmp.strides_.assign(target_shape.size(), 0);
+    for (size_t i = diff; i < target_shape.size(); i++) {
+      const size_t s = i - diff;
+      tmp.strides_[i] = (shape_[s] == 1 && target_shape[i] != 1) ? 0 : strides_[s];
+    }
+    return tmp;
+  }
+
+  // 1-D -> {1, n}; {1, n} -> {n}; 2-D: zero-copy stride swap; 3-D: reversed
+  // axes, copied (include/array.h:1051-1099).
+  array transpose() const {
+    ensure_evaluated_();
+    if (dimension() == 1) {
+      array tmp = *this;
+      tmp.node_.reset();
+      tmp.shape_ = {1, element_count()};
+      tmp.strides_ = {element_count(), 1};
+      if (!is_contiguous_()) return materialize_().transpose();
+      return tmp;
+    }
+    if (dimension() == 2) {
+      if (shape_[0] == 1 && is_contiguous_()) {
+        array tmp = *this;
+        tmp.node_.reset();
+        tmp.shape_ = {shape_[1]};
+        tmp.strides_ = {1};
+        return tmp;
+      }
+      array tmp = *this;
+      tmp.node_.reset();
+      tmp.shape_ = {shape_[1], shape_[0]};
+      tmp.strides_ = {strides_[1], strides_[0]};
+      return tmp;
+    }
+    if (dimension() == 3) {
+      auto shape = shape_;
+      std::ranges::reverse(shape);
+      auto tmp = make_uninit_(shape);
+      T *out = tmp.storage_.template host_out<T>();
+      const auto st = contiguous_strides(shape);
+      for (size_t z = 0; z < shape_[0]; z++)
+        for (size_t y = 0; y < shape_[1]; y++)
+          for (size_t x = 0; x < shape_[2]; x++)
+            out[x * st[0] + y * st[1] + z * st[2]] = (*this)[z, y, x];
+      return tmp;
+    }
+    throw std::runtime_error("array: can't do `transpose` operation.");
+  }
+
+  //----------------------------------------------------------------------------
+
+  T &at() { return *buffer_data(); }
+  const T &at() const { return *buffer_data(); }
+  T &at(size_t i) {
+    bounds_check_(i);
+    return buffer_data()[index_of_(i)];
+  }
+  const T &at(size_t i) const {
+    bounds_check_(i);
+    return buffer_data()[index_of_(i)];
+  }
+  T &operator[](size_t x, size_t y) {
+    bounds_check_(x, y);
+    return buffer_data()[strides_[0] * x + strides_[1] * y];
+  }
+  const T &operator[](size_t x, size_t y) const {
+    bounds_check_(x, y);
+    return buffer_data()[strides_[0] * x + strides_[1] * y];
+  }
+  T &operator[](size_t x, size_t y, size_t z) {
+    bounds_check_(x, y, z);
+    return buffer_data()[strides_[0] * x + strides_[1] * y + strides_[2] * z];
+  }
+  const T &operator[](size_t x, size_t y, size_t z) const {
+    bounds_check_(x, y, z);
+    return buffer_data()[strides_[0] * x + strides_[1] * y + strides_[2] * z];
+  }
+  T &at(const std::vector<size_t> &position) { return buffer_data()[offset_of_(position)]; }
+  const T &at(const std::vector<size_t> &position) const {
+    return buffer_data()[offset_of_(position)];
+  }
+
+  template <size_t I>
+  auto take() const {
+    if constexpr (I == 0) return std::tuple<>();
+    else return std::tuple_cat(take<I - 1>(), std::tuple<T>(at(I - 1)));
+  }
+
+  //----------------------------------------------------------------------------
+
+  // Zero-copy view of row `row` (include/array.h:1157-1175).
+  array operator[](size_t row) const {
+    if (dimension() == 0 || row >= shape_[0])
+      throw std::runtime_error("array: row is out of bounds.");
+    ensure_evaluated_();
+    array tmp(*this);
+    tmp.node_.reset();
+    tmp.shape_.erase(tmp.shape_.begin());
+    tmp.strides_.erase(tmp.strides_.begin());
+    if (tmp.shape_.empty()) tmp.strides_ = {1};
+    tmp.storage_.off = storage_.off + strides_[0] * row;
+    tmp.storage_.len = tmp.shape_.empty() ? 1 : strides_[0];
+    return tmp;
+  }
+
+  // Zero-copy view of rows [start, start + count) (include/array.h:1177-1187).
+  array slice(size_t start, size_t count) const {
+    ensure_evaluated_();
+    if (dimension() == 0 || start + count > shape_[0])
+      throw std::runtime_error("array: slice is out of bounds.");
+    array tmp(*this);
+    tmp.node_.reset();
+    tmp.shape_[0] = count;
+    tmp.storage_.off = storage_.off + strides_[0] * start;
+    tmp.storage_.len = count * strides_[0];
+    return tmp;
+  }
+
+  //----------------------------------------------------------------------------
+
+  auto element_begin() { return element_iterator_<T, false>(this, 0); }
+  auto element_end() { return element_iterator_<T, false>(this, element_count()); }
+  auto element_cbegin() const { return element_iterator_<T, true>(this, 0); }
+  auto element_cend() const { return element_iterator_<T, true>(this, element_count()); }
+
+  auto elements() { return std::ranges::subrange(element_begin(), element_end()); }
+  auto elements() const { return std::ranges::subrange(element_cbegin(), element_cend()); }
+
+  auto begin() { return row_iterator_<T, false>(this, 0); }
+  auto end() { return row_iterator_<T, false>(this, shape_.empty() ? 0 : shape_[0]); }
+  auto begin() const { return row_iterator_<T, true>(this, 0); }
+  auto end() const { return row_iterator_<T, true>(this, shape_.empty() ? 0 : shape_[0]); }
+  auto cbegin() const { return begin(); }
+  auto cend() const { return end(); }
+
+  // rows(): the rows as arrays; rows<N>(): the rows' first N elements as
+  // tuples (include/array.h:706-755).
+  template <size_t N = 0>
+  auto rows() {
+    if constexpr (N == 0) {
+      return std::ranges::subrange(begin(), end());
+    } else {
+      std::vector<decltype(std::declval<array>().template take<N>())> out;
+      for (size_t r = 0; r < length(); r++) out.push_back((*this)[r].template take<N>());
+      return out;
+    }
+  }
+  template <size_t N = 0>
+  auto rows() const {
+    if constexpr (N == 0) {
+      return std::ranges::subrange(begin(), end());
+    } else {
+      std::vector<decltype(std::declval<const array>().template take<N>())> out;
+      for (size_t r = 0; r < length(); r++) out.push_back((*this)[r].template take<N>());
+      return out;
+    }
+  }
+
+  //----------------------------------------------------------------------------
+
+  template <std::input_iterator It>
+  void set(It it) {
+    ensure_evaluated_();
+    T *p = storage_.template host_out<T>();
+    for (size_t i = 0; i < element_count(); i++) p[index_of_(i)] = static_cast<T>(*it++);
+    node_.reset();
+  }
+  void set(std::initializer_list<T> l) { set(l.begin()); }
+
+  // Fill: on the device for a large contiguous float/int array (no host
+  // mirror is created), otherwise on the host, so small arrays and scalars
+  // stay host-readable (scalar operands fold into fused programs on the
+  // host, see detail::program_builder).
+  void constants(T val) {
+    ensure_evaluated_();
+    if constexpr (sizeof(T) == 4) {
+      if (device_ == Device::GPU && element_count() >= 4096 && is_contiguous_() &&
+          element_count() == storage_.len) {
+        uint32_t bits;
+        std::memcpy(&bits, &val, 4);
+        gpu::launched_(silgpu_fill_u32(storage_.template dev_out<T>(), bits,
+                                       int64_t(storage_.len)),
+                       "fill");
+        node_.reset();
+        return;
+      }
+    }
+    T *p = storage_.template host_out<T>();
+    for (size_t i = 0; i < element_count(); i++) p[index_of_(i)] = val;
+    node_.reset();
+  }
+  void zeros() { constants(T(0)); }
+  void ones() { constants(T(1)); }
+  // Uniform [0, 1) from a per-thread Mersenne twister, as the reference
+  // (include/array.h:1284-1290).
+  void random() {
+    thread_local std::mt19937 gen(std::random_device{}());
+    std::uniform_real_distribution<float> dist(0.0f, 1.0f);
+    ensure_evaluated_();
+    T *p = storage_.template host_out<T>();
+    for (size_t i = 0; i < element_count(); i++) p[index_of_(i)] = static_cast<T>(dist(gen));
+    node_.reset();
+  }
+
+  //----------------------------------------------------------------------------
+
+  array operator+(const array &rhs) const { return binary_(detail::op::add, rhs); }
+  array operator-(const array &rhs) const { return binary_(detail::op::sub, rhs); }
+  array operator*(const array &rhs) const { return binary_(detail::op::mul, rhs); }
+  array operator/(const array &rhs) const { return binary_(detail::op::div, rhs); }
+  array pow(const array &rhs) const { return binary_(detail::op::pow, rhs); }
+
+  // Compound assignment: out of place for float (the result is a new lazy
+  // node, as the reference's GPU mode, include/array.h:2614-2628).
+  void operator+=(const array &rhs) { *this = *this + rhs; }
+  void operator-=(const array &rhs) { *this = *this - rhs; }
+  void operator*=(const array &rhs) { *this = *this * rhs; }
+  void operator/=(const array &rhs) { *this = *this / rhs; }
+
+  //----------------------------------------------------------------------------
+
+  array dot(const array &rhs) const;
+  array batched_dot(const array &rhs) const;
+  array linear(const array &W, const array &b) const;
+
+  array<float> sigmoid() const;
+  array<float> sigmoid_backward(const array<float> &dout) const;
+  array<float> linear_sigmoid(const array &W, const array &b) const;
+  array<float> relu() const;
+  array<float> layer_norm(const array<float> &gamma, const array<float> &beta,
+                          float eps = 1e-5f) const;
+  array<float> conv2d(const array<float> &, size_t) const {
+    throw std::runtime_error("array: conv2d is not part of this build.");
+  }
+
+  //----------------------------------------------------------------------------
+
+  T sum() const;
+  array sum(size_t axis) const;
+  float mean() const { return static_cast<float>(sum()) / static_cast<float>(element_count()); }
+  array<float> mean(size_t axis) const;
+  T min() const;
+  T max() const;
+
+  size_t count() const {
+    size_t n = 0;
+    for (size_t i = 0; i < element_count(); i++) n += !!at(i);
+    return n;
+  }
+  bool all(arithmetic auto val) const {
+    for (size_t i = 0; i < element_count(); i++)
+      if (!(at(i) == static_cast<T>(val))) return false;
+    return true;
+  }
+  template <typename F>
+    requires std::invocable<F, T>
+  bool all(F fn) const {
+    for (size_t i = 0; i < element_count(); i++)
+      if (!fn(at(i))) return false;
+    return true;
+  }
+
+  array<float> softmax() const;
+  array<int> argmax() const;
+  float mean_square_error(const array &rhs) const {
+    return (*this - rhs).pow(array(static_cast<T>(2))).mean();
+  }
+  template <value_type U = T>
+  array<U> one_hot(size_t class_count) const {
+    if (dimension() != 1)
+      throw std::runtime_error("array: one_hot is available only for 1 dimension array.");
+    array<U> tmp({shape_[0], class_count}, U{});
+    for (size_t i = 0; i < element_count(); i++)
+      tmp[i, static_cast<size_t>(at(i))] = U(1);
+    return tmp;
+  }
+
+  //----------------------------------------------------------------------------
+
+  std::string print_shape_type(const shape_type &shape) const {
+    std::string s = "{";
+    for (size_t i = 0; i < shape.size(); i++) {
+      if (i) s += ", ";
+      s += std::to_string(shape[i]);
+    }
+    return s + "}";
+  }
+  std::string print_shape() const { return print_shape_type(shape_); }
+  std::string print_strides() const { return print_shape_type(strides_); }
+  std::string print_data_type() const {
+    if constexpr (std::is_same_v<T, float>) return "float";
+    else if constexpr (std::is_same_v<T, int>) return "int";
+    else return "bool";
+  }
+  std::string print_info() const {
+    std::ostringstream os;
+    os << "dtype: " << print_data_type() << ", dim: " << dimension()
+       << ", shape: " << print_shape() << ", strides: " << print_strides();
+    return os.str();
+  }
+  std::string print_array() const {
+    std::ostringstream os;
+    if (dimension() == 0) {
+      print_value_(os, at());
+      return os.str();
+    }
+    size_t idx = 0;
+    print_level_(os, 0, idx);
+    return os.str();
+  }
+
+  //----------------------------------------------------------------------------
+  // Backend access (also used by the reference's boundary-level tests).
+
+  const storage &storage_ref() const {
+    ensure_evaluated_();
+    return storage_;
+  }
+
+  // An evaluated array over existing storage (no copy).
+  static array view_(const storage &s, const shape_type &shape, const strides_type &strides) {
+    array a;
+    a.storage_ = s;
+    a.shape_ = shape;
+    a.strides_ = strides;
+    return a;
+  }
+
+  static array make_uninit_(const shape_type &shape) {
+    array a;
+    a.reshape_raw_(shape);
+    a.allocate_();
+    return a;
+  }
+
+  bool is_contiguous_() const {
+    if (shape_.empty()) return true;
+    return strides_ == contiguous_strides(shape_);
+  }
+
+  // A contiguous copy of this (possibly strided or broadcast) view.
+  array materialize_() const;
+
+ private:
+  shape_type shape_;
+  strides_type strides_;
+  storage storage_;
+  std::shared_ptr<detail::node> node_;
+
+  void reshape_raw_(const shape_type &shape) {
+    shape_ = shape;
+    strides_ = contiguous_strides(shape);
+  }
+
+  void allocate_() {
+    const size_t len = element_count();
+    storage_ = storage::make_device(len * sizeof(T));
+    storage_.off = 0;
+    storage_.len = len;
+  }
+
+  template <typename L>
+  void init_list_(const L &l) {
+    shape_type s;
+    detail::nested_shape(l, s, 0);
+    reshape_raw_(s);
+    allocate_();
+    if (detail::nested_count(l) != element_count())
+      throw std::runtime_error("array: invalid initializer list.");
+    T *p = storage_.template host_out<T>();
+    detail::nested_copy(p, l);
+  }
+
+  void ensure_evaluated_() const {
+    if (!node_) return;
+    if (!node_->evaluated) detail::evaluate({node_.get()});
+    if (!storage_ || storage_.buf != node_->data.buf || storage_.off != node_->data.off) {
+      auto &self = const_cast<array &>(*this);
+      self.shape_ = node_->shape;
+      self.strides_ = node_->strides;
+      self.storage_ = node_->data;
+    }
+  }
+
+  // Buffer offset (relative to storage_.off) of the i-th element in
+  // row-major order of this view.
+  size_t index_of_(size_t i) const {
+    if (is_contiguous_()) return i;
+    size_t off = 0;
+    for (size_t d = shape_.size(); d-- > 0;) {
+      off += (i % shape_[d]) * strides_[d];
+      i /= shape_[d];
+    }
+    return off;
+  }
+  size_t offset_of_(const std::vector<size_t> &pos) const {
+    size_t off = 0;
+    for (size_t i = 0; i < pos.size(); i++) off += strides_[i] * pos[i];
+    return off;
+  }
+
+  void bounds_check_(size_t i) const {
+    if (strides_.empty() || i >= element_count())
+      throw std::runtime_error("array: index is out of bounds.");
+  }
+  void bounds_check_(size_t x, size_t y) const {
+    if (dimension() != 2 || x >= shape_[0] || y >= shape_[1])
+      throw std::runtime_error("array: (x, y) is out of bounds.");
+  }
+  void bounds_check_(size_t x, size_t y, size_t z) const {
+    if (dimension() != 3 || x >= shape_[0] || y >= shape_[1] || z >= shape_[2])
+      throw std::runtime_error("array: (x, y, z) is out of bounds.");
+  }
+
+  static std::shared_ptr<detail::node> to_node_(const array &a) {
+    if (a.node_ && !a.node_->evaluated) return a.node_;
+    if (a.node_ && a.node_->evaluated && !a.storage_)
+      return detail::node::leaf(a.node_->data, a.node_->shape, a.node_->strides);
+    return detail::node::leaf(a.storage_, a.shape_, a.strides_);
+  }
+
+  static array from_node_(std::shared_ptr<detail::node> n) {
+    array a;
+    a.shape_ = n->shape;
+    a.strides_ = n->strides;
+    a.node_ = std::move(n);
+    return a;
+  }
+
+  static void require_gpu_() {
+    if (device_ == Device::CPU)
+      throw std::runtime_error(
+          "array: float evaluation needs the GPU backend (sil::use_gpu()); the CPU backend "
+          "is not part of this build.");
+  }
+
+  array binary_(detail::op o, const array &rhs) const;
+  array int_binary_(detail::op o, const array &rhs) const;
+  array host_binary_(detail::op o, const array &rhs, const shape_type &shape) const;
+
+  template <typename F>
+  array<bool> compare_(const array &rhs, F f) const {
+    const auto shape = broadcast_shape(shape_, rhs.shape_);
+    auto l = broadcast(shape);
+    auto r = rhs.broadcast(shape);
+    array<bool> out(shape, false);
+    bool *o = out.buffer_data();
+    for (size_t i = 0; i < out.element_count(); i++) o[i] = f(l.at(i), r.at(i));
+    return out;
+  }
+
+  static void print_value_(std::ostream &os, const T &v) {
+    if constexpr (std::is_same_v<T, bool>) os << (v ? "true" : "false");
+    else os << v;
+  }
+  void print_level_(std::ostream &os, size_t dim, size_t &idx) const {
+    os << '{';
+    for (size_t i = 0; i < shape_[dim]; i++) {
+      if (i) {
+        os << ", ";
+        if (dim + 1 < dimension()) os << '\n' << std::string(dim + 1, ' ');
+      }
+      if (dim + 1 == dimension()) print_value_(os, at(idx++));
+      else print_level_(os, dim + 1, idx);
+    }
+    os << '}';
+  }
+};
+
+//------------------------------------------------------------------------------
+// Iterators
+//------------------------------------------------------------------------------
+
+template <value_type T, bool IsConst>
+class element_iterator_ {
+  using arr_ptr = std::conditional_t<IsConst, const array<T> *, array<T> *>;
+
+ public:
+  using difference_type = std::ptrdiff_t;
+  using value_type = T;
+  using reference = std::conditional_t<IsConst, const T &, T &>;
+  using iterator_concept = std::forward_iterator_tag;
+
+  element_iterator_() = default;
+  element_iterator_(arr_ptr a, size_t i) : a_(a), i_(i) {}
+  reference operator*() const { return a_->at(i_); }
+  element_iterator_ &operator++() {
+    ++i_;
+    return *this;
+  }
+  element_iterator_ operator++(int) {
+    auto t = *this;
+    ++i_;
+    return t;
+  }
+  bool operator==(const element_iterator_ &o) const { return i_ == o.i_; }
+
+ private:
+  arr_ptr a_ = nullptr;
+  size_t i_ = 0;
+};
+
+template <value_type T, bool IsConst>
+class row_iterator_ {
+  using arr_ptr = std::conditional_t<IsConst, const array<T> *, array<T> *>;
+
+ public:
+  using difference_type = std::ptrdiff_t;
+  using value_type = array<T>;
+  using iterator_concept = std::forward_iterator_tag;
+
+  row_iterator_() = default;
+  row_iterator_(arr_ptr a, size_t i) : a_(a), i_(i) {}
+  array<T> operator*() const { return (*a_)[i_]; }
+  row_iterator_ &operator++() {
+    ++i_;
+    return *this;
+  }
+  row_iterator_ operator++(int) {
+    auto t = *this;
+    ++i_;
+    return t;
+  }
+  bool operator==(const row_iterator_ &o) const { return i_ == o.i_; }
+
+ private:
+  arr_ptr a_ = nullptr;
+  size_t i_ = 0;
+};
+
+//------------------------------------------------------------------------------
+// Lazy float ops
+//------------------------------------------------------------------------------
+
+template <value_type T>
+inline array<T> array<T>::binary_(detail::op o, const array &rhs) const {
+  if constexpr (std::is_same_v<T, float>) {
+    auto shape = broadcast_shape(shape_, rhs.shape_);
+    return from_node_(detail::node::make(o, {to_node_(*this), to_node_(rhs)}, shape));
+  } else {
+    return int_binary_(o, rhs);
+  }
+}
+
+// int arithmetic, eager on the GPU (the reference's msl::add<int> path,
+// include/gpu.h:1331-1369); bool arithmetic on the host.
+template <value_type T>
+inline array<T> array<T>::int_binary_(detail::op o, const array &rhs) const {
+  const auto shape = broadcast_shape(shape_, rhs.shape_);
+  if constexpr (std::is_same_v<T, int>) {
+    if (device_ == Device::CPU) return host_binary_(o, rhs, shape);
+    auto full = [&](const array &a) {
+      return (a.shape_ == shape && a.is_contiguous_()) ? a : a.broadcast(shape).materialize_();
+    };
+    auto l = full(*this);
+    auto r = full(rhs);
+    auto out = make_uninit_(shape);
+    int opc = o == detail::op::add ? SILGPU_ADD : o == detail::op::sub ? SILGPU_SUB
+              : o == detail::op::mul ? SILGPU_MUL : o == detail::op::div ? SILGPU_DIV
+                                                                        : SILGPU_POW;
+    gpu::launched_(silgpu_binary_i32(opc, l.storage_.template dev_in<int32_t>(),
+                                     int64_t(l.storage_.len),
+                                     r.storage_.template dev_in<int32_t>(),
+                                     int64_t(r.storage_.len),
+                                     out.storage_.template dev_out<int32_t>(),
+                                     int64_t(out.element_count())),
+                   "arithmetic");
+    return out;
+  } else {
+    return host_binary_(o, rhs, shape);
+  }
+}
+
+// Host evaluation of int / bool arithmetic (the reference's CPU mode for
+// non-float arrays, include/cpu.h:76-237).
+template <value_type T>
+inline array<T> array<T>::host_binary_(detail::op o, const array &rhs,
+                                       const shape_type &shape) const {
+  {
+    auto l = broadcast(shape);
+    auto r = rhs.broadcast(shape);
+    array out(shape, T{});
+    T *p = out.buffer_data();
+    for (size_t i = 0; i < out.element_count(); i++) {
+      const int a = l.at(i), b = r.at(i);
+      int v = o == detail::op::add ? a + b : o == detail::op::sub ? a - b
+              : o == detail::op::mul ? a * b : o == detail::op::div ? (b ? a / b : 0)
+              // powi of the reference: round(pow(float(a), float(b)))
+              : int(std::rint(std::pow(float(a), float(b))));
+      p[i] = static_cast<T>(v);
+    }
+    return out;
+  }
+}
+
+template <value_type T>
+inline array<T> array<T>::materialize_() const {
+  ensure_evaluated_();
+  auto out = make_uninit_(shape_);
+  if constexpr (std::is_same_v<T, float>) {
+    if (element_count() == 0) return out;
+    // One-input program: a strided / broadcast gather into contiguous memory.
+    if (shape_.size() > SILGPU_PROG_MAX_DIMS) throw std::runtime_error("array: too many axes.");
+    silgpu_program p{};
+    p.ndim = static_cast<int32_t>(shape_.size());
+    for (size_t d = 0; d < shape_.size(); d++) {
+      p.shape[d] = int64_t(shape_[d]);
+      p.inputs[0].strides[d] = int64_t(strides_[d]);
+    }
+    p.n_inputs = 1;
+    p.inputs[0].ptr = storage_.template dev_in<float>();
+    p.n_instrs = 1;
+    p.instrs[0] = {SILGPU_PI_LOAD, 0, 0, 0, 0.0f, 0.0f};
+    p.out_reg = 0;
+    gpu::program(p, out.storage_);
+  } else {
+    T *o = out.storage_.template host_out<T>();
+    for (size_t i = 0; i < element_count(); i++) o[i] = at(i);
+  }
+  return out;
+}
+
+template <value_type T>
+inline array<T> array<T>::dot(const array &rhs) const {
+  shape_type out_shape;
+  if (dimension() == 2 && rhs.dimension() == 2 && shape_[1] == rhs.shape_[0])
+    out_shape = {shape_[0], rhs.shape_[1]};
+  else if (dimension() == 1 && rhs.dimension() == 2 && shape_[0] == rhs.shape_[0])
+    out_shape = {rhs.shape_[1]};
+  else if (dimension() == 2 && rhs.dimension() == 1 && shape_[1] == rhs.shape_[0])
+    out_shape = {shape_[0]};
+  else if (dimension() == 1 && rhs.dimension() == 1 && shape_[0] == rhs.shape_[0])
+    out_shape = {};
+  else
+    throw std::runtime_error("array: can't do `dot` operation.");
+  if constexpr (std::is_same_v<T, float>) {
+    return from_node_(detail::node::make(detail::op::dot, {to_node_(*this), to_node_(rhs)},
+                                         out_shape));
+  } else {
+    // Integer products on the host, as the reference (include/cpu.h:239-264).
+    auto a = dimension() == 1 ? broadcast({1, shape_[0]}) : *this;
+    auto b = rhs.dimension() == 1 ? rhs.broadcast({1, rhs.shape_[0]}).transpose() : rhs;
+    const size_t M = a.shape_[0], K = a.shape_[1], N = b.shape_[1];
+    array out(out_shape, T{});
+    T *o = out.buffer_data();
+    for (size_t i = 0; i < M; i++)
+      for (size_t j = 0; j < N; j++) {
+        T s{};
+        for (size_t k = 0; k < K; k++) s += a[i, k] * b[k, j];
+        o[i * N + j] = s;
+      }
+    return out;
+  }
+}
+
+template <value_type T>
+inline array<T> array<T>::batched_dot(const array &rhs) const {
+  static_assert(std::is_same_v<T, float>, "batched_dot requires float");
+  if (dimension() != 3 || rhs.dimension() != 3)
+    throw std::runtime_error("batched_dot: requires 3D arrays");
+  if (shape_[0] != rhs.shape_[0] || shape_[2] != rhs.shape_[1])
+    throw std::runtime_error("batched_dot: shape mismatch");
+  return from_node_(detail::node::make(detail::op::batched_dot, {to_node_(*this), to_node_(rhs)},
+                                       {shape_[0], shape_[1], rhs.shape_[2]}));
+}
+
+template <value_type T>
+inline array<T> array<T>::linear(const array &W, const array &b) const {
+  if constexpr (std::is_same_v<T, float>) {
+    if (dimension() != 2 || W.dimension() != 2 || shape_[1] != W.shape_[0])
+      throw std::runtime_error("array: can't do `linear` operation.");
+    return from_node_(detail::node::make(detail::op::linear,
+                                         {to_node_(*this), to_node_(W), to_node_(b)},
+                                         {shape_[0], W.shape_[1]}));
+  } else {
+    return dot(W) + b;
+  }
+}
+
+template <value_type T>
+inline array<float> array<T>::sigmoid() const {
+  if constexpr (std::is_same_v<T, float>)
+    return from_node_(detail::node::make(detail::op::sigmoid, {to_node_(*this)}, shape_));
+  else
+    return clone<float>().sigmoid();
+}
+
+template <value_type T>
+inline array<float> array<T>::sigmoid_backward(const array<float> &dout) const {
+  if constexpr (std::is_same_v<T, float>)
+    return from_node_(detail::node::make(detail::op::sigmoid_backward,
+                                         {to_node_(*this), to_node_(dout)}, shape_));
+  else
+    return clone<float>().sigmoid_backward(dout);
+}
+
+template <value_type T>
+inline array<float> array<T>::linear_sigmoid(const array &W, const array &b) const {
+  if constexpr (std::is_same_v<T, float>) {
+    if (dimension() != 2 || W.dimension() != 2 || shape_[1] != W.shape_[0])
+      throw std::runtime_error("array: can't do `linear` operation.");
+    return from_node_(detail::node::make(detail::op::linear_sigmoid,
+                                         {to_node_(*this), to_node_(W), to_node_(b)},
+                                         {shape_[0], W.shape_[1]}));
+  } else {
+    return linear(W, b).sigmoid();
+  }
+}
+
+template <value_type T>
+inline array<float> array<T>::relu() const {
+  if constexpr (std::is_same_v<T, float>)
+    return from_node_(detail::node::make(detail::op::relu, {to_node_(*this)}, shape_));
+  else
+    return clone<float>().relu();
+}
+
+template <value_type T>
+inline array<float> array<T>::layer_norm(const array<float> &gamma, const array<float> &beta,
+                                         float eps) const {
+  if (dimension() != 2) throw std::runtime_error("array: layer_norm requires 2D array.");
+  if constexpr (std::is_same_v<T, float>) {
+    auto n = detail::node::make(detail::op::layer_norm,
+                                {to_node_(*this), to_node_(gamma), to_node_(beta)}, shape_);
+    n->eps = eps;
+    return from_node_(std::move(n));
+  } else {
+    return clone<float>().layer_norm(gamma, beta, eps);
+  }
+}
+
+template <value_type T>
+inline array<float> array<T>::softmax() const {
+  if (dimension() != 1 && dimension() != 2)
+    throw std::runtime_error("array: softmax is available only for 1 or 2 dimension array.");
+  if constexpr (std::is_same_v<T, float>) {
+    // A vector is one row (the reference computes this case on the host,
+    // include/array.h:1678-1685).
+    return from_node_(detail::node::make(detail::op::softmax, {to_node_(*this)}, shape_));
+  } else {
+    return clone<float>().softmax();
+  }
+}
+
+template <value_type T>
+inline array<T> array<T>::sum(size_t axis) const {
+  if (axis >= dimension()) throw std::runtime_error("array: invalid axis.");
+  auto s = shape_;
+  s.erase(s.begin() + axis);
+  if constexpr (std::is_same_v<T, float>) {
+    auto n = detail::node::make(detail::op::sum_axis, {to_node_(*this)}, s);
+    n->axis = axis;
+    return from_node_(std::move(n));
+  } else {
+    array tmp(s, T{});
+    std::vector<size_t> pos(dimension()), p2;
+    for (size_t i = 0; i < element_count(); i++) {
+      size_t r = i;
+      for (size_t d = dimension(); d-- > 0;) {
+        pos[d] = r % shape_[d];
+        r /= shape_[d];
+      }
+      p2 = pos;
+      p2.erase(p2.begin() + axis);
+      tmp.at(p2) += at(pos);
+    }
+    return tmp;
+  }
+}
+
+template <value_type T>
+inline array<float> array<T>::mean(size_t axis) const {
+  if constexpr (std::is_same_v<T, float>)
+    return sum(axis) / array<float>(static_cast<float>(shape_[axis]));
+  else
+    return sum(axis).template clone<float>() / array<float>(static_cast<float>(shape_[axis]));
+}
+
+// Full reductions return a host value: the device reduces to one float and
+// the host reads it (one 4-byte download instead of the reference's partials).
+template <value_type T>
+inline T array<T>::sum() const {
+  if constexpr (std::is_same_v<T, float>) {
+    require_gpu_();
+    ensure_evaluated_();
+    auto src = (is_contiguous_() && storage_.len >= element_count()) ? *this : materialize_();
+    auto out = array<float>::make_uninit_({});
+    gpu::sum_f32(src.storage_, out.storage_, src.element_count());
+    return *out.storage_.template host_in<float>();
+  } else {
+    T s{};
+    for (size_t i = 0; i < element_count(); i++) s += at(i);
+    return s;
+  }
+}
+
+template <value_type T>
+inline T array<T>::min() const {
+  if constexpr (std::is_same_v<T, float>) {
+    require_gpu_();
+    if (element_count() == 0) throw std::runtime_error("array: min of an empty array.");
+    ensure_evaluated_();
+    auto src = (is_contiguous_() && storage_.len >= element_count()) ? *this : materialize_();
+    auto out = array<float>::make_uninit_({});
+    gpu::min_f32(src.storage_, out.storage_, src.element_count());
+    return *out.storage_.template host_in<float>();
+  } else {
+    T m = at(0);
+    for (size_t i = 1; i < element_count(); i++) m = std::min(m, at(i));
+    return m;
+  }
+}
+
+template <value_type T>
+inline T array<T>::max() const {
+  if constexpr (std::is_same_v<T, float>) {
+    require_gpu_();
+    if (element_count() == 0) throw std::runtime_error("array: max of an empty array.");
+    ensure_evaluated_();
+    auto src = (is_contiguous_() && storage_.len >= element_count()) ? *this : materialize_();
+    auto out = array<float>::make_uninit_({});
+    gpu::max_f32(src.storage_, out.storage_, src.element_count());
+    return *out.storage_.template host_in<float>();
+  } else {
+    T m = at(0);
+    for (size_t i = 1; i < element_count(); i++) m = std::max(m, at(i));
+    return m;
+  }
+}
+
+// Per-row argmax of a 2-D array, first index of the maximum
+// (include/array.h:1711-1750).  The float result stays on the device.
+template <value_type T>
+inline array<int> array<T>::argmax() const {
+  if (dimension() != 2)
+    throw std::runtime_error("array: argmax is available for 2 dimension array.");
+  const size_t rows = shape_[0], cols = shape_[1];
+  if constexpr (std::is_same_v<T, float>) {
+    require_gpu_();
+    auto src = is_contiguous_() ? *this : materialize_();
+    src.ensure_evaluated_();
+    auto out = array<int>::make_uninit_({rows});
+    gpu::argmax_f32(src.storage_, out.storage_, uint32_t(rows), uint32_t(cols));
+    return out;
+  } else {
+    array<int> out({rows}, 0);
+    for (size_t r = 0; r < rows; r++) {
+      size_t best = 0;
+      for (size_t c = 1; c < cols; c++)
+        if ((*this)[r, c] > (*this)[r, best]) best = c;
+      out.at(r) = static_cast<int>(best);
+    }
+    return out;
+  }
+}
+
+//------------------------------------------------------------------------------
+// Free functions (include/array.h:2730-2831)
+//------------------------------------------------------------------------------
+
+template <value_type T>
+inline std::ostream &operator<<(std::ostream &os, const array<T> &arr) {
+  return os << arr.print_array();
+}
+
+template <value_type T>
+inline array<T> operator+(arithmetic auto lhs, const array<T> &rhs) {
+  return array<T>(static_cast<T>(lhs)) + rhs;
+}
+template <value_type T>
+inline array<T> operator-(arithmetic auto lhs, const array<T> &rhs) {
+  return array<T>(static_cast<T>(lhs)) - rhs;
+}
+template <value_type T>
+inline array<T> operator*(arithmetic auto lhs, const array<T> &rhs) {
+  return array<T>(static_cast<T>(lhs)) * rhs;
+}
+template <value_type T>
+inline array<T> operator/(arithmetic auto lhs, const array<T> &rhs) {
+  return array<T>(static_cast<T>(lhs)) / rhs;
+}
+template <value_type T>
+inline array<T> operator+(const array<T> &lhs, arithmetic auto rhs) {
+  return lhs + array<T>(static_cast<T>(rhs));
+}
+template <value_type T>
+inline array<T> operator-(const array<T> &lhs, arithmetic auto rhs) {
+  return lhs - array<T>(static_cast<T>(rhs));
+}
+template <value_type T>
+inline array<T> operator*(const array<T> &lhs, arithmetic auto rhs) {
+  return lhs * array<T>(static_cast<T>(rhs));
+}
+template <value_type T>
+inline array<T> operator/(const array<T> &lhs, arithmetic auto rhs) {
+  return lhs / array<T>(static_cast<T>(rhs));
+}
+
+template <value_type T, value_type U>
+inline array<T> where(const array<U> &cond, T x, T y) {
+  array<T> tmp(cond.shape(), T{});
+  for (size_t i = 0; i < cond.element_count(); i++) tmp.at(i) = cond.at(i) ? x : y;
+  return tmp;
+}
+
+template <value_type T>
+inline bool array_equal(const array<T> &a, const array<T> &b) {
+  if (&a == &b) return true;
+  if (a.shape() != b.shape()) return false;
+  for (size_t i = 0; i < a.element_count(); i++)
+    if (a.at(i) != b.at(i)) return false;
+  return true;
+}
+
+template <std::floating_point T, std::floating_point U>
+inline bool is_close(T a, U b, float tolerance = 1e-3) {
+  return std::abs(static_cast<float>(a) - static_cast<float>(b)) <= tolerance;
+}
+template <std::integral T, std::integral U>
+inline bool is_close(T a, U b) {
+  return a == b;
+}
+
+template <value_type T>
+inline bool allclose(const array<T> &a, const array<T> &b, float tolerance = 1e-3) {
+  if (&a == &b) return true;
+  if (a.shape() != b.shape()) return false;
+  for (size_t i = 0; i < a.element_count(); i++) {
+    if constexpr (std::is_same_v<T, float>) {
+      if (std::abs(a.at(i) - b.at(i)) > tolerance) return false;
+    } else {
+      if (a.at(i) != b.at(i)) return false;
+    }
+  }
+  return true;
+}
+
+template <value_type T>
+inline auto empty(const shape_type &shape) {
+  return array<T>(shape, T{});
+}
+template <value_type T>
+inline auto zeros(const shape_type &shape) {
+  return array<T>(shape, T(0));
+}
+template <value_type T>
+inline auto ones(const shape_type &shape) {
+  return array<T>(shape, T(1));
+}
+inline auto random(const shape_type &shape) {
+  array<float> tmp(shape, 0.0f);
+  tmp.random();
+  return tmp;
+}
+
+// Evaluates several arrays' graphs in one pass and waits for the GPU
+// (include/array.h:2836-2888).
+template <value_type... Ts>
+inline void eval(array<Ts> &...arrays) {
+  std::vector<detail::node *> roots;
+  auto collect = [&](auto &arr) {
+    auto n = arr.lazy_node_ptr();
+    if (n && !n->evaluated) roots.push_back(n.get());
+  };
+  (collect(arrays), ...);
+  if (!roots.empty()) detail::evaluate(roots);
+  if (gpu_pending_) gpu_context::instance().flush();
+  (arrays.eval(), ...);
+}
+
+//------------------------------------------------------------------------------
+// Graph evaluation
+//------------------------------------------------------------------------------
+
+namespace detail {
+
+// Host value of a length-1 operand, if it can be read without waiting for
+// the GPU (a host-written scalar); std::nullopt otherwise.
+inline bool host_scalar(const node *n, float &v) {
+  if (!n->evaluated || n->data.len != 1) return false;
+  auto *b = n->data.buf.get();
+  if (!b->host || !b->host_valid) return false;
+  v = static_cast<const float *>(b->host)[n->data.off];
+  return true;
+}
+
+struct program_builder {
+  silgpu_program p{};
+  shape_type out_shape;
+  std::vector<storage> keep;  // inputs kept alive until launch
+  std::vector<std::tuple<const void *, strides_type>> slots;
+  bool free_reg[SILGPU_PROG_MAX_REGS];
+  const std::unordered_set<node *> *fused = nullptr;  // nodes computed inside this program
+
+  struct too_big {};
+
+  explicit program_builder(const shape_type &shape) : out_shape(shape) {
+    if (shape.size() > SILGPU_PROG_MAX_DIMS) throw too_big{};
+    p.ndim = static_cast<int32_t>(shape.size());
+    for (size_t d = 0; d < shape.size(); d++) p.shape[d] = int64_t(shape[d]);
+    std::fill(std::begin(free_reg), std::end(free_reg), true);
+  }
+
+  int alloc() {
+    for (int r = 0; r < SILGPU_PROG_MAX_REGS; r++)
+      if (free_reg[r]) {
+        free_reg[r] = false;
+        return r;
+      }
+    throw too_big{};
+  }
+  void release(int r) { free_reg[r] = true; }
+
+  void emit(int32_t op, int32_t dst, int32_t a, int32_t b = 0, float imm = 0, float imm2 = 0) {
+    if (p.n_instrs >= SILGPU_PROG_MAX_INSTRS) throw too_big{};
+    p.instrs[p.n_instrs++] = silgpu_prog_instr{op, dst, a, b, imm, imm2};
+  }
+
+  // Input slot for an evaluated node, with strides relative to the output
+  // shape (right-aligned broadcast; size-1 axes broadcast with stride 0).
+  int slot(node *n) {
+    const size_t no = out_shape.size(), ni = n->shape.size();
+    strides_type st(no, 0);
+    for (size_t d = 0; d < no; d++) {
+      if (d + ni < no) continue;
+      const size_t di = d + ni - no;
+      st[d] = (n->shape[di] == 1 && out_shape[d] != 1) ? 0 : n->strides[di];
+    }
+    const void *ptr = n->data.template dev_in<float>();
+    for (size_t i = 0; i < slots.size(); i++)
+      if (std::get<0>(slots[i]) == ptr && std::get<1>(slots[i]) == st) return int(i);
+    if (slots.size() >= SILGPU_PROG_MAX_INPUTS) throw too_big{};
+    const int s = int(slots.size());
+    slots.emplace_back(ptr, st);
+    keep.push_back(n->data);
+    p.inputs[s].ptr = static_cast<const float *>(ptr);
+    for (size_t d = 0; d < no; d++) p.inputs[s].strides[d] = int64_t(st[d]);
+    p.n_inputs = s + 1;
+    return s;
+  }
+
+  // Sethi-Ullman register need of the fused subtree at n.
+  int need(node *n) const {
+    if (!fused->count(n)) return 1;
+    if (n->operation == op::sigmoid || n->operation == op::relu) return need(n->inputs[0].get());
+    int a = need(n->inputs[0].get()), b = need(n->inputs[1].get());
+    return a == b ? a + 1 : std::max(a, b);
+  }
+
+  // Emits the value of n into a register and returns it.
+  int value(node *n) {
+    if (!fused->count(n)) {
+      int r = alloc();
+      emit(SILGPU_PI_LOAD, r, slot(n));
+      return r;
+    }
+    const op o = n->operation;
+    if (o == op::sigmoid || o == op::relu) {
+      int r = value(n->inputs[0].get());
+      emit(o == op::sigmoid ? SILGPU_PI_SIGMOID : SILGPU_PI_RELU, r, r);
+      return r;
+    }
+    node *a = n->inputs[0].get(), *b = n->inputs[1].get();
+    if (o == op::sigmoid_backward) {  // inputs {x, dout}
+      auto [ra, rb] = pair_(a, b);
+      emit(SILGPU_PI_SIGBWD, ra, ra, rb);
+      release(rb);
+      return ra;
+    }
+    // Scalar operand folded the way the reference's try_affine_reduce folds
+    // one level per node (include/array.h:1888-1940): x op s and s op x
+    // become fma(x, scale, offset) with scale/offset formed in fp32 on the
+    // host, so the fused result is bit-identical to that evaluation.
+    float s;
+    if (o != op::pow && host_scalar(b, s) && !fused->count(b)) {
+      int r = value(a);
+      float scale = 1.0f, offset = 0.0f;
+      switch (o) {
+        case op::add: offset = 0.0f + s; break;
+        case op::sub: offset = 0.0f - s; break;
+        case op::mul: scale = 1.0f * s; offset = 0.0f * s; break;
+        default: scale = 1.0f / s; offset = 0.0f / s; break;  // div
+      }
+      emit(SILGPU_PI_FMAI, r, r, 0, scale, offset);
+      return r;
+    }
+    if (o != op::pow && o != op::div && host_scalar(a, s) && !fused->count(a)) {
+      int r = value(b);
+      float scale = 1.0f, offset = 0.0f;
+      switch (o) {
+        case op::add: offset = 0.0f + s; break;
+        case op::sub: scale = -1.0f; offset = s - 0.0f; break;
+        default: scale = 1.0f * s; offset = 0.0f * s; break;  // mul
+      }
+      emit(SILGPU_PI_FMAI, r, r, 0, scale, offset);
+      return r;
+    }
+    auto [ra, rb] = pair_(a, b);
+    const int32_t code = o == op::add ? SILGPU_PI_ADD : o == op::sub ? SILGPU_PI_SUB
+                         : o == op::mul ? SILGPU_PI_MUL : o == op::div ? SILGPU_PI_DIV
+                                                                        : SILGPU_PI_POW;
+    emit(code, ra, ra, rb);
+    release(rb);
+    return ra;
+  }
+
+  // Both operands in registers, the subtree needing more registers first.
+  std::pair<int, int> pair_(node *a, node *b) {
+    if (need(b) > need(a)) {
+      int rb = value(b);
+      int ra = value(a);
+      return {ra, rb};
+    }
+    int ra = value(a);
+    int rb = value(b);
+    return {ra, rb};
+  }
+};
+
+inline storage new_output(const shape_type &shape) {
+  auto s = storage::make_device(shape_count(shape) * sizeof(float));
+  s.len = shape_count(shape);
+  return s;
+}
+
+inline void finish(node *n, storage out) {
+  n->data = std::move(out);
+  n->strides = contiguous_strides(n->shape);
+  n->evaluated = true;
+}
+
+inline array<float> as_array(node *n) { return array<float>::view_(n->data, n->shape, n->strides); }
+
+// The storage of an evaluated node as a contiguous float array (copies
+// strided or broadcast views).
+inline array<float> contiguous(node *n) {
+  auto a = as_array(n);
+  a.eval();
+  if (a.is_contiguous_() && n->data.len >= shape_count(n->shape)) return a;
+  return a.materialize_();
+}
+
+// 2-D operand of a product: (storage, leading dimension, transposed?) for a
+// view whose inner axis is unit-stride (row-major) or whose outer axis is
+// (a transposed view); anything else is copied first.
+struct gemm_operand {
+  array<float> arr;
+  size_t ld = 0;
+  bool trans = false;
+};
+
+inline gemm_operand operand2d(node *n, const shape_type &as2d) {
+  auto a = as_array(n);
+  a.eval();
+  if (n->shape.size() == 2) {
+    const auto &st = n->strides;
+    if (st[1] == 1 && st[0] >= n->shape[1] && st[0] > 0) return {a, st[0], false};
+    if (st[0] == 1 && st[1] >= n->shape[0] && st[1] > 0) return {a, st[1], true};
+  }
+  auto c = a.is_contiguous_() ? a : a.materialize_();
+  return {c, as2d[1], false};
+}
+
+inline void eval_dot(node *n) {
+  node *l = n->inputs[0].get(), *r = n->inputs[1].get();
+  // 1-D operands: v . m -> {1,K}.{K,N}; m . v -> {M,K}.{K,1}; v . v -> {1,K}.{K,1}
+  // (include/array.h:2700-2728).
+  const bool lv = l->shape.size() == 1, rv = r->shape.size() == 1;
+  const size_t M = lv ? 1 : l->shape[0], K = lv ? l->shape[0] : l->shape[1];
+  const size_t N = rv ? 1 : r->shape[1];
+  gemm_operand A, B;
+  if (lv) {
+    auto c = contiguous(l);
+    A = {c, K, false};
+  } else {
+    A = operand2d(l, {M, K});
+  }
+  if (rv) {
+    auto c = contiguous(r);
+    B = {c, 1, false};  // K x 1, ld 1
+  } else {
+    B = operand2d(r, {K, N});
+  }
+  auto out = new_output(n->shape);
+  gpu::gemm_(A.arr.storage_ref(), B.arr.storage_ref(), out, M, N, K, A.ld, B.ld, A.trans,
+             B.trans, 1, 0, 0, 0, nullptr, 0, SILGPU_EPI_NONE);
+  finish(n, std::move(out));
+}
+
+inline void eval_linear(node *n, bool with_sigmoid) {
+  node *x = n->inputs[0].get(), *w = n->inputs[1].get(), *b = n->inputs[2].get();
+  const size_t M = x->shape[0], K = x->shape[1], N = w->shape[1];
+  auto A = operand2d(x, {M, K});
+  auto B = operand2d(w, {K, N});
+  auto out = new_output(n->shape);
+  const size_t bl = shape_count(b->shape);
+  if (b->shape.size() <= 1 && bl > 0) {
+    // Bias read as bias[col % bias_len] in the GEMM epilogue
+    // (include/gpu_kernels.metal:506-542).
+    auto bias = contiguous(b);
+    gpu::gemm_(A.arr.storage_ref(), B.arr.storage_ref(), out, M, N, K, A.ld, B.ld, A.trans,
+               B.trans, 1, 0, 0, 0, &bias.storage_ref(), bl,
+               with_sigmoid ? SILGPU_EPI_BIAS_SIGMOID : SILGPU_EPI_BIAS);
+    finish(n, std::move(out));
+    return;
+  }
+  // Higher-rank bias: product, then a broadcast add (and sigmoid) program.
+  gpu::gemm_(A.arr.storage_ref(), B.arr.storage_ref(), out, M, N, K, A.ld, B.ld, A.trans,
+             B.trans, 1, 0, 0, 0, nullptr, 0, SILGPU_EPI_NONE);
+  auto prod = node::leaf(out, n->shape, contiguous_strides(n->shape));
+  std::unordered_set<node *> none;
+  program_builder pb(n->shape);
+  pb.fused = &none;
+  int r = pb.alloc();
+  pb.emit(SILGPU_PI_LOAD, r, pb.slot(prod.get()));
+  int rb = pb.alloc();
+  pb.emit(SILGPU_PI_LOAD, rb, pb.slot(b));
+  pb.emit(SILGPU_PI_ADD, r, r, rb);
+  if (with_sigmoid) pb.emit(SILGPU_PI_SIGMOID, r, r);
+  pb.p.out_reg = r;
+  auto res = new_output(n->shape);
+  gpu::program(pb.p, res);
+  finish(n, std::move(res));
+}
+
+inline void eval_node_nonfused(node *n) {
+  switch (n->operation) {
+    case op::dot:
+      eval_dot(n);
+      return;
+    case op::batched_dot: {
+      auto a = contiguous(n->inputs[0].get());
+      auto b = contiguous(n->inputs[1].get());
+      const size_t Bt = n->shape[0], M = n->shape[1], N = n->shape[2];
+      const size_t K = n->inputs[0]->shape[2];
+      auto out = new_output(n->shape);
+      gpu::gemm_(a.storage_ref(), b.storage_ref(), out, M, N, K, K, N, false, false, Bt, M * K,
+                 K * N, M * N, nullptr, 0, SILGPU_EPI_NONE);
+      finish(n, std::move(out));
+      return;
+    }
+    case op::linear:
+      eval_linear(n, false);
+      return;
+    case op::linear_sigmoid:
+      eval_linear(n, true);
+      return;
+    case op::softmax: {
+      auto a = contiguous(n->inputs[0].get());
+      auto out = new_output(n->shape);
+      const size_t rows = n->shape.size() == 2 ? n->shape[0] : 1;
+      gpu::softmax(a.storage_ref(), out, uint32_t(rows), uint32_t(n->shape.back()));
+      finish(n, std::move(out));
+      return;
+    }
+    case op::layer_norm: {
+      auto a = contiguous(n->inputs[0].get());
+      auto g = contiguous(n->inputs[1].get());
+      auto b = contiguous(n->inputs[2].get());
+      const size_t cols = n->shape[1];
+      if (g.element_count() < cols || b.element_count() < cols)
+        throw std::runtime_error("array: layer_norm gamma/beta shorter than the rows.");
+      auto out = new_output(n->shape);
+      gpu::layer_norm(a.storage_ref(), out, g.storage_ref(), b.storage_ref(),
+                      uint32_t(n->shape[0]), uint32_t(cols), n->eps);
+      finish(n, std::move(out));
+      return;
+    }
+    case op::sum_axis: {
+      node *in = n->inputs[0].get();
+      auto a = contiguous(in);
+      size_t outer = 1, inner = 1;
+      for (size_t d = 0; d < n->axis; d++) outer *= in->shape[d];
+      for (size_t d = n->axis + 1; d < in->shape.size(); d++) inner *= in->shape[d];
+      auto out = new_output(n->shape);
+      gpu::sum_axis(a.storage_ref(), out, outer, in->shape[n->axis], inner);
+      finish(n, std::move(out));
+      return;
+    }
+    default:
+      throw std::runtime_error("array: unsupported lazy operation.");
+  }
+}
+
+// Runs the fused program for elementwise root n over the subtree in `fused`.
+inline bool try_program(node *n, const std::unordered_set<node *> &fused) {
+  try {
+    program_builder pb(n->shape);
+    pb.fused = &fused;
+    int r = pb.value(n);
+    pb.p.out_reg = r;
+    auto out = new_output(n->shape);
+    if (shape_count(n->shape) > 0) gpu::program(pb.p, out);
+    finish(n, std::move(out));
+    return true;
+  } catch (program_builder::too_big &) {
+    return false;
+  }
+}
+
+inline void evaluate(const std::vector<node *> &roots) {
+  if (device_ == Device::CPU)
+    throw std::runtime_error(
+        "array: float evaluation needs the GPU backend (sil::use_gpu()); the CPU backend "
+        "is not part of this build.");
+  // Post-order DFS over unevaluated nodes (include/array.h:1945-1971).
+  std::vector<node *> order;
+  std::unordered_set<node *> seen;
+  std::vector<std::pair<node *, uint8_t>> stack;
+  for (node *r : roots)
+    if (r && !r->evaluated && seen.insert(r).second) stack.push_back({r, 0});
+  while (!stack.empty()) {
+    auto &[cur, idx] = stack.back();
+    if (idx < cur->num_inputs) {
+      node *c = cur->inputs[idx++].get();
+      if (c && !c->evaluated && seen.insert(c).second) stack.push_back({c, 0});
+    } else {
+      order.push_back(cur);
+      stack.pop_back();
+    }
+  }
+  // Consumers inside this graph, and the single consumer where there is one.
+  std::unordered_map<node *, int> consumers;
+  std::unordered_map<node *, node *> parent;
+  for (node *n : order)
+    for (uint8_t i = 0; i < n->num_inputs; i++) {
+      node *c = n->inputs[i].get();
+      if (!c->evaluated) {
+        consumers[c]++;
+        parent[c] = n;
+      }
+    }
+  const std::unordered_set<node *> root_set(roots.begin(), roots.end());
+  // A node is computed inside its consumer's program when it is elementwise,
+  // has exactly one consumer, that consumer is elementwise, it is not a root
+  // and no array outside the graph holds it.
+  auto fusable = [&](node *c) {
+    if (c->evaluated || root_set.count(c) || !is_elementwise(c->operation)) return false;
+    auto it = consumers.find(c);
+    if (it == consumers.end() || it->second != 1) return false;
+    if (!is_elementwise(parent[c]->operation)) return false;
+    // The consumer's input slot must be the only owner (no array holds c).
+    node *p = parent[c];
+    for (uint8_t i = 0; i < p->num_inputs; i++)
+      if (p->inputs[i].get() == c) return p->inputs[i].use_count() == 1;
+    return false;
+  };
+  for (node *n : order) {
+    if (n->evaluated) continue;
+    if (!is_elementwise(n->operation)) {
+      eval_node_nonfused(n);
+    } else if (fusable(n)) {
+      continue;  // computed by its consumer's program
+    } else {
+      // Collect the fused subtree below n.
+      std::unordered_set<node *> fused{n};
+      std::vector<node *> work{n};
+      while (!work.empty()) {
+        node *x = work.back();
+        work.pop_back();
+        for (uint8_t i = 0; i < x->num_inputs; i++) {
+          node *c = x->inputs[i].get();
+          if (fusable(c) && fused.insert(c).second) work.push_back(c);
+        }
+      }
+      if (!try_program(n, fused)) {
+        // Too large for one program: evaluate the subtree node by node.
+        std::vector<node *> sub;
+        for (node *m : order)
+          if (fused.count(m) && m != n) sub.push_back(m);
+        for (node *m : sub) {
+          std::unordered_set<node *> one{m};
+          if (!try_program(m, one)) throw std::runtime_error("array: elementwise node too large.");
+        }
+        std::unordered_set<node *> one{n};
+        if (!try_program(n, one)) throw std::runtime_error("array: elementwise node too large.");
+      }
+    }
+  }
+  // Release inputs so intermediates are freed (include/array.h:2056-2060).
+  for (node *n : order) {
+    for (auto &i : n->inputs) i.reset();
+    n->num_inputs = 0;
+  }
+}
+
+}  // namespace detail
+
+}  // namespace sil

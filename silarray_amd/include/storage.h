@@ -1,0 +1,222 @@
+#pragma once
+// Device memory for sil::array on MI355X.
+//
+// The reference hands out unified-memory MTLBuffers whose `data` pointer the
+// host reads and writes directly (include/unified_memory.h:17-79).  MI355X
+// memory is discrete HBM, so a storage here owns a pooled HBM block
+// (silgpu_alloc, on first device use) and, only when the host touches the
+// data, a host mirror.  A small state machine keeps the two coherent:
+//
+//   host_read()   : download if the device copy is newer; host copy valid
+//   host_write()  : as host_read(), then the device copy becomes stale
+//   dev_read()    : upload if the host copy is newer
+//   dev_write()   : the host copy becomes stale (kernel output)
+//
+// Views (slices, rows, broadcasts, transposes) share one `block` and differ
+// in `off`/`len`, as in the reference.  Raw users of `data` (the reference's
+// boundary tests write into storage::make()'s buffer and call gpu:: directly)
+// start in the host-valid state, so the first kernel that reads the storage
+// uploads it; synchronize() downloads every storage a kernel has written.
+
+#include <cstddef>
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <unordered_set>
+
+#include "../../include/silgpu.h"
+
+namespace sil {
+
+namespace detail {
+
+inline void check(int rc, const char *what) {
+  if (rc != SILGPU_OK)
+    throw std::runtime_error(std::string("gpu: ") + what + ": " + silgpu_last_error());
+}
+
+inline void ensure_init() {
+  static bool done = false;
+  if (!done) {
+    check(silgpu_init(), "init");
+    done = true;
+  }
+}
+
+struct block;
+
+// Blocks whose device copy is newer than the host mirror; synchronize()
+// downloads them (reference semantics: after synchronize the host sees
+// every result).
+struct dirty_set {
+  std::mutex mu;
+  std::unordered_set<block *> blocks;
+  static dirty_set &instance() {
+    static auto *s = new dirty_set();
+    return *s;
+  }
+};
+
+struct block {
+  void *dev = nullptr;   // HBM, allocated on first device use
+  void *host = nullptr;  // host mirror, allocated on first host access
+  size_t bytes = 0;
+  // Neither valid: a fresh block whose content nobody has written yet.
+  bool host_valid = false;
+  bool dev_valid = false;
+
+  explicit block(size_t n) : bytes(n) {}
+  block(const block &) = delete;
+  block &operator=(const block &) = delete;
+  ~block() {
+    {
+      auto &d = dirty_set::instance();
+      std::lock_guard<std::mutex> lk(d.mu);
+      d.blocks.erase(this);
+    }
+    if (dev) silgpu_free(dev);
+    std::free(host);
+  }
+
+  void *dev_ptr() {
+    if (!dev) {
+      ensure_init();
+      check(silgpu_alloc(bytes ? bytes : 4, &dev), "alloc");
+    }
+    return dev;
+  }
+
+  // Plain (pageable) host memory: host access is the exception on this
+  // backend, and host-only work (shape logic, int reductions) then runs
+  // without a GPU at all.
+  void *host_ptr() {
+    if (!host) {
+      host = std::aligned_alloc(64, ((bytes ? bytes : 4) + 63) / 64 * 64);
+      if (!host) throw std::bad_alloc();
+    }
+    return host;
+  }
+
+  void host_read() {
+    host_ptr();
+    if (!host_valid) {
+      if (dev_valid) check(silgpu_memcpy_d2h(host, dev_ptr(), bytes), "download");
+      else std::memset(host, 0, bytes);  // fresh block: defined as zeros
+      host_valid = true;
+      unmark_dirty();
+    }
+  }
+
+  void host_write() {
+    host_read();
+    dev_valid = false;
+  }
+
+  void dev_read() {
+    if (!dev_valid) {
+      if (host_valid) check(silgpu_memcpy_h2d(dev_ptr(), host, bytes), "upload");
+      dev_valid = true;
+    }
+  }
+
+  void dev_write() {
+    dev_valid = true;
+    host_valid = false;
+    mark_dirty();
+  }
+
+  // A kernel writes part of the block: keep untouched bytes by making the
+  // device copy current first.
+  void dev_write_partial() {
+    dev_read();
+    dev_write();
+  }
+
+  void mark_dirty() {
+    auto &d = dirty_set::instance();
+    std::lock_guard<std::mutex> lk(d.mu);
+    d.blocks.insert(this);
+  }
+  void unmark_dirty() {
+    auto &d = dirty_set::instance();
+    std::lock_guard<std::mutex> lk(d.mu);
+    d.blocks.erase(this);
+  }
+};
+
+}  // namespace detail
+
+// A typed window onto a block: elements [off, off + len) of the block.
+// Replaces the reference's storage {buf, data, mtl_buf, off, len}
+// (include/unified_memory.h:17-25).  `data` is the host mirror's base
+// address, valid after host_data()/storage::make; device code never reads
+// it.
+struct storage {
+  std::shared_ptr<detail::block> buf;
+  void *data = nullptr;  // host mirror base (element 0 of the block)
+  size_t off = 0;        // in elements
+  size_t len = 0;        // in elements
+
+  // A new block of `bytes`, zero-filled and host-authoritative, with `data`
+  // ready for host writes (the reference's boundary tests memcpy into it
+  // before launching a kernel).
+  static storage make(size_t bytes) {
+    storage s;
+    s.buf = std::make_shared<detail::block>(bytes);
+    s.buf->host_read();
+    s.data = s.buf->host;
+    return s;
+  }
+
+  // A new block with undefined content and no host mirror yet: the form for
+  // kernel outputs and for arrays whose elements are set afterwards.
+  static storage make_device(size_t bytes) {
+    storage s;
+    s.buf = std::make_shared<detail::block>(bytes);
+    return s;
+  }
+
+  explicit operator bool() const { return static_cast<bool>(buf); }
+
+  // Device address of element `off` for element type T, made current.
+  template <typename T>
+  const T *dev_in() const {
+    buf->dev_read();
+    return static_cast<const T *>(buf->dev_ptr()) + off;
+  }
+  template <typename T>
+  T *dev_out() {
+    if (off == 0 && len * sizeof(T) >= buf->bytes) buf->dev_write();
+    else buf->dev_write_partial();
+    return static_cast<T *>(buf->dev_ptr()) + off;
+  }
+
+  // In-place kernels: the device copy is read and then overwritten.
+  template <typename T>
+  T *dev_inout() {
+    buf->dev_read();
+    buf->dev_write();
+    return static_cast<T *>(buf->dev_ptr()) + off;
+  }
+
+  // Host address of element `off`, made current (read) or made current and
+  // taken over (write).
+  template <typename T>
+  const T *host_in() const {
+    buf->host_read();
+    const_cast<storage *>(this)->data = buf->host;
+    return static_cast<const T *>(buf->host) + off;
+  }
+  template <typename T>
+  T *host_out() {
+    buf->host_write();
+    data = buf->host;
+    return static_cast<T *>(buf->host) + off;
+  }
+};
+
+}  // namespace sil

@@ -1,0 +1,460 @@
+// C++ front-end tests: the behaviour the reference's doctest suite pins
+// (test/test_array.cpp, test/test_examples.cpp, test/test_2lnn.cpp) checked
+// against this build's sil::array on the MI355X backend, plus checks of
+// the eval() lowering (fusion, reference rounding of scalar chains) and the
+// storage/host-mirror protocol.  HOST_CASEs touch no GPU and run in the CPU
+// test suite; TEST_CASEs need the GPU.
+#include <silarray.h>
+
+#include <cmath>
+#include <cstring>
+#include <numeric>
+#include <ranges>
+#include <vector>
+
+#include "harness.h"
+
+using namespace sil;
+
+static auto iota_n(size_t n, int start = 1) {
+  return std::views::iota(start) | std::views::take(n);
+}
+
+//------------------------------------------------------------------------------
+// Shapes, views, host-side logic (no GPU)
+//------------------------------------------------------------------------------
+
+HOST_CASE("scalar shape") {
+  auto s = array<int>(100);
+  CHECK(s.element_count() == 1);
+  CHECK(s.dimension() == 0);
+  CHECK(s.shape() == shape_type{});
+  CHECK(s.at() == 100);
+  CHECK_THROWS_WITH(s.length(), "array: cannot call with a scalar value.");
+}
+
+HOST_CASE("vector shape and construction") {
+  auto v = empty<int>({3});
+  CHECK(v.element_count() == 3 && v.length() == 3 && v.dimension() == 1);
+  auto w = array<int>{1, 2, 3, 4};
+  CHECK(w.element_count() == 4);
+  std::vector<int> src{1, 2, 3, 4};
+  auto v1 = array<int>({src.size() - 1}, src);
+  CHECK(array_equal(v1, {1, 2, 3}));
+  auto v3 = array<int>(src);
+  CHECK(array_equal(v3, {1, 2, 3, 4}));
+  auto r = array<int>({10}, iota_n(10));
+  CHECK(array_equal(r, {1, 2, 3, 4, 5, 6, 7, 8, 9, 10}));
+}
+
+HOST_CASE("matrix and tensor initializers") {
+  auto m2 = array<int>{{1, 2, 3, 4}, {5, 6, 7, 8}, {9, 10, 11, 12}};
+  CHECK(m2.shape() == (shape_type{3, 4}));
+  CHECK(m2.strides() == (strides_type{4, 1}));
+  auto m3 = array<int>{{{1, 2, 3}, {4, 5, 6}}, {{7, 8, 9}, {10, 11, 12}}};
+  CHECK(m3.shape() == (shape_type{2, 2, 3}));
+  CHECK(m3.strides() == (strides_type{6, 3, 1}));
+  CHECK_THROWS_WITH((array<int>{{{1, 2, 3}, {4, 5}}, {{7, 8, 9}, {10, 11, 12}}}),
+                    "array: invalid initializer list.");
+  auto m = array<int>({3, 4}, iota_n(12));
+  size_t i = 0;
+  for (size_t r = 0; r < 3; r++)
+    for (size_t c = 0; c < 4; c++) CHECK((m[r, c]) == m.at(i++));
+}
+
+HOST_CASE("bounds checks") {
+  auto v = array<int>({10}, iota_n(10, 0));
+  CHECK(v.at(9) == 9);
+  CHECK_THROWS_WITH(v.at(10), "array: index is out of bounds.");
+  auto t = array<int>{{{1, 2, 3}, {4, 5, 6}}};
+  CHECK_THROWS_WITH(t[3], "array: row is out of bounds.");
+}
+
+HOST_CASE("transpose views") {
+  auto v = array<int>{1, 2, 3, 4};
+  auto vT = v.transpose();
+  CHECK(vT.shape() == (shape_type{1, 4}));
+  CHECK(array_equal(vT, {{1, 2, 3, 4}}));
+  CHECK(array_equal(vT.transpose(), {1, 2, 3, 4}));
+  auto m = array<int>{{1, 2, 3, 4}, {5, 6, 7, 8}, {9, 10, 11, 12}};
+  auto mT = m.transpose();
+  CHECK(mT.shape() == (shape_type{4, 3}));
+  CHECK(array_equal(mT, {{1, 5, 9}, {2, 6, 10}, {3, 7, 11}, {4, 8, 12}}));
+  CHECK(array_equal(mT.transpose(), m));
+  auto t = array<int>{{{1, 2, 3, 4}, {5, 6, 7, 8}}, {{9, 10, 11, 12}, {13, 14, 15, 16}}};
+  auto tT = t.transpose();
+  CHECK(tT.shape() == (shape_type{4, 2, 2}));
+  CHECK(array_equal(tT.transpose(), t));
+}
+
+HOST_CASE("broadcast view") {
+  auto a = array<int>{{1, 2, 3}, {4, 5, 6}};
+  auto b = a.broadcast({3, 2, 3});
+  CHECK(array_equal(b, {{{1, 2, 3}, {4, 5, 6}}, {{1, 2, 3}, {4, 5, 6}}, {{1, 2, 3}, {4, 5, 6}}}));
+  CHECK(b.element_count() == 18);
+  CHECK(b.buffer_element_count() == 6);
+  CHECK((b[2, 1, 2]) == 6);
+  CHECK(b.strides() == (strides_type{0, 3, 1}));
+}
+
+HOST_CASE("row views share storage") {
+  auto t = array<int>{{{1, 2, 3}, {4, 5, 6}}, {{7, 8, 9}, {10, 11, 12}}, {{13, 14, 15}, {16, 17, 18}}};
+  auto m = t[1];
+  auto v = m[1];
+  auto s = v[1];
+  CHECK(array_equal(m, {{7, 8, 9}, {10, 11, 12}}));
+  CHECK(array_equal(s, array<int>(11)));
+  s.at() += 100;
+  CHECK(array_equal(t, {{{1, 2, 3}, {4, 5, 6}}, {{7, 8, 9}, {10, 111, 12}}, {{13, 14, 15}, {16, 17, 18}}}));
+  m.zeros();
+  CHECK(array_equal(v, {0, 0, 0}));
+  CHECK(array_equal(t, {{{1, 2, 3}, {4, 5, 6}}, {{0, 0, 0}, {0, 0, 0}}, {{13, 14, 15}, {16, 17, 18}}}));
+}
+
+HOST_CASE("int aggregates") {
+  auto v = array<int>{1, 2, 3, 4, 5, 6};
+  auto t = array<int>{{{1, 2, 3}, {4, 5, 6}}, {{7, 8, 9}, {10, 11, 12}}, {{13, 14, 15}, {16, 17, 18}}};
+  CHECK(v.min() == 1 && v.max() == 6 && t.min() == 1 && t.max() == 18);
+  CHECK(v.sum() == 21 && t.sum() == 171);
+  CHECK(array_equal(t.sum(0), {{21, 24, 27}, {30, 33, 36}}));
+  CHECK(array_equal(t.sum(1), {{5, 7, 9}, {17, 19, 21}, {29, 31, 33}}));
+  CHECK(array_equal(t.sum(2), {{6, 15}, {24, 33}, {42, 51}}));
+  CHECK(v.mean() == 3.5f && t.mean() == 9.5f);
+  auto row = array<int>{{10, 20, 30}, {1, 2, 3}}[1];
+  CHECK(row.min() == 1 && row.max() == 3 && row.count() == 3 && !row.all(1));
+}
+
+HOST_CASE("iterators") {
+  auto t = array<int>{{{1, 2, 3}, {4, 5, 6}}, {{7, 8, 9}, {10, 11, 12}}, {{13, 14, 15}, {16, 17, 18}}};
+  for (auto row : t)
+    for (auto &x : row.elements()) x += 100;
+  const auto ct = t;
+  int cur = 101;
+  for (auto row : ct.rows())
+    for (const auto &x : row.elements()) CHECK(x == cur++);
+  cur = 101;
+  for (auto row : ct.rows())
+    for (auto [a, b, c] : row.rows<3>()) {
+      CHECK(a == cur++);
+      CHECK(b == cur++);
+      CHECK(c == cur++);
+    }
+}
+
+HOST_CASE("int argmax, one_hot, where") {
+  auto m = array<int>{{3, 1, 2}, {6, 8, 7}};
+  CHECK(array_equal(m.argmax(), {0, 1}));
+  auto v = array<float>{0, 1, 5, 9};
+  auto oh = v.one_hot(10);
+  CHECK(oh.shape() == (shape_type{4, 10}));
+  CHECK((oh[2, 5]) == 1.0f && (oh[2, 4]) == 0.0f && (oh[3, 9]) == 1.0f);
+  auto w = where(array<int>{1, 0, 2} > array<int>(0), 5, 7);
+  CHECK(array_equal(w, {5, 7, 5}));
+}
+
+HOST_CASE("int arithmetic in CPU mode") {
+  use_cpu();
+  auto a = array<int>({3, 4}, iota_n(12));
+  auto b = array<int>({3, 4}, iota_n(12));
+  CHECK(array_equal(a + b, {{2, 4, 6, 8}, {10, 12, 14, 16}, {18, 20, 22, 24}}));
+  CHECK(array_equal(a * b, {{1, 4, 9, 16}, {25, 36, 49, 64}, {81, 100, 121, 144}}));
+  CHECK(array_equal(a / b, {{1, 1, 1, 1}, {1, 1, 1, 1}, {1, 1, 1, 1}}));
+  CHECK(array_equal(array<int>{1, 2, 3}.pow(array<int>{2, 2, 2}), {1, 4, 9}));
+  auto c = array<int>({3, 1}, std::vector{1, 2, 3}) + array<int>({1, 3}, std::vector{10, 20, 30});
+  CHECK(array_equal(c, {{11, 21, 31}, {12, 22, 32}, {13, 23, 33}}));
+  // float evaluation is GPU-only in this build
+  CHECK_THROWS_WITH((array<float>{1.0f} + array<float>{2.0f}).at(0),
+                    "array: float evaluation needs the GPU backend (sil::use_gpu()); the CPU "
+                    "backend is not part of this build.");
+  use_gpu();
+}
+
+//------------------------------------------------------------------------------
+// GPU: elementwise, broadcast, scalars
+//------------------------------------------------------------------------------
+
+TEST_CASE("float vector arithmetic goldens") {
+  auto a = array<float>{7.82637e-06, 0.131538, 0.755605, 0.45865, 0.532767, 0.218959, 0.0470446,
+                        0.678865, 0.679296, 0.934693, 0.383502, 0.519416, 0.830965, 0.0345721,
+                        0.0534616, 0.5297};
+  auto b = array<float>{0.671149, 0.00769819, 0.383416, 0.0668422, 0.417486, 0.686773, 0.588977,
+                        0.930436, 0.846167, 0.526929, 0.0919649, 0.653919, 0.415999, 0.701191,
+                        0.910321, 0.762198};
+  CHECK(allclose(a + b, {0.671157, 0.139236, 1.13902, 0.525492, 0.950253, 0.905732, 0.636021,
+                         1.6093, 1.52546, 1.46162, 0.475467, 1.17334, 1.24696, 0.735763,
+                         0.963782, 1.2919}));
+  CHECK(allclose(a - b, {-0.671141, 0.12384, 0.372189, 0.391808, 0.115281, -0.467814, -0.541932,
+                         -0.251571, -0.166871, 0.407764, 0.291537, -0.134503, 0.414966, -0.666619,
+                         -0.856859, -0.232498}));
+  CHECK(allclose(a * b, {5.25266e-06, 0.0010126, 0.289711, 0.0306572, 0.222423, 0.150375,
+                         0.0277082, 0.63164, 0.574798, 0.492517, 0.0352687, 0.339656, 0.345681,
+                         0.0242416, 0.0486672, 0.403736}));
+  CHECK(allclose(a / b, {1.16612e-05, 17.0869, 1.97072, 6.86168, 1.27613, 0.318823, 0.0798751,
+                         0.72962, 0.802792, 1.77385, 4.17009, 0.794312, 1.99752, 0.0493048,
+                         0.0587283, 0.694964}));
+  CHECK_THROWS_WITH(random({4}) + random({8}), "array: invalid operation.");
+}
+
+TEST_CASE("pow int and float") {
+  CHECK(array_equal(array<int>{1, 2, 3}.pow(array<int>{2, 2, 2}), {1, 4, 9}));
+  CHECK(array_equal(array<int>{2, 2, 2}.pow(array<int>{1, 2, 3}), {2, 4, 8}));
+  CHECK(allclose(array<float>{1, 2, 3}.pow(array<float>{2, 2, 2}), {1, 4, 9}));
+  CHECK(allclose(array<float>{2, 2, 2}.pow(array<float>{1, 2, 3}), {2, 4, 8}));
+}
+
+TEST_CASE("int matrix arithmetic on the GPU") {
+  auto a = array<int>({3, 4}, iota_n(12));
+  auto b = array<int>({3, 4}, iota_n(12));
+  CHECK(array_equal(a + b, {{2, 4, 6, 8}, {10, 12, 14, 16}, {18, 20, 22, 24}}));
+  CHECK(array_equal(a - b, {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}}));
+  CHECK(array_equal(a * b, {{1, 4, 9, 16}, {25, 36, 49, 64}, {81, 100, 121, 144}}));
+  CHECK(array_equal(a / b, {{1, 1, 1, 1}, {1, 1, 1, 1}, {1, 1, 1, 1}}));
+}
+
+TEST_CASE("scalar arithmetic") {
+  auto a = array<float>{{1, 2}, {3, 4}};
+  CHECK(array_equal(a + 1, {{2, 3}, {4, 5}}));
+  CHECK(array_equal(a - 1, {{0, 1}, {2, 3}}));
+  CHECK(array_equal(a * 2, {{2, 4}, {6, 8}}));
+  CHECK(array_equal(a / 2, {{0.5, 1}, {1.5, 2}}));
+  CHECK(array_equal(1 + a, {{2, 3}, {4, 5}}));
+  CHECK(array_equal(1 - a, {{0, -1}, {-2, -3}}));
+  CHECK(array_equal(2 * a, {{2, 4}, {6, 8}}));
+  CHECK(array_equal(2 / a, {{2, 1}, {2.0f / 3.0f, 0.5}}));
+}
+
+TEST_CASE("broadcast arithmetic") {
+  auto a23 = array<int>{{1, 2, 3}, {4, 5, 6}};
+  auto a223 = array<int>{{{1, 2, 3}, {4, 5, 6}}, {{7, 8, 9}, {10, 11, 12}}};
+  auto b = array<int>(1);
+  auto b3 = array<int>{1, 2, 3};
+  auto b23 = array<int>{{1, 2, 3}, {4, 5, 6}};
+  CHECK(array_equal(a23 + b, {{2, 3, 4}, {5, 6, 7}}));
+  CHECK(array_equal(a223 + b3, {{{2, 4, 6}, {5, 7, 9}}, {{8, 10, 12}, {11, 13, 15}}}));
+  CHECK(array_equal(a223 + b23, {{{2, 4, 6}, {8, 10, 12}}, {{8, 10, 12}, {14, 16, 18}}}));
+  CHECK(array_equal(b3 + a23, {{2, 4, 6}, {5, 7, 9}}));
+  CHECK(array_equal(b23 + a223, {{{2, 4, 6}, {8, 10, 12}}, {{8, 10, 12}, {14, 16, 18}}}));
+  auto c = array<int>({3, 1}, std::vector{1, 2, 3}) + array<int>({1, 3}, std::vector{10, 20, 30});
+  CHECK(array_equal(c, {{11, 21, 31}, {12, 22, 32}, {13, 23, 33}}));
+  // float, including a middle-axis broadcast the i % len rule cannot express
+  auto f = array<float>({2, 2, 3}, iota_n(12)) * array<float>({2, 1, 3}, iota_n(6));
+  CHECK(array_equal(f, {{{1, 4, 9}, {4, 10, 18}}, {{28, 40, 54}, {40, 55, 72}}}));
+}
+
+TEST_CASE("sigmoid and relu") {
+  auto s = array<float>{0.0f, 1.0f, -1.0f, 5.0f, -5.0f}.sigmoid();
+  CHECK(is_close(s.at(0), 0.5f) && is_close(s.at(1), 0.7310f) && is_close(s.at(2), 0.2689f));
+  CHECK(s.at(3) > 0.99f && s.at(4) < 0.01f);
+  auto big = random({64, 128}).sigmoid();
+  CHECK(big.all([](float x) { return x >= 0.0f && x <= 1.0f; }));
+  auto r = array<float>{-2.0f, -1.0f, 0.0f, 1.0f, 2.0f}.relu();
+  CHECK(array_equal(r, {0.0f, 0.0f, 0.0f, 1.0f, 2.0f}));
+  auto br = (random({64, 128}) - array<float>(0.5f)).relu();
+  CHECK(br.all([](float x) { return x >= 0.0f; }));
+}
+
+//------------------------------------------------------------------------------
+// GPU: products
+//------------------------------------------------------------------------------
+
+TEST_CASE("dot goldens") {
+  CHECK(array_equal(array<int>({4}, iota_n(4)).dot(array<int>({4}, iota_n(4))), array<int>(30)));
+  CHECK(array_equal(array<int>({3, 4}, iota_n(12)).dot(array<int>({4, 2}, iota_n(8))),
+                    {{50, 60}, {114, 140}, {178, 220}}));
+  auto fa = array<float>({3, 4}, std::vector<float>{1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12});
+  auto fb = array<float>({4, 2}, std::vector<float>{1, 2, 3, 4, 5, 6, 7, 8});
+  auto fo = fa.dot(fb);
+  CHECK(fo.shape() == (shape_type{3, 2}));
+  CHECK(array_equal(fo, {{50, 60}, {114, 140}, {178, 220}}));
+  CHECK(array_equal(array<float>({4}, iota_n(4)).dot(array<float>({4, 2}, iota_n(8))), {50, 60}));
+  CHECK(array_equal(array<float>({2, 4}, iota_n(8)).dot(array<float>({4}, iota_n(4))), {30, 70}));
+  auto vv = array<float>({4}, iota_n(4)).dot(array<float>({4}, iota_n(4)));
+  CHECK(vv.shape() == shape_type{} && vv.at() == 30.0f);
+  auto y = array<float>{1, 2, 3}.dot(array<float>{{1, 2}, {3, 4}, {5, 6}});
+  CHECK(array_equal(y, {22, 28}));
+}
+
+TEST_CASE("dot with transposed views") {
+  auto x = ones<float>({4, 3});
+  auto dout = ones<float>({4, 2});
+  auto W = ones<float>({3, 2}) * 0.5f;
+  auto dx = dout.dot(W.transpose());
+  CHECK(dx.shape() == (shape_type{4, 3}));
+  CHECK(dx.all([](float v) { return std::abs(v - 1.0f) < 1e-6f; }));
+  auto dW = x.transpose().dot(dout);
+  CHECK(dW.shape() == (shape_type{3, 2}));
+  CHECK(dW.all([](float v) { return std::abs(v - 4.0f) < 1e-6f; }));
+}
+
+TEST_CASE("linear and linear_sigmoid") {
+  auto x = array<float>({2, 3}, std::vector<float>{1, 2, 3, 4, 5, 6});
+  auto W = array<float>({3, 2}, std::vector<float>{1, 2, 3, 4, 5, 6});
+  auto b = array<float>({2}, std::vector<float>{10, 20});
+  auto out = x.linear(W, b);
+  CHECK(array_equal(out, {{32, 48}, {59, 84}}));
+  auto out2 = out.sigmoid().linear(array<float>({2, 1}, std::vector<float>{1, 1}),
+                                   array<float>({1}, std::vector<float>{0}));
+  CHECK(out2.shape() == (shape_type{2, 1}));
+  CHECK(std::abs(*out2.element_cbegin() - 2.0f) < 0.02f);
+  auto ls = x.linear_sigmoid(W, b);
+  CHECK(ls.all([](float v) { return v > 0.999f; }));
+}
+
+TEST_CASE("batched_dot") {
+  auto a = array<float>({2, 2, 3}, iota_n(12));
+  auto b = array<float>({2, 3, 2}, iota_n(12));
+  auto c = a.batched_dot(b);
+  CHECK(c.shape() == (shape_type{2, 2, 2}));
+  CHECK(array_equal(c, {{{22, 28}, {49, 64}}, {{220, 244}, {301, 334}}}));
+}
+
+//------------------------------------------------------------------------------
+// GPU: reductions and row ops
+//------------------------------------------------------------------------------
+
+TEST_CASE("float aggregates") {
+  CHECK(is_close(array<float>{1.1f, 2.2f}.sum(), 3.3f));
+  CHECK(is_close(ones<float>({10000}).sum(), 10000.0f, 1.0f));
+  auto big2d = ones<float>({256, 128});
+  CHECK(is_close(big2d.sum(), 32768.0f, 1.0f));
+  auto s0 = big2d.sum(0);
+  CHECK(s0.shape() == shape_type{128} && is_close(s0.at(0), 256.0f, 1.0f));
+  auto t = array<float>({3, 2, 3}, iota_n(18));
+  CHECK(array_equal(t.sum(0), {{21, 24, 27}, {30, 33, 36}}));
+  CHECK(array_equal(t.sum(1), {{5, 7, 9}, {17, 19, 21}, {29, 31, 33}}));
+  CHECK(array_equal(t.sum(2), {{6, 15}, {24, 33}, {42, 51}}));
+  CHECK(array_equal(t.mean(0), {{7, 8, 9}, {10, 11, 12}}));
+  CHECK(array_equal(t.mean(2), {{2, 5}, {8, 11}, {14, 17}}));
+  CHECK(t.min() == 1.0f && t.max() == 18.0f && t.mean() == 9.5f);
+  auto fm = array<float>{{3, 1, 2}, {6, 8, 7}};
+  CHECK(array_equal(fm.argmax(), {0, 1}));
+  CHECK((array<float>{1, 2, 3, 4}.mean_square_error(array<float>{0, 2, 3, 6}) == 1.25f));
+}
+
+TEST_CASE("layer_norm") {
+  auto x = array<float>{{1.0f, 2.0f, 3.0f}, {4.0f, 5.0f, 6.0f}};
+  auto out = x.layer_norm(array<float>{1, 1, 1}, array<float>{0, 0, 0});
+  CHECK(out.shape() == (shape_type{2, 3}));
+  CHECK(is_close((out[0, 0]), -1.2247f, 1e-2f) && is_close((out[0, 1]), 0.0f, 1e-2f) &&
+        is_close((out[0, 2]), 1.2247f, 1e-2f));
+  auto out2 = x.layer_norm(array<float>{2, 2, 2}, array<float>{1, 1, 1});
+  CHECK(is_close((out2[0, 1]), 1.0f, 1e-2f));
+  auto big = random({64, 256}).layer_norm(ones<float>({256}), zeros<float>({256}));
+  for (size_t i = 0; i < 64; i++) CHECK(is_close(big[i].mean(), 0.0f, 0.1f));
+}
+
+TEST_CASE("softmax") {
+  auto vsm = array<int>{1, 2, 3, 4, 5, 6}.softmax();
+  CHECK(is_close(vsm.sum(), 1.0f, 1e-6f));
+  auto msm = array<int>{{7, 8, 9}, {10, 11, 12}}.softmax();
+  CHECK(allclose(msm.sum(1), array<float>{1, 1}, 1e-6f));
+  auto sm = array<float>{1.0f, 2.0f, 3.0f}.softmax();
+  CHECK(is_close(sm.at(0), 0.0900f) && is_close(sm.at(1), 0.2447f) && is_close(sm.at(2), 0.6652f));
+  auto big = random({64, 32}).softmax();
+  for (size_t i = 0; i < 64; i++) CHECK(is_close(big[i].sum(), 1.0f, 1e-3f));
+}
+
+//------------------------------------------------------------------------------
+// GPU: eval() lowering
+//------------------------------------------------------------------------------
+
+TEST_CASE("affine chain fuses and keeps reference rounding") {
+  // 20 scalar affine nodes on one array: one fused launch whose result
+  // equals node-by-node evaluation with the reference's folding
+  // (mul -> fma(x, s, 0), add -> fma(x, 1, b), div -> fma(x, 1/r, 0)).
+  const size_t n = 1 << 20;
+  auto x = random({n});
+  std::vector<float> host(x.buffer_data(), x.buffer_data() + n);
+  auto y = x;
+  for (int i = 0; i < 10; i++) y = y * (1.0f + 0.01f * i) + (0.001f * i);
+  y = y / 3.0f - 0.5f;
+  eval(y);
+  std::vector<float> ref = host;
+  for (auto &v : ref) {
+    for (int i = 0; i < 10; i++) {
+      v = std::fma(v, 1.0f + 0.01f * i, 0.0f * (1.0f + 0.01f * i));
+      v = std::fma(v, 1.0f, 0.0f + 0.001f * i);
+    }
+    v = std::fma(v, 1.0f / 3.0f, 0.0f / 3.0f);
+    v = std::fma(v, 1.0f, 0.0f - 0.5f);
+  }
+  bool same = true;
+  const float *p = y.buffer_data();
+  for (size_t i = 0; i < n; i++) same = same && (p[i] == ref[i]);
+  CHECK(same);
+}
+
+TEST_CASE("fused graph with shared and broadcast operands") {
+  auto a = random({33, 129});
+  auto b = random({129});
+  auto c = random({33, 1});
+  auto t = (a * b + c).relu();       // intermediate used twice -> materialised
+  auto u = t * t - t.sigmoid() / 2.0f;
+  eval(u, t);
+  const float *pa = a.buffer_data(), *pb = b.buffer_data(), *pc = c.buffer_data();
+  bool ok = true;
+  for (size_t i = 0; i < 33; i++)
+    for (size_t j = 0; j < 129; j++) {
+      float tv = std::max(pa[i * 129 + j] * pb[j] + pc[i], 0.0f);
+      float s = 1.0f / (1.0f + std::exp(-tv));
+      float uv = tv * tv - std::fma(s, 0.5f, 0.0f * 0.5f);
+      ok = ok && std::abs((t[i, j]) - tv) <= 1e-6f && std::abs((u[i, j]) - uv) <= 2e-6f;
+    }
+  CHECK(ok);
+}
+
+TEST_CASE("arrays held outside the graph are materialised") {
+  auto x = random({1000});
+  auto y = x * 2.0f;      // held by `y`
+  auto z = y + 1.0f;
+  eval(z);
+  CHECK(y.lazy_node_ptr()->evaluated);
+  bool ok = true;
+  for (size_t i = 0; i < 1000; i++) ok = ok && (y.at(i) == x.at(i) * 2.0f) && (z.at(i) == y.at(i) + 1.0f);
+  CHECK(ok);
+}
+
+//------------------------------------------------------------------------------
+// GPU: storage boundary (the reference's msl:: tests, test/test_array.cpp:643-706)
+//------------------------------------------------------------------------------
+
+TEST_CASE("msl add float / int / broadcast on raw storage") {
+  auto a = storage::make(4 * sizeof(float));
+  auto b = storage::make(4 * sizeof(float));
+  auto o = storage::make(4 * sizeof(float));
+  float av[] = {1, 2, 3, 4}, bv[] = {10, 20, 30, 40};
+  std::memcpy(a.data, av, sizeof(av));
+  std::memcpy(b.data, bv, sizeof(bv));
+  a.len = b.len = o.len = 4;
+  msl::add<float>(a, b, o);
+  synchronize();
+  CHECK(array_equal(array<float>({4}, static_cast<float *>(o.data)), {11.0f, 22.0f, 33.0f, 44.0f}));
+
+  auto ia = storage::make(4 * sizeof(int)), ib = storage::make(4 * sizeof(int)),
+       io = storage::make(4 * sizeof(int));
+  int iav[] = {1, 2, 3, 4}, ibv[] = {10, 20, 30, 40};
+  std::memcpy(ia.data, iav, sizeof(iav));
+  std::memcpy(ib.data, ibv, sizeof(ibv));
+  ia.len = ib.len = io.len = 4;
+  msl::add<int>(ia, ib, io);
+  synchronize();
+  CHECK(array_equal(array<int>({4}, static_cast<int *>(io.data)), {11, 22, 33, 44}));
+
+  auto s1 = storage::make(sizeof(float));
+  float one[] = {10.0f};
+  std::memcpy(s1.data, one, sizeof(one));
+  s1.len = 1;
+  msl::add<float>(a, s1, o);
+  synchronize();
+  CHECK(array_equal(array<float>({4}, static_cast<float *>(o.data)), {11.0f, 12.0f, 13.0f, 14.0f}));
+}
+
+TEST_CASE("host writes after device use are uploaded") {
+  auto x = ones<float>({8192});
+  auto s1 = x.sum();
+  x.at(5) = 3.0f;  // host write marks the device copy stale
+  auto s2 = x.sum();
+  CHECK(s1 == 8192.0f && s2 == 8194.0f);
+}
+
+int main(int argc, char **argv) { return harness::run(argc, argv); }

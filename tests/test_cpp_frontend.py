@@ -1,0 +1,30 @@
+"""Runs the C++ front-end test binary (tests/cpp/test_array.cpp, built by
+__graft_entry__.build()).  Host-only cases need no GPU; the full run does."""
+
+import subprocess
+from pathlib import Path
+
+import pytest
+
+BIN = Path(__file__).resolve().parent / "cpp" / "test_array"
+
+
+def _run(args, timeout):
+    assert BIN.exists(), f"{BIN} not built: run __graft_entry__.build()"
+    proc = subprocess.run([str(BIN), *args], capture_output=True, text=True, timeout=timeout)
+    print(proc.stdout[-4000:])
+    print(proc.stderr[-4000:])
+    return proc
+
+
+def test_cpp_host_cases():
+    proc = _run(["--host-only"], 120)
+    assert proc.returncode == 0, proc.stderr
+    assert "failed checks" in proc.stdout and " 0 failed checks" in proc.stdout
+
+
+@pytest.mark.gpu
+def test_cpp_all_cases_on_gpu():
+    proc = _run([], 300)
+    assert proc.returncode == 0, proc.stderr
+    assert " 0 failed checks" in proc.stdout
