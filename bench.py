@@ -12,7 +12,9 @@ steps with a device synchronisation on both sides.
 The other rows of the workload (GEMV, small-batch SGEMM, linear_sigmoid, row
 softmax / layer_norm / sum(axis=1), full sum/min/max/argmax, the 20-op affine
 chain, the 2048^3 and 4096^3 SGEMMs) are reported under "secondary" with
-their own roofline fractions.  Bandwidth rows rotate >= 1 GiB of buffers so
+their own roofline fractions, together with whole sil::eval graphs run
+through the C++ front end (the encoder block, the reference's transformer
+and MLP benchmarks, the affine chain at the API level).  Bandwidth rows rotate >= 1 GiB of buffers so
 the 256 MiB Infinity Cache cannot serve repeated reads.
 
 cpu_baseline: cblas_sgemm from OpenBLAS (the x86 stand-in for the
@@ -245,6 +247,32 @@ def bench_copy(nat, g, reps=20):
     return {"gbs": 8 * n / (ms / 1e3) / 1e9, "us": ms * 1e3, "bytes": 8 * n}
 
 
+GRAPH_BENCH = ROOT / "silarray_amd" / "bench" / "bench_graph"
+# The reference's published sil-gpu times for its single-head transformer
+# block on an Apple M1 Pro (bench/README.md:196-199), keyed by (seq, d_model).
+REF_TRANSFORMER_MS = {(256, 512): 1.53, (256, 768): 2.30, (256, 1024): 2.93, (512, 1024): 5.32}
+
+
+def bench_graphs(timeout: float = 300.0) -> list[dict]:
+    """Whole sil::eval graphs through the C++ front end (bench_graph): the
+    B4 S512 d768 H12 encoder block, the reference's single-head transformer
+    and linear_sigmoid MLP benchmarks, and the 20-op affine chain at the API
+    level.  Each iteration is eval + synchronize, as the reference times it."""
+    import subprocess
+
+    if not GRAPH_BENCH.exists():
+        raise RuntimeError(f"{GRAPH_BENCH} is not built (run __graft_entry__.build())")
+    out = []
+    for argv in (["encoder", "10"], ["transformer"], ["mlp"], ["chain", str(64 << 20), "20"]):
+        log(f"bench_graph {' '.join(argv)}")
+        proc = subprocess.run([str(GRAPH_BENCH), *argv], capture_output=True, text=True,
+                              timeout=timeout)
+        if proc.returncode != 0:
+            raise RuntimeError(f"bench_graph {argv} failed ({proc.returncode}): {proc.stderr}")
+        out += [json.loads(l) for l in proc.stdout.splitlines() if l.startswith("{")]
+    return out
+
+
 def cpu_baseline(seconds: float) -> dict:
     """cblas_sgemm (OpenBLAS) 2048^3 fp32 on this host's cores, repeated for
     about `seconds`; TFLOP/s of the same SGEMM shape family as the headline."""
@@ -353,6 +381,29 @@ def main():
             log(f"sgemm {s}^3 {r}")
             secondary[f"sgemm_{s}"] = {"value": round(r["tflops_kernel"], 2), "unit": "TFLOP/s",
                                        "roofline": roofline("mfma", r["tflops_kernel"])}
+
+    if want("graphs"):
+        for r in bench_graphs():
+            log(f"graph {r}")
+            w = r["workload"]
+            if w == "encoder_block":
+                key = f"encoder_block_B{r['B']}_S{r['S']}_D{r['D']}_H{r['H']}_F{r['F']}"
+            elif w == "transformer_block":
+                key = f"transformer_block_seq{r['seq']}_d{r['d_model']}"
+            elif w == "mlp_linear_sigmoid":
+                key = f"mlp_linear_sigmoid_batch{r['batch']}"
+            else:
+                key = f"{w}_64M_api"
+            if "gemm_tflops" in r:
+                e = {"value": r["gemm_tflops"], "unit": "TFLOP/s (GEMM flops / wall)",
+                     "ms": r["ms"], "timing": "median of eval+synchronize iterations"}
+            else:
+                e = {"value": r["gbs"], "unit": "GB/s", "ms": r["ms"],
+                     "timing": "median of eval+synchronize iterations"}
+            ref = REF_TRANSFORMER_MS.get((r.get("seq"), r.get("d_model")))
+            if w == "transformer_block" and ref is not None:
+                e["reference_m1pro_ms"] = ref
+            secondary[key] = e
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -1,0 +1,293 @@
+// Benchmarks and checks of whole sil::eval graphs through the C++ front end.
+//
+//   bench_graph chain   [n] [reps]            20 scalar affine nodes (x*a+b x10)
+//                                             on n floats, one sil::eval
+//   bench_graph encoder [B S D H F] [reps]    one transformer encoder block
+//                                             (pre-norm, multi-head attention,
+//                                             ReLU FFN) as one sil::eval graph
+//   bench_graph encoder-dump B S D H F DIR    writes the block's inputs and
+//                                             output (raw float32) to DIR for
+//                                             the parity test
+//   bench_graph transformer [seq d ff] [reps] the reference's single-head block
+//   bench_graph mlp [batch] [reps]            the reference's linear_sigmoid MLP
+//
+// Each timed iteration is sil::eval + wait, the reference's convention
+// (bench/bench_common.h:42-68); the median of `reps` iterations is reported
+// as one JSON line.  Inputs come from a SplitMix64 stream (seeded, portable)
+// so the parity test can regenerate them.
+#include <silarray.h>
+
+#include <algorithm>
+#include <array>
+#include <stdexcept>
+#include <chrono>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <fstream>
+#include <string>
+#include <vector>
+
+using namespace sil;
+
+namespace {
+
+// SplitMix64; uniform in [-1, 1) from the top 24 bits; normal by Box-Muller.
+struct rng {
+  uint64_t s;
+  explicit rng(uint64_t seed) : s(seed) {}
+  uint64_t next() {
+    uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+  }
+  float uniform() { return float(next() >> 40) * (2.0f / 16777216.0f) - 1.0f; }
+  float normal(float std) {
+    double u1 = (double(next() >> 11) + 1.0) / 9007199254740993.0;
+    double u2 = double(next() >> 11) / 9007199254740992.0;
+    return float(std * std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2));
+  }
+};
+
+array<float> filled(const shape_type &shape, rng &g, float std, bool uniform = false) {
+  array<float> a = array<float>::make_uninit_(shape);
+  float *p = a.buffer_data();
+  for (size_t i = 0; i < a.element_count(); i++) p[i] = uniform ? g.uniform() : g.normal(std);
+  return a;
+}
+
+template <typename F>
+double median_ms(int reps, F fn) {
+  fn();  // warmup
+  fn();
+  std::vector<double> t;
+  for (int i = 0; i < reps; i++) {
+    auto t0 = std::chrono::steady_clock::now();
+    fn();
+    auto t1 = std::chrono::steady_clock::now();
+    t.push_back(std::chrono::duration<double, std::milli>(t1 - t0).count());
+  }
+  std::sort(t.begin(), t.end());
+  return t[t.size() / 2];
+}
+
+struct encoder {
+  size_t B, S, D, H, F;
+  array<float> x, g1, b1, Wqkv, bqkv, Wo, bo, g2, b2, W1, c1, W2, c2;
+
+  encoder(size_t B_, size_t S_, size_t D_, size_t H_, size_t F_, uint64_t seed)
+      : B(B_), S(S_), D(D_), H(H_), F(F_) {
+    rng g(seed);
+    x = filled({B * S, D}, g, 1.0f);
+    Wqkv = filled({D, 3 * D}, g, 0.02f);
+    bqkv = filled({3 * D}, g, 0.02f);
+    Wo = filled({D, D}, g, 0.02f);
+    bo = filled({D}, g, 0.02f);
+    W1 = filled({D, F}, g, 0.02f);
+    c1 = filled({F}, g, 0.02f);
+    W2 = filled({F, D}, g, 0.02f);
+    c2 = filled({D}, g, 0.02f);
+    g1 = ones<float>({D});
+    b1 = zeros<float>({D});
+    g2 = ones<float>({D});
+    b2 = zeros<float>({D});
+  }
+
+  // The block as one lazy graph:
+  //   h = LN1(x); [q k v] = split(h Wqkv + bqkv) into H heads of D/H
+  //   attn = softmax(q k^T / sqrt(D/H)) v; r1 = x + merge(attn) Wo + bo
+  //   out = r1 + relu(LN2(r1) W1 + c1) W2 + c2
+  array<float> build() const {
+    const size_t dh = D / H;
+    const float scale = 1.0f / std::sqrt(float(dh));
+    auto h = x.layer_norm(g1, b1);
+    auto qkv = h.linear(Wqkv, bqkv);                                   // [B*S, 3D]
+    auto heads = qkv.view({B, S, 3, H, dh}).permute({2, 0, 3, 1, 4});  // [3, B, H, S, dh]
+    auto q = heads.select(0, 0), k = heads.select(0, 1), v = heads.select(0, 2);
+    auto scores = q.batched_dot(k.permute({0, 1, 3, 2})) * scale;      // [B, H, S, S]
+    auto attn = scores.view({B * H * S, S}).softmax().view({B, H, S, S});
+    auto ctx = attn.batched_dot(v);                                    // [B, H, S, dh]
+    auto merged = ctx.permute({0, 2, 1, 3}).view({B * S, D});
+    auto r1 = x + merged.linear(Wo, bo);
+    auto ff = r1.layer_norm(g2, b2).linear(W1, c1).relu();
+    return r1 + ff.linear(W2, c2);
+  }
+
+  double gemm_flops() const {
+    const double M = double(B * S);
+    return 2.0 * M * D * 3 * D + 2.0 * B * H * S * S * (D / H) * 2 + 2.0 * M * D * D +
+           2.0 * M * D * F * 2;
+  }
+};
+
+// The reference's single-head transformer block, written exactly as its
+// composite benchmark writes it (bench/composite/bench_transformer.cpp:34-71):
+// separate Q/K/V projections, scores = Q K^T * scale with K^T a transposed
+// view, row softmax, one sil::eval + synchronize per iteration.
+double transformer_ms(size_t seq, size_t d_model, size_t d_ff, int reps) {
+  const float scale = 1.0f / std::sqrt(float(d_model));
+  auto x = random({seq, d_model});
+  auto Wq = random({d_model, d_model}) * scale, bq = zeros<float>({d_model});
+  auto Wk = random({d_model, d_model}) * scale, bk = zeros<float>({d_model});
+  auto Wv = random({d_model, d_model}) * scale, bv = zeros<float>({d_model});
+  auto Wo = random({d_model, d_model}) * scale, bo = zeros<float>({d_model});
+  auto W1 = random({d_model, d_ff}) * (1.0f / std::sqrt(float(d_model)));
+  auto b1 = zeros<float>({d_ff});
+  auto W2 = random({d_ff, d_model}) * (1.0f / std::sqrt(float(d_ff)));
+  auto b2 = zeros<float>({d_model});
+  auto gamma1 = ones<float>({d_model}), beta1 = zeros<float>({d_model});
+  auto gamma2 = ones<float>({d_model}), beta2 = zeros<float>({d_model});
+  eval(Wq, Wk, Wv, Wo, W1, W2);
+  synchronize();
+  return median_ms(reps, [&] {
+    auto h = x.layer_norm(gamma1, beta1);
+    auto Q = h.linear(Wq, bq);
+    auto K = h.linear(Wk, bk);
+    auto V = h.linear(Wv, bv);
+    auto scores = Q.dot(K.transpose()) * scale;
+    auto attn = scores.softmax();
+    auto context = attn.dot(V);
+    auto attn_out = context.linear(Wo, bo);
+    auto r1 = x + attn_out;
+    auto h2 = r1.layer_norm(gamma2, beta2);
+    auto ff = h2.linear(W1, b1).relu();
+    auto out = r1 + ff.linear(W2, b2);
+    eval(out);
+    synchronize();
+  });
+}
+
+// The reference's MLP inference benchmark (bench/composite/bench_mlp.cpp:28-41):
+// 768 -> 2048 -> sigmoid -> 768 -> sigmoid through linear_sigmoid.
+double mlp_ms(size_t batch, int reps) {
+  const size_t D = 768, H = 2048;
+  auto x = random({batch, D});
+  auto W1 = random({D, H});
+  auto b1 = zeros<float>({H});
+  auto W2 = random({H, D});
+  auto b2 = zeros<float>({D});
+  synchronize();
+  return median_ms(reps, [&] {
+    auto h1 = x.linear_sigmoid(W1, b1);
+    auto out = h1.linear_sigmoid(W2, b2);
+    eval(out);
+    synchronize();
+  });
+}
+
+void write_raw(const std::string &path, const array<float> &a) {
+  std::ofstream f(path, std::ios::binary);
+  const float *p = a.buffer_data();
+  f.write(reinterpret_cast<const char *>(p), std::streamsize(a.element_count() * sizeof(float)));
+  f.close();
+  if (!f) throw std::runtime_error("cannot write " + path);
+}
+
+}  // namespace
+
+int main(int argc, char **argv) {
+  const std::string mode = argc > 1 ? argv[1] : "encoder";
+  try {
+    if (mode == "chain") {
+      const size_t n = argc > 2 ? std::strtoull(argv[2], nullptr, 10) : (size_t(64) << 20);
+      const int reps = argc > 3 ? std::atoi(argv[3]) : 20;
+      if (reps < 1 || n == 0) throw std::runtime_error("n and reps must be >= 1");
+      rng g(7);
+      auto x = filled({n}, g, 1.0f, true);
+      auto run = [&] {
+        auto y = x;
+        for (int i = 0; i < 10; i++) y = y * (1.0f + 0.001f * float(i)) + (0.01f * float(i));
+        eval(y);
+      };
+      const double ms = median_ms(reps, run);
+      std::printf("{\"workload\": \"affine_chain20\", \"n\": %zu, \"ms\": %.4f, \"gbs\": %.1f}\n", n,
+                  ms, 8.0 * double(n) / (ms * 1e-3) / 1e9);
+      return 0;
+    }
+    if (mode == "encoder" || mode == "encoder-dump") {
+      // argv: mode [B S D H F [reps|DIR]] or, for "encoder", mode [reps].
+      size_t dims[5] = {4, 512, 768, 12, 3072};
+      const bool has_dims = argc >= 7;
+      if (has_dims)
+        for (int i = 0; i < 5; i++) dims[i] = std::strtoull(argv[2 + i], nullptr, 10);
+      if (dims[3] == 0 || dims[2] % dims[3] != 0) {
+        std::fprintf(stderr, "bench_graph: D must be a multiple of H\n");
+        return 2;
+      }
+      encoder e(dims[0], dims[1], dims[2], dims[3], dims[4], 2026);
+      if (mode == "encoder-dump") {
+        const std::string dir = has_dims && argc > 7 ? argv[7] : ".";
+        auto out = e.build();
+        eval(out);
+        write_raw(dir + "/x.bin", e.x);
+        write_raw(dir + "/Wqkv.bin", e.Wqkv);
+        write_raw(dir + "/bqkv.bin", e.bqkv);
+        write_raw(dir + "/Wo.bin", e.Wo);
+        write_raw(dir + "/bo.bin", e.bo);
+        write_raw(dir + "/W1.bin", e.W1);
+        write_raw(dir + "/c1.bin", e.c1);
+        write_raw(dir + "/W2.bin", e.W2);
+        write_raw(dir + "/c2.bin", e.c2);
+        write_raw(dir + "/out.bin", out);
+        std::printf("{\"dumped\": \"%s\"}\n", dir.c_str());
+        return 0;
+      }
+      const int reps = has_dims ? (argc > 7 ? std::atoi(argv[7]) : 10)
+                                : (argc > 2 ? std::atoi(argv[2]) : 10);
+      if (reps < 1) {
+        std::fprintf(stderr, "bench_graph: reps must be >= 1\n");
+        return 2;
+      }
+      const double ms = median_ms(reps, [&] {
+        auto out = e.build();
+        eval(out);
+      });
+      std::printf(
+          "{\"workload\": \"encoder_block\", \"B\": %zu, \"S\": %zu, \"D\": %zu, \"H\": %zu, "
+          "\"F\": %zu, \"ms\": %.4f, \"gemm_tflops\": %.2f}\n",
+          e.B, e.S, e.D, e.H, e.F, ms, e.gemm_flops() / (ms * 1e-3) / 1e12);
+      return 0;
+    }
+    if (mode == "transformer") {
+      // argv: [seq d_model d_ff [reps]]; default: the reference's four configs
+      // (bench/composite/bench_transformer.cpp:77-82).
+      std::vector<std::array<size_t, 3>> cfgs = {
+          {256, 512, 2048}, {256, 768, 3072}, {256, 1024, 4096}, {512, 1024, 4096}};
+      if (argc >= 5)
+        cfgs = {{std::strtoull(argv[2], nullptr, 10), std::strtoull(argv[3], nullptr, 10),
+                 std::strtoull(argv[4], nullptr, 10)}};
+      const int reps = argc > 5 ? std::atoi(argv[5]) : 20;
+      if (reps < 1) throw std::runtime_error("reps must be >= 1");
+      for (auto [seq, d, f] : cfgs) {
+        const double ms = transformer_ms(seq, d, f, reps);
+        const double flops = 2.0 * seq * d * d * 4 + 2.0 * seq * seq * d * 2 + 2.0 * seq * d * f * 2;
+        std::printf("{\"workload\": \"transformer_block\", \"seq\": %zu, \"d_model\": %zu, "
+                    "\"d_ff\": %zu, \"ms\": %.4f, \"gemm_tflops\": %.2f}\n",
+                    seq, d, f, ms, flops / (ms * 1e-3) / 1e12);
+      }
+      return 0;
+    }
+    if (mode == "mlp") {
+      // argv: [batch [reps]]; default: the reference's batches 128, 256, 1024.
+      std::vector<size_t> batches = {128, 256, 1024};
+      if (argc >= 3) batches = {std::strtoull(argv[2], nullptr, 10)};
+      const int reps = argc > 3 ? std::atoi(argv[3]) : 50;
+      if (reps < 1) throw std::runtime_error("reps must be >= 1");
+      for (size_t b : batches) {
+        const double ms = mlp_ms(b, reps);
+        const double flops = 2.0 * b * 768 * 2048 * 2;
+        std::printf("{\"workload\": \"mlp_linear_sigmoid\", \"batch\": %zu, \"ms\": %.4f, "
+                    "\"gemm_tflops\": %.2f}\n",
+                    b, ms, flops / (ms * 1e-3) / 1e12);
+      }
+      return 0;
+    }
+    std::fprintf(stderr, "usage: bench_graph chain|encoder|encoder-dump|transformer|mlp ...\n");
+    return 2;
+  } catch (std::exception &ex) {
+    std::fprintf(stderr, "bench_graph: %s\n", ex.what());
+    return 1;
+  }
+}

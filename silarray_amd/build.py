@@ -78,18 +78,31 @@ CXX = os.environ.get("SIL_CXX", "/opt/rocm/llvm/bin/clang++")
 CPP_TESTS = ROOT / "tests" / "cpp"
 
 
-def build_cpp_tests() -> Path:
-    """Compiles the C++ front-end tests (tests/cpp/test_array.cpp) against the
-    headers in silarray_amd/include, linked to the in-tree libsilgpu.so."""
-    out = CPP_TESTS / "test_array"
+def _cxx(src: Path, out: Path, rpath: str) -> Path:
     tmp = out.with_suffix(".tmp")
     _run([CXX, "-std=c++23", "-O2", "-ffp-contract=off", "-Wall", "-Wno-unused-function",
-          f"-I{PKG / 'include'}", str(CPP_TESTS / "test_array.cpp"), "-o", str(tmp),
-          f"-L{PKG}", "-lsilgpu", "-Wl,-rpath,$ORIGIN/../../silarray_amd"])
+          f"-I{PKG / 'include'}", str(src), "-o", str(tmp), f"-L{PKG}", "-lsilgpu",
+          f"-Wl,-rpath,{rpath}"])
     os.replace(tmp, out)
     return out
 
 
+def build_cpp_tests() -> Path:
+    """Compiles the C++ front-end tests (tests/cpp/test_array.cpp) against the
+    headers in silarray_amd/include, linked to the in-tree libsilgpu.so."""
+    return _cxx(CPP_TESTS / "test_array.cpp", CPP_TESTS / "test_array",
+                "$ORIGIN/../../silarray_amd")
+
+
+def build_cpp_bench() -> Path:
+    """Compiles the sil::eval graph benchmark (silarray_amd/bench/bench_graph.cpp)."""
+    return _cxx(PKG / "bench" / "bench_graph.cpp", PKG / "bench" / "bench_graph", "$ORIGIN/..")
+
+
+def build_cpp() -> list[Path]:
+    return [build_cpp_tests(), build_cpp_bench()]
+
+
 if __name__ == "__main__":
     print(build_library())
-    print(build_cpp_tests())
+    print(build_cpp())

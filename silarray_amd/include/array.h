@@ -89,10 +89,12 @@ namespace detail {
 enum class op : uint8_t {
   leaf,
   add, sub, mul, div, pow,           // binary elementwise
-  sigmoid, relu, sigmoid_backward,   // unary elementwise (+ dout)
+  sigmoid, relu, copy,               // unary elementwise (copy: identity)
+  sigmoid_backward,                  // elementwise (x, dout)
   softmax, layer_norm,               // row ops
   dot, batched_dot, linear, linear_sigmoid,
   sum_axis,
+  view,                              // zero-copy strided view of inputs[0]
 };
 
 inline bool is_elementwise(op o) { return o >= op::add && o <= op::sigmoid_backward; }
@@ -110,6 +112,8 @@ struct node {
 
   float eps = 0.0f;   // layer_norm
   size_t axis = 0;    // sum_axis
+  size_t view_off = 0;  // view: element offset into inputs[0]'s contiguous result
+  int epilogue = 0;     // linear: epilogue fused by the lowering (relu)
 
   static std::shared_ptr<node> leaf(const storage &s, const shape_type &sh, const strides_type &st) {
     auto n = std::make_shared<node>();
@@ -330,6 +334,10 @@ class array {
   // 1-D -> {1, n}; {1, n} -> {n}; 2-D: zero-copy stride swap; 3-D: reversed
   // axes, copied (include/array.h:1051-1099).
   array transpose() const {
+    // A lazy matrix stays in the graph as a transposed view; products read
+    // it in place (transposed operand), elementwise programs by strides.
+    if (node_ && !node_->evaluated && dimension() == 2 && shape_[0] != 1)
+      return permute({1, 0});
     ensure_evaluated_();
     if (dimension() == 1) {
       array tmp = *this;
@@ -541,7 +549,19 @@ class array {
   //----------------------------------------------------------------------------
 
   array dot(const array &rhs) const;
+  // Batched product over the leading axes: {..., M, K} x {..., K, N} ->
+  // {..., M, N} (the reference's {B, M, K} x {B, K, N}, include/array.h:1360-1373,
+  // extended to strided and higher-rank operands).
   array batched_dot(const array &rhs) const;
+
+  // Zero-copy views (no reference counterpart; the reference copies on 3-D
+  // transpose, include/array.h:1079-1096).  Lazy when the array is lazy.
+  //   view(shape)        the same elements under a new contiguous shape
+  //   permute(axes)      axes reordered: result axis i is source axis axes[i]
+  //   select(axis, i)    index i of one axis; that axis is removed
+  array view(const shape_type &shape) const;
+  array permute(const std::vector<size_t> &axes) const;
+  array select(size_t axis, size_t index) const;
   array linear(const array &W, const array &b) const;
 
   array<float> sigmoid() const;
@@ -977,12 +997,109 @@ inline array<T> array<T>::dot(const array &rhs) const {
 template <value_type T>
 inline array<T> array<T>::batched_dot(const array &rhs) const {
   static_assert(std::is_same_v<T, float>, "batched_dot requires float");
-  if (dimension() != 3 || rhs.dimension() != 3)
+  const size_t nd = dimension();
+  if (nd < 3 || rhs.dimension() != nd)
     throw std::runtime_error("batched_dot: requires 3D arrays");
-  if (shape_[0] != rhs.shape_[0] || shape_[2] != rhs.shape_[1])
-    throw std::runtime_error("batched_dot: shape mismatch");
+  for (size_t d = 0; d + 2 < nd; d++)
+    if (shape_[d] != rhs.shape_[d]) throw std::runtime_error("batched_dot: shape mismatch");
+  if (shape_[nd - 1] != rhs.shape_[nd - 2]) throw std::runtime_error("batched_dot: shape mismatch");
+  auto out_shape = shape_;
+  out_shape[nd - 1] = rhs.shape_[nd - 1];
   return from_node_(detail::node::make(detail::op::batched_dot, {to_node_(*this), to_node_(rhs)},
-                                       {shape_[0], shape_[1], rhs.shape_[2]}));
+                                       out_shape));
+}
+
+// A view is (shape, strides, offset) over the contiguous result of a source
+// that is not itself a view, so views of views compose by arithmetic on
+// those three.
+template <value_type T>
+inline array<T> array<T>::view(const shape_type &shape) const {
+  if (shape_count(shape) != element_count())
+    throw std::runtime_error("array: invalid shape for view.");
+  if (node_ && !node_->evaluated) {
+    if (node_->operation == detail::op::view) {
+      if (node_->strides != contiguous_strides(node_->shape)) {
+        // Gather the strided view into a contiguous result first (a copy
+        // node, fused into its producer's or consumer's program).
+        auto c = detail::node::make(detail::op::copy, {node_}, node_->shape);
+        return from_node_(detail::node::make(detail::op::view, {c}, shape));
+      }
+      auto n = detail::node::make(detail::op::view, {node_->inputs[0]}, shape);
+      n->view_off = node_->view_off;
+      return from_node_(std::move(n));
+    }
+    auto n = detail::node::make(detail::op::view, {node_}, shape);
+    return from_node_(std::move(n));
+  }
+  ensure_evaluated_();
+  array src = is_contiguous_() ? *this : materialize_();
+  array tmp = src;
+  tmp.node_.reset();
+  tmp.shape_ = shape;
+  tmp.strides_ = contiguous_strides(shape);
+  return tmp;
+}
+
+template <value_type T>
+inline array<T> array<T>::permute(const std::vector<size_t> &axes) const {
+  if (axes.size() != dimension()) throw std::runtime_error("array: invalid permutation.");
+  std::vector<bool> seen(axes.size(), false);
+  for (auto a : axes) {
+    if (a >= axes.size() || seen[a]) throw std::runtime_error("array: invalid permutation.");
+    seen[a] = true;
+  }
+  auto apply = [&](const shape_type &sh, const strides_type &st, shape_type &nsh,
+                   strides_type &nst) {
+    nsh.resize(axes.size());
+    nst.resize(axes.size());
+    for (size_t i = 0; i < axes.size(); i++) {
+      nsh[i] = sh[axes[i]];
+      nst[i] = st[axes[i]];
+    }
+  };
+  if (node_ && !node_->evaluated) {
+    const bool v = node_->operation == detail::op::view;
+    auto n = std::make_shared<detail::node>();
+    n->operation = detail::op::view;
+    n->inputs[0] = v ? node_->inputs[0] : node_;
+    n->num_inputs = 1;
+    n->view_off = v ? node_->view_off : 0;
+    apply(node_->shape, node_->strides, n->shape, n->strides);
+    return from_node_(std::move(n));
+  }
+  ensure_evaluated_();
+  array tmp = *this;
+  tmp.node_.reset();
+  apply(shape_, strides_, tmp.shape_, tmp.strides_);
+  return tmp;
+}
+
+template <value_type T>
+inline array<T> array<T>::select(size_t axis, size_t index) const {
+  if (axis >= dimension() || index >= shape_[axis])
+    throw std::runtime_error("array: select is out of bounds.");
+  if (node_ && !node_->evaluated) {
+    const bool v = node_->operation == detail::op::view;
+    auto n = std::make_shared<detail::node>();
+    n->operation = detail::op::view;
+    n->inputs[0] = v ? node_->inputs[0] : node_;
+    n->num_inputs = 1;
+    n->view_off = (v ? node_->view_off : 0) + node_->strides[axis] * index;
+    n->shape = node_->shape;
+    n->strides = node_->strides;
+    n->shape.erase(n->shape.begin() + axis);
+    n->strides.erase(n->strides.begin() + axis);
+    if (n->shape.empty()) n->strides = {1};
+    return from_node_(std::move(n));
+  }
+  ensure_evaluated_();
+  array tmp = *this;
+  tmp.node_.reset();
+  tmp.storage_.off = storage_.off + strides_[axis] * index;
+  tmp.shape_.erase(tmp.shape_.begin() + axis);
+  tmp.strides_.erase(tmp.strides_.begin() + axis);
+  if (tmp.shape_.empty()) tmp.strides_ = {1};
+  return tmp;
 }
 
 template <value_type T>
@@ -1363,7 +1480,8 @@ struct program_builder {
   // Sethi-Ullman register need of the fused subtree at n.
   int need(node *n) const {
     if (!fused->count(n)) return 1;
-    if (n->operation == op::sigmoid || n->operation == op::relu) return need(n->inputs[0].get());
+    if (n->operation == op::sigmoid || n->operation == op::relu || n->operation == op::copy)
+      return need(n->inputs[0].get());
     int a = need(n->inputs[0].get()), b = need(n->inputs[1].get());
     return a == b ? a + 1 : std::max(a, b);
   }
@@ -1376,6 +1494,7 @@ struct program_builder {
       return r;
     }
     const op o = n->operation;
+    if (o == op::copy) return value(n->inputs[0].get());
     if (o == op::sigmoid || o == op::relu) {
       int r = value(n->inputs[0].get());
       emit(o == op::sigmoid ? SILGPU_PI_SIGMOID : SILGPU_PI_RELU, r, r);
@@ -1521,7 +1640,9 @@ inline void eval_linear(node *n, bool with_sigmoid) {
     auto bias = contiguous(b);
     gpu::gemm_(A.arr.storage_ref(), B.arr.storage_ref(), out, M, N, K, A.ld, B.ld, A.trans,
                B.trans, 1, 0, 0, 0, &bias.storage_ref(), bl,
-               with_sigmoid ? SILGPU_EPI_BIAS_SIGMOID : SILGPU_EPI_BIAS);
+               with_sigmoid ? SILGPU_EPI_BIAS_SIGMOID
+               : n->epilogue == SILGPU_EPI_BIAS_RELU ? SILGPU_EPI_BIAS_RELU
+                                                      : SILGPU_EPI_BIAS);
     finish(n, std::move(out));
     return;
   }
@@ -1538,10 +1659,90 @@ inline void eval_linear(node *n, bool with_sigmoid) {
   pb.emit(SILGPU_PI_LOAD, rb, pb.slot(b));
   pb.emit(SILGPU_PI_ADD, r, r, rb);
   if (with_sigmoid) pb.emit(SILGPU_PI_SIGMOID, r, r);
+  if (n->epilogue == SILGPU_EPI_BIAS_RELU) pb.emit(SILGPU_PI_RELU, r, r);
   pb.p.out_reg = r;
   auto res = new_output(n->shape);
   gpu::program(pb.p, res);
   finish(n, std::move(res));
+}
+
+// Matrix layout of the last two axes of an operand view: row-major with
+// leading dimension ld, or transposed (column-major) with leading dimension
+// ld; false if neither (the operand is then copied).
+inline bool mat_layout(const node *x, size_t rows, size_t cols, size_t &ld, bool &trans) {
+  const size_t nd = x->shape.size();
+  const size_t sr = x->strides[nd - 2], sc = x->strides[nd - 1];
+  if ((sc == 1 || cols == 1) && sr >= cols && sr > 0) {
+    ld = sr;
+    trans = false;
+    return true;
+  }
+  if ((sr == 1 || rows == 1) && sc >= rows && sc > 0) {
+    ld = sc;
+    trans = true;
+    return true;
+  }
+  return false;
+}
+
+// {..., M, K} x {..., K, N}.  The leading axes that both operands stride
+// uniformly become one batched launch; the rest are looped over.
+inline void eval_batched(node *n) {
+  node *l = n->inputs[0].get(), *r = n->inputs[1].get();
+  const size_t nd = n->shape.size(), L = nd - 2;
+  const size_t M = n->shape[nd - 2], N = n->shape[nd - 1], K = l->shape[nd - 1];
+  std::shared_ptr<node> lc, rc;  // contiguous copies when a layout is not usable
+  size_t lda, ldb;
+  bool ta, tb;
+  if (!mat_layout(l, M, K, lda, ta)) {
+    auto c = contiguous(l);
+    lc = node::leaf(c.storage_ref(), l->shape, contiguous_strides(l->shape));
+    l = lc.get();
+    mat_layout(l, M, K, lda, ta);
+  }
+  if (!mat_layout(r, K, N, ldb, tb)) {
+    auto c = contiguous(r);
+    rc = node::leaf(c.storage_ref(), r->shape, contiguous_strides(r->shape));
+    r = rc.get();
+    mat_layout(r, K, N, ldb, tb);
+  }
+  // Fold leading axes from the innermost outwards while both operands
+  // stride them uniformly (stride[d] == stride[d+1] * extent[d+1]).
+  size_t inner = L;  // axes [inner, L) form the batch
+  size_t batch = 1;
+  if (L > 0) {
+    inner = L - 1;
+    batch = n->shape[L - 1];
+    while (inner > 0) {
+      const size_t d = inner - 1;
+      const bool ul = l->strides[d] == l->strides[d + 1] * l->shape[d + 1];
+      const bool ur = r->strides[d] == r->strides[d + 1] * r->shape[d + 1];
+      if (!ul || !ur) break;
+      batch *= n->shape[d];
+      inner = d;
+    }
+  }
+  const size_t sa = L > 0 ? l->strides[L - 1] : 0, sb = L > 0 ? r->strides[L - 1] : 0;
+  auto out = new_output(n->shape);
+  size_t outer = 1;
+  for (size_t d = 0; d < inner; d++) outer *= n->shape[d];
+  for (size_t o = 0; o < outer; o++) {
+    size_t rem = o, offa = 0, offb = 0;
+    for (size_t d = inner; d-- > 0;) {
+      const size_t idx = rem % n->shape[d];
+      rem /= n->shape[d];
+      offa += idx * l->strides[d];
+      offb += idx * r->strides[d];
+    }
+    storage A = l->data, B = r->data, C = out;
+    A.off += offa;
+    B.off += offb;
+    C.off += o * batch * M * N;
+    C.len = batch * M * N;
+    gpu::gemm_(A, B, C, M, N, K, lda, ldb, ta, tb, batch, sa, sb, M * N, nullptr, 0,
+               SILGPU_EPI_NONE);
+  }
+  finish(n, std::move(out));
 }
 
 inline void eval_node_nonfused(node *n) {
@@ -1549,15 +1750,19 @@ inline void eval_node_nonfused(node *n) {
     case op::dot:
       eval_dot(n);
       return;
-    case op::batched_dot: {
-      auto a = contiguous(n->inputs[0].get());
-      auto b = contiguous(n->inputs[1].get());
-      const size_t Bt = n->shape[0], M = n->shape[1], N = n->shape[2];
-      const size_t K = n->inputs[0]->shape[2];
-      auto out = new_output(n->shape);
-      gpu::gemm_(a.storage_ref(), b.storage_ref(), out, M, N, K, K, N, false, false, Bt, M * K,
-                 K * N, M * N, nullptr, 0, SILGPU_EPI_NONE);
-      finish(n, std::move(out));
+    case op::batched_dot:
+      eval_batched(n);
+      return;
+    case op::view: {
+      node *src = n->inputs[0].get();
+      storage v = src->data;
+      v.off = src->data.off + n->view_off;
+      size_t span = 1;
+      for (size_t d = 0; d < n->shape.size(); d++)
+        if (n->shape[d] > 0) span += (n->shape[d] - 1) * n->strides[d];
+      v.len = shape_count(n->shape) == 0 ? 0 : span;
+      n->data = v;
+      n->evaluated = true;  // shape and strides are the view's own
       return;
     }
     case op::linear:
@@ -1627,17 +1832,21 @@ inline void evaluate(const std::vector<node *> &roots) {
   // Post-order DFS over unevaluated nodes (include/array.h:1945-1971).
   std::vector<node *> order;
   std::unordered_set<node *> seen;
+  // Each root's traversal completes before the next root starts, so a root
+  // that another root consumes is ordered before its consumer.
   std::vector<std::pair<node *, uint8_t>> stack;
-  for (node *r : roots)
-    if (r && !r->evaluated && seen.insert(r).second) stack.push_back({r, 0});
-  while (!stack.empty()) {
-    auto &[cur, idx] = stack.back();
-    if (idx < cur->num_inputs) {
-      node *c = cur->inputs[idx++].get();
-      if (c && !c->evaluated && seen.insert(c).second) stack.push_back({c, 0});
-    } else {
-      order.push_back(cur);
-      stack.pop_back();
+  for (node *r : roots) {
+    if (!r || r->evaluated || !seen.insert(r).second) continue;
+    stack.push_back({r, 0});
+    while (!stack.empty()) {
+      auto &[cur, idx] = stack.back();
+      if (idx < cur->num_inputs) {
+        node *c = cur->inputs[idx++].get();
+        if (c && !c->evaluated && seen.insert(c).second) stack.push_back({c, 0});
+      } else {
+        order.push_back(cur);
+        stack.pop_back();
+      }
     }
   }
   // Consumers inside this graph, and the single consumer where there is one.
@@ -1652,6 +1861,18 @@ inline void evaluate(const std::vector<node *> &roots) {
       }
     }
   const std::unordered_set<node *> root_set(roots.begin(), roots.end());
+  // relu(linear(x, W, b)) with the linear node used only there: the relu
+  // runs in the GEMM epilogue and the relu node takes the product's result.
+  std::unordered_set<node *> relu_fused;
+  for (node *n : order) {
+    if (n->operation != op::relu) continue;
+    node *c = n->inputs[0].get();
+    if (c->evaluated || c->operation != op::linear || root_set.count(c)) continue;
+    if (consumers[c] != 1 || n->inputs[0].use_count() != 1) continue;
+    if (shape_count(c->inputs[2]->shape) == 0 || c->inputs[2]->shape.size() > 1) continue;
+    c->epilogue = SILGPU_EPI_BIAS_RELU;
+    relu_fused.insert(n);
+  }
   // A node is computed inside its consumer's program when it is elementwise,
   // has exactly one consumer, that consumer is elementwise, it is not a root
   // and no array outside the graph holds it.
@@ -1668,6 +1889,13 @@ inline void evaluate(const std::vector<node *> &roots) {
   };
   for (node *n : order) {
     if (n->evaluated) continue;
+    if (relu_fused.count(n)) {
+      node *c = n->inputs[0].get();
+      n->data = c->data;
+      n->strides = c->strides;
+      n->evaluated = true;
+      continue;
+    }
     if (!is_elementwise(n->operation)) {
       eval_node_nonfused(n);
     } else if (fusable(n)) {

@@ -16,7 +16,9 @@
 // in `off`/`len`, as in the reference.  Raw users of `data` (the reference's
 // boundary tests write into storage::make()'s buffer and call gpu:: directly)
 // start in the host-valid state, so the first kernel that reads the storage
-// uploads it; synchronize() downloads every storage a kernel has written.
+// uploads it; synchronize() downloads every such raw storage a kernel has
+// written.  Array-owned blocks are downloaded only when the host reads them
+// (buffer_data, at, iteration), so synchronize() costs no copies for them.
 
 #include <cstddef>
 #include <cstdint>
@@ -49,9 +51,9 @@ inline void ensure_init() {
 
 struct block;
 
-// Blocks whose device copy is newer than the host mirror; synchronize()
-// downloads them (reference semantics: after synchronize the host sees
-// every result).
+// Raw blocks (storage::make) whose device copy is newer than the host
+// mirror; synchronize() downloads them (reference semantics: after
+// synchronize the host sees every result through `data`).
 struct dirty_set {
   std::mutex mu;
   std::unordered_set<block *> blocks;
@@ -68,12 +70,15 @@ struct block {
   // Neither valid: a fresh block whose content nobody has written yet.
   bool host_valid = false;
   bool dev_valid = false;
+  // Handed out through storage::make(): the caller may read `data` directly
+  // after synchronize(), so kernel writes are tracked for download.
+  bool raw = false;
 
   explicit block(size_t n) : bytes(n) {}
   block(const block &) = delete;
   block &operator=(const block &) = delete;
   ~block() {
-    {
+    if (raw) {
       auto &d = dirty_set::instance();
       std::lock_guard<std::mutex> lk(d.mu);
       d.blocks.erase(this);
@@ -137,11 +142,13 @@ struct block {
   }
 
   void mark_dirty() {
+    if (!raw) return;
     auto &d = dirty_set::instance();
     std::lock_guard<std::mutex> lk(d.mu);
     d.blocks.insert(this);
   }
   void unmark_dirty() {
+    if (!raw) return;
     auto &d = dirty_set::instance();
     std::lock_guard<std::mutex> lk(d.mu);
     d.blocks.erase(this);
@@ -167,6 +174,7 @@ struct storage {
   static storage make(size_t bytes) {
     storage s;
     s.buf = std::make_shared<detail::block>(bytes);
+    s.buf->raw = true;
     s.buf->host_read();
     s.data = s.buf->host;
     return s;

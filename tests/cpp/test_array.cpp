@@ -10,6 +10,7 @@
 #include <cstring>
 #include <numeric>
 #include <ranges>
+#include <utility>
 #include <vector>
 
 #include "harness.h"
@@ -412,6 +413,113 @@ TEST_CASE("arrays held outside the graph are materialised") {
   bool ok = true;
   for (size_t i = 0; i < 1000; i++) ok = ok && (y.at(i) == x.at(i) * 2.0f) && (z.at(i) == y.at(i) + 1.0f);
   CHECK(ok);
+}
+
+TEST_CASE("eval of a root that another root consumes") {
+  // Both roots are products; the second consumes the first, so the first
+  // must be computed before it even though both are requested together.
+  auto x = array<float>({2, 3}, std::vector<float>{1, 2, 3, 4, 5, 6});
+  auto W = array<float>({3, 2}, std::vector<float>{1, 2, 3, 4, 5, 6});
+  auto W2 = array<float>({2, 1}, std::vector<float>{1, -1});
+  auto a = x.dot(W);
+  auto b = a.dot(W2);
+  eval(a, b);
+  CHECK(array_equal(a, {{22, 28}, {49, 64}}));
+  CHECK(array_equal(b, {{-6}, {-15}}));
+}
+
+TEST_CASE("product with the transpose of a lazy matrix") {
+  // scores = Q K^T as the reference's transformer writes it
+  // (bench/composite/bench_transformer.cpp:60): K^T stays a lazy view.
+  auto x = random({20, 12});
+  auto Wq = random({12, 8}) - 0.5f, Wk = random({12, 8}) - 0.5f;
+  auto bq = random({8}), bk = random({8});
+  eval(x, Wq, Wk, bq, bk);
+  auto Q = x.linear(Wq, bq);
+  auto K = x.linear(Wk, bk);
+  auto Kt = K.transpose();
+  CHECK(Kt.shape() == (shape_type{8, 20}));
+  auto s = Q.dot(Kt) * 0.5f;
+  eval(s, Q, K);
+  bool ok = true;
+  for (size_t i = 0; i < 20; i++)
+    for (size_t j = 0; j < 20; j++) {
+      double acc = 0;
+      for (size_t e = 0; e < 8; e++) acc += double(Q[i, e]) * double(K[j, e]);
+      ok = ok && std::abs((s[i, j]) - 0.5 * acc) <= 1e-5 * (1 + std::abs(acc));
+    }
+  CHECK(ok);
+}
+
+TEST_CASE("lazy views feed strided batched products") {
+  // qkv [B*S, 3*H*dh] split into heads by view/permute/select, as an
+  // attention block does; every product reads its operand in place.
+  const size_t B = 2, S = 3, H = 2, dh = 4, D = H * dh;
+  auto qkv = random({B * S, 3 * D});
+  auto heads = (qkv * 1.0f).view({B, S, 3, H, dh}).permute({2, 0, 3, 1, 4});
+  CHECK(heads.shape() == (shape_type{3, B, H, S, dh}));
+  auto q = heads.select(0, 0), k = heads.select(0, 1), v = heads.select(0, 2);
+  auto scores = q.batched_dot(k.permute({0, 1, 3, 2}));
+  auto ctx = scores.batched_dot(v);
+  auto merged = ctx.permute({0, 2, 1, 3}).view({B * S, D});
+  eval(scores, merged);
+  CHECK(scores.shape() == (shape_type{B, H, S, S}) && merged.shape() == (shape_type{B * S, D}));
+  const float *p = std::as_const(qkv).buffer_data();
+  const float *ps = std::as_const(scores).buffer_data();
+  auto at = [&](size_t part, size_t b, size_t h, size_t s, size_t e) {
+    return double(p[(b * S + s) * 3 * D + part * D + h * dh + e]);
+  };
+  bool ok = true;
+  for (size_t b = 0; b < B; b++)
+    for (size_t h = 0; h < H; h++)
+      for (size_t i = 0; i < S; i++) {
+        double sc[S];
+        for (size_t j = 0; j < S; j++) {
+          sc[j] = 0;
+          for (size_t e = 0; e < dh; e++) sc[j] += at(0, b, h, i, e) * at(1, b, h, j, e);
+          ok = ok && std::abs(ps[((b * H + h) * S + i) * S + j] - sc[j]) <= 1e-5;
+        }
+        for (size_t e = 0; e < dh; e++) {
+          double c = 0;
+          for (size_t j = 0; j < S; j++) c += sc[j] * at(2, b, h, j, e);
+          ok = ok && std::abs((merged[b * S + i, h * dh + e]) - c) <= 1e-5;
+        }
+      }
+  CHECK(ok);
+}
+
+HOST_CASE("view, permute and select on evaluated arrays") {
+  auto m = array<int>({2, 3, 4}, iota_n(24));
+  auto p = m.permute({2, 0, 1});
+  CHECK(p.shape() == (shape_type{4, 2, 3}));
+  CHECK((p[1, 0, 2]) == (m[0, 2, 1]) && (p[3, 1, 0]) == (m[1, 0, 3]));
+  auto s = m.select(1, 2);
+  CHECK(s.shape() == (shape_type{2, 4}));
+  CHECK(array_equal(s, {{9, 10, 11, 12}, {21, 22, 23, 24}}));
+  auto v = m.view({6, 4});
+  CHECK(v.shape() == (shape_type{6, 4}) && (v[5, 3]) == 24);
+  CHECK_THROWS_WITH(m.view({5, 5}), "array: invalid shape for view.");
+  CHECK_THROWS_WITH(m.permute({0, 0, 1}), "array: invalid permutation.");
+  CHECK_THROWS_WITH(m.select(1, 3), "array: select is out of bounds.");
+}
+
+TEST_CASE("relu of linear runs in the GEMM epilogue") {
+  auto x = random({37, 70}) - 0.5f;
+  auto W = random({70, 45}) - 0.5f;
+  auto b = random({45}) - 0.5f;
+  eval(x, W, b);
+  auto y = x.linear(W, b).relu();
+  auto z = x.linear(W, b);  // unfused twin for the bit-exact comparison
+  eval(y, z);
+  bool ok = true, some_zero = false, some_pos = false;
+  for (size_t i = 0; i < 37; i++)
+    for (size_t j = 0; j < 45; j++) {
+      const float zv = z[i, j], yv = y[i, j];
+      ok = ok && yv == std::max(zv, 0.0f);
+      some_zero = some_zero || yv == 0.0f;
+      some_pos = some_pos || yv > 0.0f;
+    }
+  CHECK(ok && some_zero && some_pos);
 }
 
 //------------------------------------------------------------------------------

@@ -1,0 +1,96 @@
+"""The sil::eval graph benchmark (silarray_amd/bench/bench_graph.cpp): one
+transformer encoder block written against the C++ sil::array API, lowered by
+sil::eval onto the HIP kernels, checked against a float64 numpy restatement of
+the same block.  The block combines every §-row of the hot path the reference
+exposes to a model (examples/transformer_*.cpp use the same operators):
+layer_norm, linear (bias epilogue), strided batched products over head views,
+row softmax, the relu epilogue fusion and fused residual adds."""
+
+from __future__ import annotations
+
+import json
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+BENCH = ROOT / "silarray_amd" / "bench" / "bench_graph"
+
+
+def _bench() -> Path:
+    if not BENCH.exists():
+        pytest.fail(f"{BENCH} is not built (run __graft_entry__.build())")
+    return BENCH
+
+
+def test_usage_without_gpu():
+    proc = subprocess.run([str(_bench()), "no-such-mode"], capture_output=True, text=True,
+                          timeout=60)
+    assert proc.returncode == 2 and "usage" in proc.stderr
+
+
+def test_rejects_bad_head_split():
+    proc = subprocess.run([str(_bench()), "encoder", "1", "8", "30", "4", "16", "1"],
+                          capture_output=True, text=True, timeout=60)
+    assert proc.returncode == 2 and "multiple of H" in proc.stderr
+
+
+def _layer_norm(x, eps=1e-5):
+    mu = x.mean(axis=1, keepdims=True)
+    var = ((x - mu) ** 2).mean(axis=1, keepdims=True)
+    return (x - mu) / np.sqrt(var + eps)
+
+
+def _softmax(x):
+    e = np.exp(x - x.max(axis=-1, keepdims=True))
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+def encoder_f64(p, B, S, D, H, F):
+    """Float64 restatement of the block bench_graph builds (gamma=1, beta=0)."""
+    dh = D // H
+    x = p["x"].reshape(B * S, D)
+    h = _layer_norm(x)
+    qkv = h @ p["Wqkv"].reshape(D, 3 * D) + p["bqkv"]
+    heads = qkv.reshape(B, S, 3, H, dh).transpose(2, 0, 3, 1, 4)
+    q, k, v = heads[0], heads[1], heads[2]
+    scores = (q @ k.transpose(0, 1, 3, 2)) * (1.0 / np.sqrt(np.float32(dh)).astype(np.float64))
+    ctx = _softmax(scores) @ v
+    merged = ctx.transpose(0, 2, 1, 3).reshape(B * S, D)
+    r1 = x + merged @ p["Wo"].reshape(D, D) + p["bo"]
+    ff = np.maximum(_layer_norm(r1) @ p["W1"].reshape(D, F) + p["c1"], 0.0)
+    return r1 + ff @ p["W2"].reshape(F, D) + p["c2"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dims", [(2, 64, 128, 4, 256), (1, 37, 96, 3, 200)])
+def test_encoder_block_matches_f64(tmp_path, dims):
+    B, S, D, H, F = dims
+    print(f"encoder-dump {dims}", flush=True)
+    proc = subprocess.run([str(_bench()), "encoder-dump", *map(str, dims), str(tmp_path)],
+                          capture_output=True, text=True, timeout=120)
+    assert proc.returncode == 0, proc.stderr
+    p = {n: np.fromfile(tmp_path / f"{n}.bin", dtype=np.float32).astype(np.float64)
+         for n in ("x", "Wqkv", "bqkv", "Wo", "bo", "W1", "c1", "W2", "c2")}
+    out = np.fromfile(tmp_path / "out.bin", dtype=np.float32).reshape(B * S, D)
+    ref = encoder_f64(p, B, S, D, H, F)
+    # fp32 products over K <= F with O(1) activations: 1e-5 * sqrt(K) per
+    # product, four products deep, plus the two layer norms.
+    tol = 4e-5 * np.sqrt(max(D, F))
+    err = np.abs(out - ref).max()
+    assert err <= tol, f"max abs error {err:.3e} > {tol:.3e}"
+
+
+@pytest.mark.gpu
+def test_chain_and_encoder_report_json():
+    print("bench_graph chain / encoder (small)", flush=True)
+    out = subprocess.run([str(_bench()), "chain", str(1 << 20), "3"], capture_output=True,
+                         text=True, timeout=120, check=True).stdout
+    rec = json.loads(out.strip().splitlines()[-1])
+    assert rec["workload"] == "affine_chain20" and rec["ms"] > 0
+    out = subprocess.run([str(_bench()), "encoder", "1", "32", "64", "2", "128", "3"],
+                         capture_output=True, text=True, timeout=120, check=True).stdout
+    rec = json.loads(out.strip().splitlines()[-1])
+    assert rec["workload"] == "encoder_block" and rec["ms"] > 0
