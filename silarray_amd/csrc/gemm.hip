@@ -296,17 +296,23 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
 // ---- GEMV: y[1 x N] = x[1 x K] * B[K x N] -----------------------------------
 //
 // HBM-bound: B (K*N floats) is read once.  Pass 1: workgroup (ct, ks) covers
-// 256 columns (one float4 per lane) and rows [ks*kc, (ks+1)*kc); its four
-// wavefronts take interleaved rows with eight 16-byte non-temporal loads in
+// 256 columns (one float4 per lane) and rows [ks*kc, (ks+1)*kc); its eight
+// wavefronts take interleaved rows with four 16-byte non-temporal loads in
 // flight per lane, add their results in LDS and write one partial row
 // partial[ks][ct*256 ..] to scratch.  The K split gives ~1024 workgroups to
-// fill the GPU.  Pass 2 adds the partials per column in split order.  (An
-// in-kernel finish needs agent-scope fences or device-coherent stores and
-// measured slower on MI355X than the second launch.)
-constexpr int kGemvBlock = 256;
+// fill the GPU.  Pass 2 adds the partials per column.  Finishing inside
+// pass 1 was measured on MI355X at 1x4096x4096 and lost every time: the
+// last-workgroup pattern needs agent-scope fences (58 us per call), a packed
+// (count, sum) compare-and-swap per column serialises at the memory-side
+// atomic unit (50-300 us), and zero-fill + atomicAdd costs a launch as well
+// (16.1 us); the second launch costs ~2 us.
+constexpr int kGemvBlock = 256;  // finish kernels
 constexpr int kGemvWaves = kGemvBlock / kWave;
+constexpr int kGemvPartWaves = 8;  // partial kernel: 8 waves x 4 loads in flight
+constexpr int kGemvPartBlock = kGemvPartWaves * kWave;
 constexpr int kGemvCols = 256;  // columns per workgroup (64 lanes x float4)
-constexpr int kGemvUnroll = 8;
+constexpr int kGemvUnroll = 4;
+constexpr int kGemvFinishLoads = 16;  // partial rows in flight per lane in pass 2
 
 __device__ __forceinline__ float4 load_nt4(const float *p) {
   const float4 *q = reinterpret_cast<const float4 *>(p);
@@ -321,12 +327,12 @@ __device__ __forceinline__ float4 load_nt4(const float *p) {
 // VEC: N % 4 == 0, ldb % 4 == 0, B 16-byte aligned; lane owns 4 adjacent
 // columns.  !VEC: lane owns columns c0 + lane + 64*q, q < 4.
 template <bool VEC>
-__global__ __launch_bounds__(kGemvBlock) void gemv_part_k(const float *__restrict__ x,
-                                                          const float *__restrict__ Bm,
-                                                          int64_t ldb, int64_t N, int64_t K,
-                                                          int64_t kc,
-                                                          float *__restrict__ partial) {
-  __shared__ float4 red[kGemvWaves][kWave];
+__global__ __launch_bounds__(kGemvPartBlock) void gemv_part_k(const float *__restrict__ x,
+                                                              const float *__restrict__ Bm,
+                                                              int64_t ldb, int64_t N, int64_t K,
+                                                              int64_t kc,
+                                                              float *__restrict__ partial) {
+  __shared__ float4 red[kGemvPartWaves][kWave];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int64_t c0 = int64_t(blockIdx.x) * kGemvCols;
   const int64_t k0 = int64_t(blockIdx.y) * kc;
@@ -337,7 +343,7 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_part_k(const float *__restric
     if (col < N) {
       const float *bp = Bm + col;
       int64_t k = k0 + wave;
-      constexpr int U = kGemvUnroll, W = kGemvWaves;
+      constexpr int U = kGemvUnroll, W = kGemvPartWaves;
       for (; k + (U - 1) * W < k1; k += U * W) {
         float4 v[U];
         float xv[U];
@@ -364,7 +370,7 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_part_k(const float *__restric
       }
     }
   } else {
-    for (int64_t k = k0 + wave; k < k1; k += kGemvWaves) {
+    for (int64_t k = k0 + wave; k < k1; k += kGemvPartWaves) {
       const float xv = x[k];
       const float *row = Bm + k * ldb;
       const int64_t c = c0 + lane;
@@ -378,7 +384,7 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_part_k(const float *__restric
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
-  for (int w = 1; w < kGemvWaves; ++w) {
+  for (int w = 1; w < kGemvPartWaves; ++w) {
     float4 o = red[w][lane];
     acc.x += o.x;
     acc.y += o.y;
@@ -390,9 +396,9 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_part_k(const float *__restric
   reinterpret_cast<float4 *>(prow)[lane] = acc;
 }
 
-// Pass 2: 64 columns per workgroup, the four wavefronts split the K splits.
-// Partial slot q of lane l in tile ct maps to column c0 + 4l + q (VEC) or
-// c0 + l + 64q (!VEC).
+// Pass 2 (used for !VEC): 64 columns per workgroup, the four wavefronts split
+// the K splits.  Partial slot q of lane l in tile ct maps to column
+// c0 + 4l + q (VEC) or c0 + l + 64q (!VEC).
 template <bool VEC>
 __global__ __launch_bounds__(kGemvBlock) void gemv_finish_k(const float *__restrict__ partial,
                                                             int64_t ks, int64_t pitch,
@@ -422,6 +428,55 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_finish_k(const float *__restr
   const int64_t ct = slot / kGemvCols, within = slot % kGemvCols;
   const int64_t col = VEC ? slot : ct * kGemvCols + (within % 4) * 64 + within / 4;
   if (col < N) y[col] = s;
+}
+
+// Pass 2 for VEC: 256 columns per workgroup as float4 lanes; the four
+// wavefronts take partial rows w, w+4, ... with kGemvFinishLoads loads in
+// flight per lane, so the pass costs about one memory latency.
+// EXACT: ks == kGemvFinishLoads * kGemvWaves (the usual 64 splits), so every
+// lane issues its loads unguarded in one group.
+template <bool EXACT>
+__global__ __launch_bounds__(kGemvBlock) void gemv_finish_vec_k(const float *__restrict__ partial,
+                                                                int64_t ks, int64_t pitch,
+                                                                int64_t N, float *__restrict__ y) {
+  __shared__ float4 red[kGemvWaves][kWave];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int64_t col = int64_t(blockIdx.x) * kGemvCols + lane * 4;  // < pitch
+  constexpr int G = kGemvFinishLoads;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int64_t j0 = wave; j0 < ks; j0 += int64_t(G) * kGemvWaves) {
+    float4 v[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t j = j0 + int64_t(g) * kGemvWaves;
+      v[g] = (EXACT || j < ks) ? *reinterpret_cast<const float4 *>(partial + j * pitch + col)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      s.x += v[g].x;
+      s.y += v[g].y;
+      s.z += v[g].z;
+      s.w += v[g].w;
+    }
+  }
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 1; w < kGemvWaves; ++w) {
+    const float4 o = red[w][lane];
+    s.x += o.x;
+    s.y += o.y;
+    s.z += o.z;
+    s.w += o.w;
+  }
+  if (col < N) {  // N % 4 == 0: the four columns are in range together
+    y[col] = s.x;
+    y[col + 1] = s.y;
+    y[col + 2] = s.z;
+    y[col + 3] = s.w;
+  }
 }
 
 // y[n] = sum_k x[k] * R[n*ldr + k]: one wavefront per output (rows of R
@@ -679,15 +734,20 @@ int launch_gemv_n(const float *x, const float *Bm, int64_t ldb, float *y, int64_
   float *partial = static_cast<float *>(c->partials);
   dim3 grid(static_cast<unsigned>(ct), static_cast<unsigned>(ks));
   if (vec)
-    gemv_part_k<true><<<grid, kGemvBlock, 0, c->stream>>>(x, Bm, ldb, N, K, kc, partial);
+    gemv_part_k<true><<<grid, kGemvPartBlock, 0, c->stream>>>(x, Bm, ldb, N, K, kc, partial);
   else
-    gemv_part_k<false><<<grid, kGemvBlock, 0, c->stream>>>(x, Bm, ldb, N, K, kc, partial);
+    gemv_part_k<false><<<grid, kGemvPartBlock, 0, c->stream>>>(x, Bm, ldb, N, K, kc, partial);
   SILGPU_LAUNCH_CHECK("gemv_part_k");
-  const unsigned fgrid = static_cast<unsigned>(cdiv(pitch, kWave));
-  if (vec)
-    gemv_finish_k<true><<<fgrid, kGemvBlock, 0, c->stream>>>(partial, ks, pitch, N, y);
-  else
+  if (vec && ks == int64_t(kGemvFinishLoads) * kGemvWaves) {
+    gemv_finish_vec_k<true><<<static_cast<unsigned>(ct), kGemvBlock, 0, c->stream>>>(
+        partial, ks, pitch, N, y);
+  } else if (vec) {
+    gemv_finish_vec_k<false><<<static_cast<unsigned>(ct), kGemvBlock, 0, c->stream>>>(
+        partial, ks, pitch, N, y);
+  } else {
+    const unsigned fgrid = static_cast<unsigned>(cdiv(pitch, kWave));
     gemv_finish_k<false><<<fgrid, kGemvBlock, 0, c->stream>>>(partial, ks, pitch, N, y);
+  }
   SILGPU_LAUNCH_CHECK("gemv_finish_k");
   return SILGPU_OK;
 }

@@ -350,29 +350,30 @@ __global__ __launch_bounds__(kBlock) void argmax_k(const float *__restrict__ x, 
   const int64_t c1 = c0 + chunk < cols ? c0 + chunk : cols;
   vi best{NAN, 0, kNoIndex};
   if (vec) {
+    // Compare each float4 group by its maximum (three fmaxf, which drop
+    // NaN) and, only when the group improves on the best so far (a branch
+    // the wavefront rarely takes once its maximum has settled), locate the
+    // first lane holding that maximum.  Groups are visited in increasing
+    // order and replace the best only when strictly larger, so the first
+    // maximum of this thread's columns wins, as in scan1.
     const float4 *r4 = reinterpret_cast<const float4 *>(row);
     int64_t i = c0 / 4 + threadIdx.x;
     const int64_t e4 = c1 / 4;
+    auto scan4 = [&](const float4 &v, int64_t g) {
+      const float m = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
+      if (m > best.v || (best.v != best.v && m == m)) {
+        const int j = v.x == m ? 0 : v.y == m ? 1 : v.z == m ? 2 : 3;
+        best = vi{m, 0, g * 4 + j};
+      }
+    };
     for (; i + (kUnroll - 1) * kBlock < e4; i += kUnroll * kBlock) {
       float4 v[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) v[u] = load_nt(r4 + i + u * kBlock);
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int64_t b = (i + u * kBlock) * 4;
-        scan1(best, v[u].x, b);
-        scan1(best, v[u].y, b + 1);
-        scan1(best, v[u].z, b + 2);
-        scan1(best, v[u].w, b + 3);
-      }
+      for (int u = 0; u < kUnroll; ++u) scan4(v[u], i + u * kBlock);
     }
-    for (; i < e4; i += kBlock) {
-      float4 v = load_nt(r4 + i);
-      scan1(best, v.x, i * 4);
-      scan1(best, v.y, i * 4 + 1);
-      scan1(best, v.z, i * 4 + 2);
-      scan1(best, v.w, i * 4 + 3);
-    }
+    for (; i < e4; i += kBlock) scan4(load_nt(r4 + i), i);
   } else {
     for (int64_t i = c0 + threadIdx.x; i < c1; i += kBlock) scan1(best, row[i], i);
   }

@@ -2,11 +2,12 @@
 //
 // Both are HBM-bound: the optimum is one read and one write of the array
 // (8 bytes per element).  A row of up to 16384 floats is held in registers
-// by one workgroup (256 threads x up to 16 float4) or, for rows up to 2048,
-// by one wavefront, so the row is read from HBM exactly once and every
+// by one workgroup (256 or 512 threads x up to 8 float4) or, for rows up to
+// 2048, by one wavefront, so the row is read from HBM exactly once and every
 // reduction (max, sum, mean, variance) runs over registers with wave64
-// butterflies and one LDS exchange.  Longer rows take a looped variant that
-// reads the row twice.
+// butterflies and one LDS exchange.  Inputs are read and outputs written
+// with non-temporal (streaming) accesses.  Longer rows take a looped variant
+// that reads the row twice.
 //
 // Numerics: softmax subtracts the row maximum and divides by an fp64-
 // accumulated sum; layer_norm uses the two-pass form of cpu::layer_norm
@@ -55,19 +56,24 @@ struct dsum_op {
   __device__ double operator()(double a, double b) const { return a + b; }
 };
 
-// Loads V float4 (VEC) or 4V scalars (!VEC) of row `row` owned by thread
+// Access modes of a row: scalar (any cols, any alignment), float4 with
+// per-slot bounds checks, or float4 over a row that exactly fills the
+// NT x V x 4 register tile (no checks, fewer registers).
+enum row_mode { kScalar = 0, kVec = 1, kFull = 2 };
+
+// Loads V float4 (vector modes) or 4V scalars of row `row` owned by thread
 // `t` of an NT-thread group: element j of slot k is column
 // (k*NT + t)*4 + j.  Columns >= cols read as `pad`.  STREAM: the data is read
 // once (input rows), so non-temporal loads keep it out of the caches;
 // gamma/beta are re-read by every row and use ordinary loads.
-template <int NT, int V, bool VEC, bool STREAM = true>
+template <int NT, int V, int M, bool STREAM = true>
 __device__ __forceinline__ void load_row(const float *__restrict__ row, int64_t cols, int t,
                                          float pad, float (&x)[V][4]) {
 #pragma unroll
   for (int k = 0; k < V; ++k) {
     int64_t c = (int64_t(k) * NT + t) * 4;
-    if constexpr (VEC) {
-      if (c < cols) {
+    if constexpr (M != kScalar) {
+      if (M == kFull || c < cols) {
         const float4 *q = reinterpret_cast<const float4 *>(row) + c / 4;
         float4 v;
         if constexpr (STREAM) {
@@ -92,15 +98,20 @@ __device__ __forceinline__ void load_row(const float *__restrict__ row, int64_t 
   }
 }
 
-template <int NT, int V, bool VEC>
+template <int NT, int V, int M>
 __device__ __forceinline__ void store_row(float *__restrict__ row, int64_t cols, int t,
                                           const float (&y)[V][4]) {
 #pragma unroll
   for (int k = 0; k < V; ++k) {
     int64_t c = (int64_t(k) * NT + t) * 4;
-    if constexpr (VEC) {
-      if (c < cols)
-        reinterpret_cast<float4 *>(row)[c / 4] = make_float4(y[k][0], y[k][1], y[k][2], y[k][3]);
+    if constexpr (M != kScalar) {
+      if (M == kFull || c < cols) {
+        float4 *q = reinterpret_cast<float4 *>(row) + c / 4;
+        __builtin_nontemporal_store(y[k][0], &q->x);
+        __builtin_nontemporal_store(y[k][1], &q->y);
+        __builtin_nontemporal_store(y[k][2], &q->z);
+        __builtin_nontemporal_store(y[k][3], &q->w);
+      }
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -109,18 +120,25 @@ __device__ __forceinline__ void store_row(float *__restrict__ row, int64_t cols,
   }
 }
 
-// Launch shape: NT threads per row, RPB rows per workgroup (NT * RPB <= 256).
-template <int NT, int V, bool VEC>
-__global__ __launch_bounds__(256) void softmax_reg_k(const float *__restrict__ in,
-                                                     float *__restrict__ out, int64_t rows,
-                                                     int64_t cols) {
-  constexpr int RPB = 256 / NT;
+// Launch shape: NT threads per row, RPB rows per workgroup: 256 / NT rows of
+// one wavefront each for NT == 64, one row per workgroup of NT threads
+// otherwise.
+template <int NT>
+constexpr int rows_per_block() { return NT < 256 ? 256 / NT : 1; }
+template <int NT>
+constexpr int row_block() { return NT * rows_per_block<NT>(); }
+
+template <int NT, int V, int M>
+__global__ __launch_bounds__(row_block<NT>()) void softmax_reg_k(const float *__restrict__ in,
+                                                                 float *__restrict__ out,
+                                                                 int64_t rows, int64_t cols) {
+  constexpr int RPB = rows_per_block<NT>();
   const int64_t r = int64_t(blockIdx.x) * RPB + threadIdx.x / NT;
   const int t = threadIdx.x % NT;
   if (NT == kWave && r >= rows) return;  // whole wavefronts exit together
   const float *src = in + r * cols;
   float x[V][4];
-  load_row<NT, V, VEC>(src, cols, t, -INFINITY, x);
+  load_row<NT, V, M>(src, cols, t, -INFINITY, x);
   float m = -INFINITY;
 #pragma unroll
   for (int k = 0; k < V; ++k)
@@ -142,22 +160,19 @@ __global__ __launch_bounds__(256) void softmax_reg_k(const float *__restrict__ i
   for (int k = 0; k < V; ++k)
 #pragma unroll
     for (int j = 0; j < 4; ++j) x[k][j] = x[k][j] / sf;
-  store_row<NT, V, VEC>(out + r * cols, cols, t, x);
+  store_row<NT, V, M>(out + r * cols, cols, t, x);
 }
 
-template <int NT, int V, bool VEC>
-__global__ __launch_bounds__(256) void layer_norm_reg_k(const float *__restrict__ in,
-                                                        float *__restrict__ out,
-                                                        const float *__restrict__ gamma,
-                                                        const float *__restrict__ beta,
-                                                        int64_t rows, int64_t cols,
-                                                        float eps) {
-  constexpr int RPB = 256 / NT;
+template <int NT, int V, int M>
+__global__ __launch_bounds__(row_block<NT>()) void layer_norm_reg_k(
+    const float *__restrict__ in, float *__restrict__ out, const float *__restrict__ gamma,
+    const float *__restrict__ beta, int64_t rows, int64_t cols, float eps) {
+  constexpr int RPB = rows_per_block<NT>();
   const int64_t r = int64_t(blockIdx.x) * RPB + threadIdx.x / NT;
   const int t = threadIdx.x % NT;
   if (NT == kWave && r >= rows) return;
   float x[V][4];
-  load_row<NT, V, VEC>(in + r * cols, cols, t, 0.0f, x);
+  load_row<NT, V, M>(in + r * cols, cols, t, 0.0f, x);
   double s = 0.0;
 #pragma unroll
   for (int k = 0; k < V; ++k)
@@ -173,19 +188,19 @@ __global__ __launch_bounds__(256) void layer_norm_reg_k(const float *__restrict_
       int64_t c = (int64_t(k) * NT + t) * 4 + j;
       float d = x[k][j] - mu;
       x[k][j] = d;
-      if (c < cols) ss += static_cast<double>(d) * static_cast<double>(d);
+      if (M == kFull || c < cols) ss += static_cast<double>(d) * static_cast<double>(d);
     }
   ss = group<NT>::reduce(ss, dsum_op{});
   const float var = static_cast<float>(ss / static_cast<double>(cols));
   const float inv_std = 1.0f / sqrtf(var + eps);
   float g[V][4], b[V][4];
-  load_row<NT, V, VEC, false>(gamma, cols, t, 0.0f, g);
-  load_row<NT, V, VEC, false>(beta, cols, t, 0.0f, b);
+  load_row<NT, V, M, false>(gamma, cols, t, 0.0f, g);
+  load_row<NT, V, M, false>(beta, cols, t, 0.0f, b);
 #pragma unroll
   for (int k = 0; k < V; ++k)
 #pragma unroll
     for (int j = 0; j < 4; ++j) x[k][j] = (x[k][j] * inv_std) * g[k][j] + b[k][j];
-  store_row<NT, V, VEC>(out + r * cols, cols, t, x);
+  store_row<NT, V, M>(out + r * cols, cols, t, x);
 }
 
 // Rows longer than the register path: one workgroup per row, two reads.
@@ -241,43 +256,46 @@ struct row_launch {
   int v;       // float4 slots per thread
 };
 
-// Smallest register configuration that covers `cols`, or {0,0} for the
-// looped kernels.
+// Register configuration that covers `cols`, or {0,0} for the looped
+// kernels.  Rows over 4096 take 512 threads so each thread holds at most
+// 8 float4 (measured on [4096, 8192]: 512 x 4 beats 256 x 8 for layer_norm,
+// whose gamma/beta otherwise double the register footprint).
 row_launch pick(int64_t cols) {
   if (cols <= 256) return {64, 1};
   if (cols <= 512) return {64, 2};
   if (cols <= 1024) return {64, 4};
   if (cols <= 2048) return {64, 8};
   if (cols <= 4096) return {256, 4};
-  if (cols <= 8192) return {256, 8};
-  if (cols <= 16384) return {256, 16};
+  if (cols <= 8192) return {512, 4};
+  if (cols <= 16384) return {512, 8};
   return {0, 0};
 }
 
-template <int NT, int V, bool VEC>
+template <int NT, int V, int M>
 void go_softmax(const float *in, float *out, int64_t rows, int64_t cols, hipStream_t s) {
-  constexpr int RPB = 256 / NT;
-  softmax_reg_k<NT, V, VEC><<<static_cast<unsigned>(cdiv(rows, RPB)), 256, 0, s>>>(in, out,
-                                                                                  rows, cols);
+  constexpr int RPB = rows_per_block<NT>();
+  softmax_reg_k<NT, V, M><<<static_cast<unsigned>(cdiv(rows, RPB)), row_block<NT>(), 0, s>>>(
+      in, out, rows, cols);
 }
 
-template <int NT, int V, bool VEC>
+template <int NT, int V, int M>
 void go_ln(const float *in, float *out, const float *g, const float *b, int64_t rows,
            int64_t cols, float eps, hipStream_t s) {
-  constexpr int RPB = 256 / NT;
-  layer_norm_reg_k<NT, V, VEC><<<static_cast<unsigned>(cdiv(rows, RPB)), 256, 0, s>>>(
-      in, out, g, b, rows, cols, eps);
+  constexpr int RPB = rows_per_block<NT>();
+  layer_norm_reg_k<NT, V, M>
+      <<<static_cast<unsigned>(cdiv(rows, RPB)), row_block<NT>(), 0, s>>>(in, out, g, b, rows,
+                                                                          cols, eps);
 }
 
-#define SILGPU_ROW_DISPATCH(FN, VEC, ...)                                               \
+#define SILGPU_ROW_DISPATCH(FN, MODE, ...)                                               \
   switch (L.nt * 100 + L.v) {                                                           \
-    case 6401: FN<64, 1, VEC>(__VA_ARGS__); break;                                      \
-    case 6402: FN<64, 2, VEC>(__VA_ARGS__); break;                                      \
-    case 6404: FN<64, 4, VEC>(__VA_ARGS__); break;                                      \
-    case 6408: FN<64, 8, VEC>(__VA_ARGS__); break;                                      \
-    case 25604: FN<256, 4, VEC>(__VA_ARGS__); break;                                    \
-    case 25608: FN<256, 8, VEC>(__VA_ARGS__); break;                                    \
-    default: FN<256, 16, VEC>(__VA_ARGS__); break;                                      \
+    case 6401: FN<64, 1, MODE>(__VA_ARGS__); break;                                      \
+    case 6402: FN<64, 2, MODE>(__VA_ARGS__); break;                                      \
+    case 6404: FN<64, 4, MODE>(__VA_ARGS__); break;                                      \
+    case 6408: FN<64, 8, MODE>(__VA_ARGS__); break;                                      \
+    case 25604: FN<256, 4, MODE>(__VA_ARGS__); break;                                    \
+    case 51204: FN<512, 4, MODE>(__VA_ARGS__); break;                                    \
+    default: FN<512, 8, MODE>(__VA_ARGS__); break;                                       \
   }
 
 }  // namespace
@@ -300,11 +318,13 @@ int silgpu_softmax_rows_f32(const float *d_in, float *d_out, int64_t rows, int64
     SILGPU_LAUNCH_CHECK("softmax_loop_k");
     return SILGPU_OK;
   }
-  bool vec = cols % 4 == 0 && aligned16(d_in) && aligned16(d_out);
-  if (vec) {
-    SILGPU_ROW_DISPATCH(go_softmax, true, d_in, d_out, rows, cols, c->stream);
+  const bool vec = cols % 4 == 0 && aligned16(d_in) && aligned16(d_out);
+  if (vec && cols == int64_t(L.nt) * L.v * 4) {
+    SILGPU_ROW_DISPATCH(go_softmax, kFull, d_in, d_out, rows, cols, c->stream);
+  } else if (vec) {
+    SILGPU_ROW_DISPATCH(go_softmax, kVec, d_in, d_out, rows, cols, c->stream);
   } else {
-    SILGPU_ROW_DISPATCH(go_softmax, false, d_in, d_out, rows, cols, c->stream);
+    SILGPU_ROW_DISPATCH(go_softmax, kScalar, d_in, d_out, rows, cols, c->stream);
   }
   SILGPU_LAUNCH_CHECK("softmax_reg_k");
   return SILGPU_OK;
@@ -324,13 +344,16 @@ int silgpu_layer_norm_rows_f32(const float *d_in, float *d_out, const float *d_g
     SILGPU_LAUNCH_CHECK("layer_norm_loop_k");
     return SILGPU_OK;
   }
-  bool vec = cols % 4 == 0 && aligned16(d_in) && aligned16(d_out) && aligned16(d_gamma) &&
-             aligned16(d_beta);
-  if (vec) {
-    SILGPU_ROW_DISPATCH(go_ln, true, d_in, d_out, d_gamma, d_beta, rows, cols, eps,
+  const bool vec = cols % 4 == 0 && aligned16(d_in) && aligned16(d_out) &&
+                   aligned16(d_gamma) && aligned16(d_beta);
+  if (vec && cols == int64_t(L.nt) * L.v * 4) {
+    SILGPU_ROW_DISPATCH(go_ln, kFull, d_in, d_out, d_gamma, d_beta, rows, cols, eps,
+                        c->stream);
+  } else if (vec) {
+    SILGPU_ROW_DISPATCH(go_ln, kVec, d_in, d_out, d_gamma, d_beta, rows, cols, eps,
                         c->stream);
   } else {
-    SILGPU_ROW_DISPATCH(go_ln, false, d_in, d_out, d_gamma, d_beta, rows, cols, eps,
+    SILGPU_ROW_DISPATCH(go_ln, kScalar, d_in, d_out, d_gamma, d_beta, rows, cols, eps,
                         c->stream);
   }
   SILGPU_LAUNCH_CHECK("layer_norm_reg_k");

@@ -277,6 +277,34 @@ def test_argmax_rows(native, oracle, rows, cols):
     assert np.array_equal(down(native, do, rows, np.int32), oracle.argmax_rows(x))
 
 
+def test_argmax_long_row_rules(native, oracle):
+    """Rows long enough for the split float4 kernel: the maximum shares a
+    float4 group with NaN and with a tie, equal maxima sit in different
+    chunks, signed zeros tie, a row is all NaN, and one row is all negative
+    with NaNs."""
+    announce("argmax long-row rules")
+    cols = (1 << 20) + 8
+    g = rng(4242)
+    x = g.uniform(-1, 1, (6, cols)).astype(np.float32)
+    base = 4 * 100003                       # start of a float4 group
+    x[0, base:base + 4] = [np.nan, 7.0, 9.0, 9.0]   # first 9 (lane 2) wins
+    x[1, 17] = 5.0
+    x[1, cols - 3] = 5.0                    # tie in another chunk: 17 wins
+    x[2, :] = 0.0
+    x[2, 5] = -0.0                          # all equal: index 0
+    x[3, :] = np.nan                        # no number: index 0
+    x[4, :] = -np.abs(x[4, :]) - 1.0
+    x[4, ::7] = np.nan
+    x[4, 999_999] = -0.5                    # the largest of a negative row
+    x[5, 3 * (cols // 4) + 1: 3 * (cols // 4) + 3] = [3.0, 3.0]  # tie within a group
+    dx, do = up(native, x), empty(native, 6, np.int32)
+    native.argmax_rows_f32(dx, 6, cols, do)
+    got = down(native, do, 6, np.int32)
+    ref = oracle.argmax_rows(x)
+    assert list(ref) == [base + 2, 17, 0, 0, 999_999, 3 * (cols // 4) + 1]
+    assert np.array_equal(got, ref)
+
+
 def test_argmax_golden_nan_negative(native, oracle, ref_vectors):
     announce("argmax goldens")
     a = np.array(ref_vectors["argmax"]["x"], np.float32)
@@ -291,9 +319,17 @@ def test_argmax_golden_nan_negative(native, oracle, ref_vectors):
 
 # ---- row ops ----------------------------------------------------------------------
 
-@pytest.mark.parametrize("rows,cols", [(2, 3), (64, 32), (4096, 8192), (300, 512), (100, 1000),
-                                       (50, 2048), (33, 3000), (16, 16384), (5, 40000),
-                                       (7, 4097), (1, 1)])
+# Every register configuration in its three modes: rows that exactly fill the
+# tile (256, 512, 1024, 2048, 4096, 8192, 16384), float4 rows with a ragged
+# end (768, 1000, 3000, 6000, 12000), scalar rows (3, 1001, 4097, 6001,
+# 9999), the looped kernel (40000), and row counts that leave a partial
+# workgroup.
+ROW_SHAPES = [(2, 3), (64, 32), (7, 256), (300, 512), (5, 1024), (50, 2048), (9, 4096),
+              (4096, 8192), (3, 16384), (2048, 768), (100, 1000), (33, 3000), (11, 6000),
+              (6, 12000), (9, 1001), (7, 4097), (5, 6001), (4, 9999), (5, 40000), (1, 1)]
+
+
+@pytest.mark.parametrize("rows,cols", ROW_SHAPES)
 def test_softmax_rows(native, oracle, rows, cols):
     announce(f"softmax {rows}x{cols}")
     x = rng(1100 + cols).normal(0, 3, (rows, cols)).astype(np.float32)
@@ -313,8 +349,7 @@ def test_softmax_golden(native, ref_vectors):
     assert np.max(np.abs(down(native, do, 3) - s["expected"])) <= s["tol_abs"]
 
 
-@pytest.mark.parametrize("rows,cols", [(2, 3), (64, 256), (4096, 8192), (2048, 768), (9, 1001),
-                                       (16, 16384), (3, 50000), (1, 1)])
+@pytest.mark.parametrize("rows,cols", ROW_SHAPES + [(3, 50000)])
 def test_layer_norm_rows(native, oracle, rows, cols):
     announce(f"layer_norm {rows}x{cols}")
     g = rng(1200 + cols)
@@ -490,8 +525,11 @@ def test_gemv_config(native, oracle):
     assert np.array_equal(down(native, dy2, 4096), y)
 
 
+# Float4 finish with 64 splits (4096 x 4096), 91 splits over two load
+# groups (1024 x 3000), 32 splits (8192 x 2048) and one split (100 x 5);
+# scalar paths for N % 4 != 0.
 @pytest.mark.parametrize("N,K,ldb", [(4093, 1000, 4093), (100, 5, 128), (4096, 4096, 4100),
-                                     (1, 1, 1)])
+                                     (1024, 3000, 1024), (8192, 2048, 8192), (1, 1, 1)])
 def test_gemv_ragged(native, oracle, N, K, ldb):
     announce(f"gemv N={N} K={K} ldb={ldb}")
     g = rng(1600 + N)
