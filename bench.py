@@ -41,13 +41,17 @@ METRIC = "fp32 SGEMM TFLOPS (8192^3) + GEMV GB/s (1x4096x4096); % of roofline"
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 SEED = 20261201
+# Secondary workloads warm up for at least this long (the GPU leaves its idle
+# clocks within ~0.1 s of sustained work; short kernels would otherwise be
+# timed partly at idle clocks).
+WARM_S = 0.2
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="", help="comma list of workloads (default: all)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -67,10 +71,19 @@ class Timer:
         self.e0 = nat.Event()
         self.e1 = nat.Event()
 
-    def ms_per_launch(self, fn, reps: int, warmup: int = 2) -> float:
-        for i in range(warmup):
+    def warm(self, fn, warmup: int, min_s: float = WARM_S) -> None:
+        """At least `warmup` calls and at least `min_s` seconds of them, so the
+        clocks have left their idle state before anything is timed."""
+        i, t0 = 0, time.perf_counter()
+        while i < warmup or time.perf_counter() - t0 < min_s:
             fn(i)
+            i += 1
+            if i % 16 == 0:
+                self.nat.sync()
         self.nat.sync()
+
+    def ms_per_launch(self, fn, reps: int, warmup: int = 2) -> float:
+        self.warm(fn, warmup)
         self.e0.record()
         for i in range(reps):
             fn(i)
@@ -107,7 +120,8 @@ def normal(g, shape, std):
 
 # ---- workloads -------------------------------------------------------------------
 
-def bench_sgemm(nat, S, steps, warmup, g):
+def bench_sgemm(nat, S, steps, warmup, g, min_warm_s=0.0):
+    """The headline passes min_warm_s=0: exactly `warmup` untimed steps."""
     A = nat.DeviceBuffer.from_array(uniform(g, (S, S)))
     B = nat.DeviceBuffer.from_array(uniform(g, (S, S)))
     C = nat.DeviceBuffer(S * S * 4)
@@ -115,10 +129,8 @@ def bench_sgemm(nat, S, steps, warmup, g):
     def step(_i):
         nat.sgemm(0, 0, S, S, S, A, S, 0, B, S, 0, C, S, 0)
 
-    for i in range(warmup):
-        step(i)
-    nat.sync()
     t = Timer(nat)
+    t.warm(step, warmup, min_warm_s)
     t0 = time.perf_counter()
     t.e0.record()
     for i in range(steps):
@@ -377,7 +389,7 @@ def main():
                                     "us": round(r["us"], 2)}
     if want("sgemm_sweep"):
         for s in (2048, 4096):
-            r = bench_sgemm(nat, s, 10, 3, g)
+            r = bench_sgemm(nat, s, 20, 3, g, min_warm_s=WARM_S)
             log(f"sgemm {s}^3 {r}")
             secondary[f"sgemm_{s}"] = {"value": round(r["tflops_kernel"], 2), "unit": "TFLOP/s",
                                        "roofline": roofline("mfma", r["tflops_kernel"])}

@@ -296,7 +296,7 @@ def sgemm(ta, tb, M, N, K, A, lda, sA, B, ldb, sB, Cm, ldc, sC, batch=1, bias=No
          ldc, sC, batch, vp(bias) if bias is not None else _vp(None), bias_len, epi)
 
 
-TILE_128x128, TILE_64x64, TILE_32x128, TILE_128x64 = 1, 2, 3, 4
+TILE_128x128, TILE_64x64, TILE_32x128, TILE_128x64, TILE_256x256 = 1, 2, 3, 4, 5
 
 
 def sgemm_tuned(ta, tb, M, N, K, A, lda, sA, B, ldb, sB, Cm, ldc, sC, batch=1, bias=None,

@@ -58,10 +58,14 @@ array<float> filled(const shape_type &shape, rng &g, float std, bool uniform = f
   return a;
 }
 
+// At least two untimed runs and at least 0.2 s of them, so the GPU has left
+// its idle clocks before the timed runs.
 template <typename F>
 double median_ms(int reps, F fn) {
-  fn();  // warmup
-  fn();
+  const auto w0 = std::chrono::steady_clock::now();
+  for (int i = 0; i < 2 || std::chrono::steady_clock::now() - w0 < std::chrono::milliseconds(200);
+       i++)
+    fn();
   std::vector<double> t;
   for (int i = 0; i < reps; i++) {
     auto t0 = std::chrono::steady_clock::now();

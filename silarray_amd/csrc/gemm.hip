@@ -1,16 +1,18 @@
 // Matrix products on gfx950: fp32 MFMA SGEMM and HBM-bound GEMV.
 //
 // SGEMM (the reference's STEEL / sgemm_32 / MPS paths, include/gpu.h:509-615,
-// 1296-1328) runs on v_mfma_f32_32x32x2_f32: one instruction multiplies a
-// 32x2 A fragment by a 2x32 B fragment into a 32x32 fp32 accumulator held
-// in 16 registers per lane.  On MI355X this instruction keeps the matrix
-// core busy for 64 cycles, so the kernel's job is to issue one every 64
-// cycles on every SIMD: operands are staged through LDS in k-major tiles
-// (lanes 0-31 read 32 consecutive floats of one k row, lanes 32-63 the
-// next row), the next K tile is fetched into registers while the current
-// one is multiplied (double-buffered LDS, one barrier per K tile), and the
-// workgroup -> tile mapping keeps the workgroups of one XCD on neighbouring
-// tiles so their A and B panels are shared in that XCD's L2.
+// 1296-1328) runs on the fp32 matrix cores: v_mfma_f32_16x16x4_f32 (a 16x4
+// A fragment times a 4x16 B fragment into a 16x16 accumulator of 4 registers
+// per lane) or v_mfma_f32_32x32x2_f32 (32x2 by 2x32 into 32x32, 16
+// registers).  Both keep a SIMD's matrix core busy for 256 flops per cycle
+// per CU, so the kernel's job is to issue one back to back on every SIMD:
+// operands are staged through LDS in k-major tiles, the next K tile is
+// fetched into registers while the current one is multiplied (double-
+// buffered LDS, one barrier per K tile), the fragments of k-step s+1 are read
+// from LDS while the MFMAs of step s run (a scheduling barrier per step keeps
+// the compiler from hoisting further and spilling), and the workgroup -> tile
+// mapping keeps the workgroups of one XCD on neighbouring tiles so their A
+// and B panels are shared in that XCD's L2.
 //
 // Epilogues (bias, sigmoid, relu) are applied to the accumulators before the
 // single store, so linear / linear_sigmoid are one pass over C.
@@ -24,6 +26,33 @@ namespace silgpu {
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// fp32 MFMA shapes.  MI x MI output block, KI k values per instruction.
+//   32x32x2: lane l supplies A[l%32][l/32] and B[l/32][l%32] and holds
+//            C[8*(r/4) + 4*(l/32) + r%4][l%32] in register r < 16;
+//   16x16x4: lane l supplies A[l%16][l/16] and B[l/16][l%16] and holds
+//            C[4*(l/16) + r][l%16] in register r < 4.
+template <int MI>
+struct mfma;
+template <>
+struct mfma<32> {
+  static constexpr int KI = 2, R = 16;
+  typedef floatx16 acc_t;
+  __device__ static acc_t run(float a, float b, acc_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+  __device__ static int row(int lane, int r) { return 8 * (r / 4) + 4 * (lane / 32) + (r % 4); }
+};
+template <>
+struct mfma<16> {
+  static constexpr int KI = 4, R = 4;
+  typedef floatx4 acc_t;
+  __device__ static acc_t run(float a, float b, acc_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+  __device__ static int row(int lane, int r) { return 4 * (lane / 16) + r; }
+};
 
 // ---- tile mapping -----------------------------------------------------------
 
@@ -68,11 +97,11 @@ struct gemm_args {
   float *ws;
 };
 
-template <int BM, int BN, int BK, int WM, int WN>
+template <int BM, int BN, int BK, int WM, int WN, int MI>
 struct cfg {
   static constexpr int kThreads = WM * WN * kWave;
-  static constexpr int TM = BM / WM / 32;  // 32x32 MFMA blocks per wave along M
-  static constexpr int TN = BN / WN / 32;
+  static constexpr int TM = BM / WM / MI;  // MFMA blocks per wave along M
+  static constexpr int TN = BN / WN / MI;
   static constexpr int LA = BM + 4;        // LDS row pitch (floats), padded
   static constexpr int LB = BN + 4;
   static constexpr int kAStage = BK * LA;  // floats per stage
@@ -80,11 +109,12 @@ struct cfg {
   static constexpr int kLdsBytes = 2 * (kAStage + kBStage) * 4;
   static constexpr int NA = BM * BK / 4 / kThreads;  // 4-float groups per thread
   static constexpr int NB = BK * BN / 4 / kThreads;
-  static_assert(TM >= 1 && TN >= 1, "wave tile below 32x32");
+  static_assert(TM >= 1 && TN >= 1 && TM * WM * MI == BM && TN * WN * MI == BN,
+                "wave tile not a whole number of MFMA blocks");
   static_assert(NA >= 1 && NB >= 1 && NA * 4 * kThreads == BM * BK &&
                     NB * 4 * kThreads == BK * BN,
                 "tile not divisible among threads");
-  static_assert(BK % 4 == 0 && BK % 2 == 0, "BK");
+  static_assert(BK % 4 == 0 && BK % mfma<MI>::KI == 0, "BK");
 };
 
 // Loads this thread's share of an R x Cc tile whose *contiguous* global axis
@@ -146,9 +176,10 @@ __device__ __forceinline__ void store_groups(float *__restrict__ S, int t,
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VEC, bool EDGE>
+template <int BM, int BN, int BK, int WM, int WN, int MI, bool TA, bool TB, bool VEC, bool EDGE>
 __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
-  using C = cfg<BM, BN, BK, WM, WN>;
+  using C = cfg<BM, BN, BK, WM, WN, MI>;
+  using F = mfma<MI>;
   constexpr int NT = C::kThreads;
   extern __shared__ float lds[];
   float *As = lds;                    // [2][BK][LA]
@@ -168,13 +199,13 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
   float *__restrict__ Cp = p.C + z * p.sC;
   const int M = p.M, N = p.N, K = p.K;
 
-  floatx16 acc[C::TM][C::TN];
+  typename F::acc_t acc[C::TM][C::TN];
 #pragma unroll
   for (int i = 0; i < C::TM; ++i)
 #pragma unroll
     for (int j = 0; j < C::TN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+      for (int r = 0; r < F::R; ++r) acc[i][j][r] = 0.0f;
 
   float ga[C::NA][4], gb[C::NB][4];
   // Global views: A non-trans is [M][K] (contiguous K), trans is [K][M].
@@ -209,10 +240,10 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
   const int kbeg = blockIdx.y * p.klen;
   const int kend = min(K, kbeg + p.klen);
   const int KT = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
-  const int khalf = lane / 32;  // which k of the pair this lane supplies
-  const int l32 = lane % 32;
-  const int a_col = wm * C::TM * 32 + l32;
-  const int b_col = wn * C::TN * 32 + l32;
+  const int kl = lane / MI;  // which k of the instruction this lane supplies
+  const int lm = lane % MI;  // its row of A / column of B within a block
+  const int a_col = wm * C::TM * MI + lm;
+  const int b_col = wn * C::TN * MI + lm;
 
   if (KT > 0) {
     load_a(kbeg);
@@ -228,20 +259,29 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
       load_a(kbeg + (kt + 1) * BK);
       load_b(kbeg + (kt + 1) * BK);
     }
-    const float *Sa = As + cur * C::kAStage + khalf * C::LA + a_col;
-    const float *Sb = Bs + cur * C::kBStage + khalf * C::LB + b_col;
+    const float *Sa = As + cur * C::kAStage + kl * C::LA + a_col;
+    const float *Sb = Bs + cur * C::kBStage + kl * C::LB + b_col;
+    // Fragments of k-step s+1 are read while the MFMAs of step s run.
+    constexpr int S = BK / F::KI;
+    float a[2][C::TM], b[2][C::TN];
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 2) {
-      float a[C::TM], b[C::TN];
+    for (int i = 0; i < C::TM; ++i) a[0][i] = Sa[i * MI];
 #pragma unroll
-      for (int i = 0; i < C::TM; ++i) a[i] = Sa[kk * C::LA + i * 32];
+    for (int j = 0; j < C::TN; ++j) b[0][j] = Sb[j * MI];
 #pragma unroll
-      for (int j = 0; j < C::TN; ++j) b[j] = Sb[kk * C::LB + j * 32];
+    for (int st = 0; st < S; ++st) {
+      const int cf = st & 1, nf = cf ^ 1;
+      if (st + 1 < S) {
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i) a[nf][i] = Sa[(F::KI * (st + 1)) * C::LA + i * MI];
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) b[nf][j] = Sb[(F::KI * (st + 1)) * C::LB + j * MI];
+      }
 #pragma unroll
       for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-        for (int j = 0; j < C::TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < C::TN; ++j) acc[i][j] = F::run(a[cf][i], b[cf][j], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (more) {
       store_a(cur ^ 1);
@@ -251,20 +291,20 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
   }
 
   // Epilogue.  Accumulator register r of lane l in block (i, j) is
-  // C[row][col] with col = 32j + l%32 and row = 32i + 8*(r/4) + 4*(l/32) + r%4
+  // C[row][col] with col = MI*j + l%MI and row = MI*i + F::row(l, r)
   // (relative to the wave tile).
   const int epi = p.epi;
   if (gridDim.y > 1) {
     float *W = p.ws + int64_t(blockIdx.y) * M * N;
 #pragma unroll
     for (int j = 0; j < C::TN; ++j) {
-      const int col = n0 + wn * C::TN * 32 + j * 32 + l32;
+      const int col = n0 + wn * C::TN * MI + j * MI + lm;
       if (EDGE && col >= N) continue;
 #pragma unroll
       for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + wm * C::TM * 32 + i * 32 + 8 * (r / 4) + 4 * khalf + (r % 4);
+        for (int r = 0; r < F::R; ++r) {
+          const int row = m0 + wm * C::TM * MI + i * MI + F::row(lane, r);
           if (EDGE && row >= M) continue;
           W[int64_t(row) * N + col] = acc[i][j][r];
         }
@@ -273,7 +313,7 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
   }
 #pragma unroll
   for (int j = 0; j < C::TN; ++j) {
-    const int col = n0 + wn * C::TN * 32 + j * 32 + l32;
+    const int col = n0 + wn * C::TN * MI + j * MI + lm;
     if (EDGE && col >= N) continue;
     float bv = 0.0f;
     if (epi == SILGPU_EPI_BIAS || epi == SILGPU_EPI_BIAS_SIGMOID || epi == SILGPU_EPI_BIAS_RELU)
@@ -281,8 +321,8 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
 #pragma unroll
     for (int i = 0; i < C::TM; ++i) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * C::TM * 32 + i * 32 + 8 * (r / 4) + 4 * khalf + (r % 4);
+      for (int r = 0; r < F::R; ++r) {
+        const int row = m0 + wm * C::TM * MI + i * MI + F::row(lane, r);
         if (EDGE && row >= M) continue;
         float v = acc[i][j][r] + bv;
         if (epi == SILGPU_EPI_BIAS_SIGMOID) v = sigmoidf_dev(v);
@@ -529,10 +569,10 @@ __global__ __launch_bounds__(256) void epilogue_k(float *__restrict__ C, int64_t
 
 // ---- host dispatch ----------------------------------------------------------
 
-template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VEC, bool EDGE>
+template <int BM, int BN, int BK, int WM, int WN, int MI, bool TA, bool TB, bool VEC, bool EDGE>
 int launch_cfg(const gemm_args &a, int64_t batch, int splits, hipStream_t s) {
-  using C = cfg<BM, BN, BK, WM, WN>;
-  auto kern = sgemm_mfma_k<BM, BN, BK, WM, WN, TA, TB, VEC, EDGE>;
+  using C = cfg<BM, BN, BK, WM, WN, MI>;
+  auto kern = sgemm_mfma_k<BM, BN, BK, WM, WN, MI, TA, TB, VEC, EDGE>;
   static bool attr_done = false;
   if (!attr_done) {
     SILGPU_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
@@ -553,25 +593,25 @@ int launch_cfg(const gemm_args &a, int64_t batch, int splits, hipStream_t s) {
   return splits;  // >= 1: the number of K splits actually launched
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
+template <int BM, int BN, int BK, int WM, int WN, int MI, bool TA, bool TB>
 int launch_tb(const gemm_args &a, int64_t batch, int splits, bool vec, hipStream_t s) {
   // Every split's K range is a multiple of BK except possibly the last, and
   // that one is too when K is.
   const bool edge = (a.M % BM) || (a.N % BN) || (a.K % BK);
   if (vec) {
-    return edge ? launch_cfg<BM, BN, BK, WM, WN, TA, TB, true, true>(a, batch, splits, s)
-                : launch_cfg<BM, BN, BK, WM, WN, TA, TB, true, false>(a, batch, splits, s);
+    return edge ? launch_cfg<BM, BN, BK, WM, WN, MI, TA, TB, true, true>(a, batch, splits, s)
+                : launch_cfg<BM, BN, BK, WM, WN, MI, TA, TB, true, false>(a, batch, splits, s);
   }
-  return launch_cfg<BM, BN, BK, WM, WN, TA, TB, false, true>(a, batch, splits, s);
+  return launch_cfg<BM, BN, BK, WM, WN, MI, TA, TB, false, true>(a, batch, splits, s);
 }
 
-template <int BM, int BN, int BK, int WM, int WN>
+template <int BM, int BN, int BK, int WM, int WN, int MI>
 int launch_tiles(const gemm_args &a, int64_t batch, int splits, bool ta, bool tb, bool vec,
                  hipStream_t s) {
-  if (!ta && !tb) return launch_tb<BM, BN, BK, WM, WN, false, false>(a, batch, splits, vec, s);
-  if (!ta && tb) return launch_tb<BM, BN, BK, WM, WN, false, true>(a, batch, splits, vec, s);
-  if (ta && !tb) return launch_tb<BM, BN, BK, WM, WN, true, false>(a, batch, splits, vec, s);
-  return launch_tb<BM, BN, BK, WM, WN, true, true>(a, batch, splits, vec, s);
+  if (!ta && !tb) return launch_tb<BM, BN, BK, WM, WN, MI, false, false>(a, batch, splits, vec, s);
+  if (!ta && tb) return launch_tb<BM, BN, BK, WM, WN, MI, false, true>(a, batch, splits, vec, s);
+  if (ta && !tb) return launch_tb<BM, BN, BK, WM, WN, MI, true, false>(a, batch, splits, vec, s);
+  return launch_tb<BM, BN, BK, WM, WN, MI, true, true>(a, batch, splits, vec, s);
 }
 
 // Sums the K-split partials ws[s][M][N] in split order and applies the
@@ -619,7 +659,14 @@ __global__ __launch_bounds__(256) void splitk_reduce_k(const float *__restrict__
 }
 
 // Tile configurations (BM x BN, waves WM x WN; BK = 16, 32 for 32x128).
-enum tile_cfg { TILE_AUTO = 0, TILE_128x128 = 1, TILE_64x64 = 2, TILE_32x128 = 3, TILE_128x64 = 4 };
+enum tile_cfg {
+  TILE_AUTO = 0,
+  TILE_128x128 = 1,
+  TILE_64x64 = 2,
+  TILE_32x128 = 3,
+  TILE_128x64 = 4,
+  TILE_256x256 = 5
+};
 
 struct plan {
   int tile;
@@ -651,26 +698,37 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch) {
     }
     return p;
   }
+  // Predicted time of each (tile, K split): every CU runs ceil(WG / 256)
+  // workgroups, min(that, occupancy) of them at once; a SIMD holding a
+  // single wavefront reaches 0.8 of the rate it reaches with two or more.
+  // eff is the measured fraction of fp32 MFMA peak of each tile at large K,
+  // and the K loop reaches half its rate at klen = kK0.  Split-K adds the
+  // partial-sum pass.  Fitted to a tile/split sweep of square and
+  // transformer-block shapes on MI355X.
   struct cand {
-    int tile, bm, bn;
-    double eff, k0, full;
+    int tile, bm, bn, bk, waves, occupancy;
+    double eff;
   };
-  static const cand cands[] = {{TILE_128x128, 128, 128, 0.79, 256.0, 512.0},
-                               {TILE_128x64, 128, 64, 0.79, 400.0, 512.0},
-                               {TILE_64x64, 64, 64, 0.70, 128.0, 1024.0}};
-  const double flops = 2.0 * double(M) * double(N) * double(K) * double(batch);
+  static const cand cands[] = {{TILE_256x256, 256, 256, 16, 8, 1, 0.88},
+                               {TILE_128x128, 128, 128, 16, 4, 3, 0.86},
+                               {TILE_128x64, 128, 64, 16, 4, 5, 0.88},
+                               {TILE_64x64, 64, 64, 16, 4, 8, 0.74}};
+  constexpr double kK0 = 128.0, kSingleWave = 0.8;
+  const double rate_cu = 157.3e12 / 256.0;
   plan best{TILE_128x128, 1};
   double best_t = 1e30;
   for (const cand &cd : cands) {
     for (int sp : {1, 2, 4, 8}) {
-      if (sp > 1 && (batch != 1 || K / sp < 384)) continue;
-      const double wg = double(tiles(cd.bm, cd.bn)) * sp;
-      const double klen = double(cdiv(K, sp));
-      const double fill = wg >= cd.full ? 1.0 : wg / cd.full;
-      const double use = double(M) * double(N) /
-                         (double(cdiv(M, cd.bm) * cd.bm) * double(cdiv(N, cd.bn) * cd.bn));
-      const double rate = 157.3e12 * cd.eff * fill * use * (klen / (klen + cd.k0));
-      double t = flops / rate;
+      if (sp > 1 && (batch != 1 || K / sp < 128)) continue;
+      const int64_t wg = tiles(cd.bm, cd.bn) * sp;
+      const double klen = double(cdiv(cdiv(K, sp), cd.bk) * cd.bk);
+      const int64_t per_cu = cdiv(wg, 256);
+      const double conc = double(per_cu < cd.occupancy ? per_cu : cd.occupancy);
+      const double per_simd = conc * cd.waves / 4.0;
+      const double f = per_simd >= 2.0 ? 1.0 : per_simd >= 1.0 ? kSingleWave
+                                                                : kSingleWave * per_simd;
+      double t = double(per_cu) * 2.0 * cd.bm * cd.bn * klen /
+                 (rate_cu * cd.eff * f * (klen / (klen + kK0)));
       if (sp > 1) t += double(sp) * double(M) * double(N) * 8.0 / 5.0e12 + 4.0e-6;
       if (t < best_t * 0.999) {
         best_t = t;
@@ -694,10 +752,21 @@ int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, boo
   }
   int launched;
   switch (pl.tile) {
-    case TILE_64x64: launched = launch_tiles<64, 64, 16, 2, 2>(a, batch, splits, ta, tb, vec, c->stream); break;
-    case TILE_32x128: launched = launch_tiles<32, 128, 32, 1, 4>(a, batch, splits, ta, tb, vec, c->stream); break;
-    case TILE_128x64: launched = launch_tiles<128, 64, 16, 2, 2>(a, batch, splits, ta, tb, vec, c->stream); break;
-    default: launched = launch_tiles<128, 128, 16, 2, 2>(a, batch, splits, ta, tb, vec, c->stream); break;
+    case TILE_64x64:
+      launched = launch_tiles<64, 64, 16, 2, 2, 16>(a, batch, splits, ta, tb, vec, c->stream);
+      break;
+    case TILE_32x128:
+      launched = launch_tiles<32, 128, 32, 1, 4, 16>(a, batch, splits, ta, tb, vec, c->stream);
+      break;
+    case TILE_128x64:
+      launched = launch_tiles<128, 64, 16, 2, 2, 16>(a, batch, splits, ta, tb, vec, c->stream);
+      break;
+    case TILE_256x256:
+      launched = launch_tiles<256, 256, 16, 2, 4, 16>(a, batch, splits, ta, tb, vec, c->stream);
+      break;
+    default:
+      launched = launch_tiles<128, 128, 16, 2, 2, 16>(a, batch, splits, ta, tb, vec, c->stream);
+      break;
   }
   if (launched < 0) return launched;
   if (launched > 1) {
@@ -884,7 +953,7 @@ int silgpu_sgemm_tuned(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K
                        int64_t ldb, int64_t stride_b, float *d_C, int64_t ldc, int64_t stride_c,
                        int64_t batch, const float *d_bias, int64_t bias_len, int epilogue,
                        int tile, int splits) {
-  SILGPU_REQUIRE(tile >= TILE_128x128 && tile <= TILE_128x64,
+  SILGPU_REQUIRE(tile >= TILE_128x128 && tile <= TILE_256x256,
                  "silgpu_sgemm_tuned: unknown tile configuration %d", tile);
   SILGPU_REQUIRE(splits >= 1 && splits <= 256, "silgpu_sgemm_tuned: splits %d not in [1, 256]",
                  splits);

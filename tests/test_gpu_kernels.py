@@ -560,10 +560,11 @@ def test_small_batch_config(native, oracle):
     assert ok, (nw, el)
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5])
 @pytest.mark.parametrize("splits", [1, 3, 8])
 @pytest.mark.parametrize("M,N,K,ta,tb,epi", [(33, 70, 200, 0, 0, 0), (128, 256, 512, 0, 0, 2),
-                                             (100, 130, 1000, 1, 0, 1), (64, 96, 777, 0, 1, 4)])
+                                             (100, 130, 1000, 1, 0, 1), (64, 96, 777, 0, 1, 4),
+                                             (512, 256, 320, 0, 0, 1), (256, 512, 272, 1, 1, 3)])
 def test_sgemm_tuned_configs(native, oracle, tile, splits, M, N, K, ta, tb, epi):
     """Every forced tile configuration and K split against the oracle."""
     announce(f"sgemm_tuned tile={tile} splits={splits} {M}x{N}x{K} ta={ta} tb={tb} epi={epi}")
