@@ -264,6 +264,45 @@ int silgpu_sgemm_tuned(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K
                        int64_t stride_c, int64_t batch, const float *d_bias,
                        int64_t bias_len, int epilogue, int tile, int splits);
 
+/* The general product, of which silgpu_sgemm is the common case:
+ *   C[b] = epi(op(A[b]) * op(B[b])) for every batch index b = (o, i),
+ *   o < batch_outer, i < batch_inner, with operand X[b] at
+ *   X + o*stride_x_outer + i*stride_x_inner (element strides),
+ * so a batch that runs over two axes with different strides (attention heads
+ * split out of a [batch, seq, heads*dim] array) is one launch.  The
+ * epilogue applied to each fp32 accumulator v, in this order:
+ *   1. use_scale: v = fmaf(v, scale, scale_offset) (a scalar affine node of
+ *      the graph folded into the product, rounded as that node rounds);
+ *   2. bias (SILGPU_EPI_BIAS*): v += bias[n % bias_len];
+ *   3. sigmoid or relu per `epilogue`;
+ *   4. residual (non-NULL, batch 1 only): v = v + residual[m*ldr + n].
+ * Serves array::dot / batched_dot / linear / linear_sigmoid lowered by
+ * sil::eval (include/array.h:1360-1416, 1462-1472, 2174-2258) with the
+ * graph's neighbouring scalar and residual nodes fused in. */
+typedef struct silgpu_gemm_desc {
+  int32_t trans_a, trans_b;
+  int64_t M, N, K;
+  const float *A;
+  int64_t lda;
+  const float *B;
+  int64_t ldb;
+  float *C;
+  int64_t ldc;
+  int64_t batch_outer, batch_inner;        /* both >= 1 for a non-empty product */
+  int64_t stride_a_outer, stride_a_inner;
+  int64_t stride_b_outer, stride_b_inner;
+  int64_t stride_c_outer, stride_c_inner;
+  int32_t epilogue;                        /* SILGPU_EPI_* */
+  int32_t use_scale;
+  float scale, scale_offset;
+  const float *bias;
+  int64_t bias_len;
+  const float *residual;
+  int64_t ldr;
+} silgpu_gemm_desc;
+
+int silgpu_gemm(const silgpu_gemm_desc *desc);
+
 /* y[1 x N] = x[1 x K] * B[K x N] (B row-major, ldb >= N).  Replaces gpu::sgemv
  * (include/gpu.h:549-574).  silgpu_sgemm routes M == 1 here as well. */
 int silgpu_sgemv(const float *d_x, const float *d_B, int64_t ldb, float *d_y, int64_t N,

@@ -70,6 +70,23 @@ class Program(C.Structure):
                 ("instrs", ProgInstr * PROG_MAX_INSTRS)]
 
 
+class GemmDesc(C.Structure):
+    """silgpu_gemm_desc (include/silgpu.h)."""
+    _fields_ = [("trans_a", C.c_int32), ("trans_b", C.c_int32),
+                ("M", C.c_int64), ("N", C.c_int64), ("K", C.c_int64),
+                ("A", C.c_void_p), ("lda", C.c_int64),
+                ("B", C.c_void_p), ("ldb", C.c_int64),
+                ("C", C.c_void_p), ("ldc", C.c_int64),
+                ("batch_outer", C.c_int64), ("batch_inner", C.c_int64),
+                ("stride_a_outer", C.c_int64), ("stride_a_inner", C.c_int64),
+                ("stride_b_outer", C.c_int64), ("stride_b_inner", C.c_int64),
+                ("stride_c_outer", C.c_int64), ("stride_c_inner", C.c_int64),
+                ("epilogue", C.c_int32), ("use_scale", C.c_int32),
+                ("scale", C.c_float), ("scale_offset", C.c_float),
+                ("bias", C.c_void_p), ("bias_len", C.c_int64),
+                ("residual", C.c_void_p), ("ldr", C.c_int64)]
+
+
 _SIGS = {
     "silgpu_last_error": (C.c_char_p, []),
     "silgpu_init": (_i, []),
@@ -106,6 +123,7 @@ _SIGS = {
                           _i64, _i64, _i64, _vp, _i64, _i]),
     "silgpu_sgemm_tuned": (_i, [_i, _i, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
                                 _vp, _i64, _i64, _i64, _vp, _i64, _i, _i, _i]),
+    "silgpu_gemm": (_i, [C.POINTER(GemmDesc)]),
     "silgpu_sgemv": (_i, [_vp, _vp, _i64, _vp, _i64, _i64]),
     "silgpu_event_create": (_i, [C.POINTER(_vp)]),
     "silgpu_event_destroy": (_i, [_vp]),
@@ -304,6 +322,27 @@ def sgemm_tuned(ta, tb, M, N, K, A, lda, sA, B, ldb, sB, Cm, ldc, sC, batch=1, b
     call("silgpu_sgemm_tuned", int(ta), int(tb), M, N, K, vp(A), lda, sA, vp(B), ldb, sB,
          vp(Cm), ldc, sC, batch, vp(bias) if bias is not None else _vp(None), bias_len, epi,
          tile, splits)
+
+
+def gemm(ta, tb, M, N, K, A, lda, B, ldb, Cm, ldc, batch_outer=1, batch_inner=1,
+         strides_a=(0, 0), strides_b=(0, 0), strides_c=(0, 0), epi=EPI_NONE, scale=None,
+         bias=None, bias_len=0, residual=None, ldr=0):
+    """silgpu_gemm; strides_x = (outer, inner); scale = (scale, offset) or None."""
+    d = GemmDesc()
+    d.trans_a, d.trans_b, d.M, d.N, d.K = int(ta), int(tb), M, N, K
+    d.A, d.lda, d.B, d.ldb, d.C, d.ldc = vp(A).value, lda, vp(B).value, ldb, vp(Cm).value, ldc
+    d.batch_outer, d.batch_inner = batch_outer, batch_inner
+    d.stride_a_outer, d.stride_a_inner = strides_a
+    d.stride_b_outer, d.stride_b_inner = strides_b
+    d.stride_c_outer, d.stride_c_inner = strides_c
+    d.epilogue = epi
+    if scale is not None:
+        d.use_scale, d.scale, d.scale_offset = 1, scale[0], scale[1]
+    d.bias = vp(bias).value if bias is not None else None
+    d.bias_len = bias_len
+    d.residual = vp(residual).value if residual is not None else None
+    d.ldr = ldr
+    call("silgpu_gemm", C.byref(d))
 
 
 def sgemv(x, B, ldb, y, N, K):

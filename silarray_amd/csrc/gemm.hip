@@ -79,17 +79,41 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
 
 // ---- SGEMM kernel -----------------------------------------------------------
 
+// Epilogue of one accumulator, in this order: scalar affine node folded in
+// (fmaf, the node's own rounding), bias, activation, residual add.
+struct epi_args {
+  const float *bias;
+  int64_t bias_len;
+  const float *res;  // residual (batch 1 only), res[m * ldr + n]
+  int64_t ldr;
+  float scale, offset;
+  int epi;
+  int use_scale;
+};
+
+__device__ __forceinline__ float apply_epi(float v, int64_t m, int64_t n, const epi_args &e) {
+  if (e.use_scale) v = fmaf(v, e.scale, e.offset);
+  if (e.epi == SILGPU_EPI_BIAS || e.epi == SILGPU_EPI_BIAS_SIGMOID ||
+      e.epi == SILGPU_EPI_BIAS_RELU)
+    v += e.bias[n % e.bias_len];
+  if (e.epi == SILGPU_EPI_BIAS_SIGMOID) v = sigmoidf_dev(v);
+  else if (e.epi == SILGPU_EPI_RELU || e.epi == SILGPU_EPI_BIAS_RELU) v = fmaxf(v, 0.0f);
+  if (e.res) v = v + e.res[m * e.ldr + n];
+  return v;
+}
+
 struct gemm_args {
   const float *A;
   const float *B;
   float *C;
-  const float *bias;
   int64_t lda, ldb, ldc;
+  // batch index z = zo * binner + zi: operand X at X + zo*sX2 + zi*sX
   int64_t sA, sB, sC;
-  int64_t bias_len;
+  int64_t sA2, sB2, sC2;
+  int binner;
   int M, N, K;
   int tiles_m, tiles_n;
-  int epi;
+  epi_args ep;
   // Split K: workgroup row blockIdx.y covers K range [y*klen, (y+1)*klen)
   // (klen a multiple of BK).  With gridDim.y > 1 raw accumulators go to
   // ws[y][M][N] and splitk_reduce_k applies the epilogue.
@@ -193,10 +217,10 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
   int tm, tn;
   tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int64_t z = blockIdx.z;
-  const float *__restrict__ A = p.A + z * p.sA;
-  const float *__restrict__ B = p.B + z * p.sB;
-  float *__restrict__ Cp = p.C + z * p.sC;
+  const int64_t zo = blockIdx.z / p.binner, zi = blockIdx.z % p.binner;
+  const float *__restrict__ A = p.A + zo * p.sA2 + zi * p.sA;
+  const float *__restrict__ B = p.B + zo * p.sB2 + zi * p.sB;
+  float *__restrict__ Cp = p.C + zo * p.sC2 + zi * p.sC;
   const int M = p.M, N = p.N, K = p.K;
 
   typename F::acc_t acc[C::TM][C::TN];
@@ -293,7 +317,6 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
   // Epilogue.  Accumulator register r of lane l in block (i, j) is
   // C[row][col] with col = MI*j + l%MI and row = MI*i + F::row(l, r)
   // (relative to the wave tile).
-  const int epi = p.epi;
   if (gridDim.y > 1) {
     float *W = p.ws + int64_t(blockIdx.y) * M * N;
 #pragma unroll
@@ -311,25 +334,23 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
     }
     return;
   }
+  // One MFMA row block at a time (a scheduling barrier per block), so the
+  // compiler does not precompute every store address at once and spill.
 #pragma unroll
-  for (int j = 0; j < C::TN; ++j) {
-    const int col = n0 + wn * C::TN * MI + j * MI + lm;
-    if (EDGE && col >= N) continue;
-    float bv = 0.0f;
-    if (epi == SILGPU_EPI_BIAS || epi == SILGPU_EPI_BIAS_SIGMOID || epi == SILGPU_EPI_BIAS_RELU)
-      bv = p.bias[col % p.bias_len];
+  for (int i = 0; i < C::TM; ++i) {
 #pragma unroll
-    for (int i = 0; i < C::TM; ++i) {
+    for (int r = 0; r < F::R; ++r) {
+      const int row = m0 + wm * C::TM * MI + i * MI + F::row(lane, r);
+      if (EDGE && row >= M) continue;
+      float *__restrict__ crow = Cp + int64_t(row) * p.ldc;
 #pragma unroll
-      for (int r = 0; r < F::R; ++r) {
-        const int row = m0 + wm * C::TM * MI + i * MI + F::row(lane, r);
-        if (EDGE && row >= M) continue;
-        float v = acc[i][j][r] + bv;
-        if (epi == SILGPU_EPI_BIAS_SIGMOID) v = sigmoidf_dev(v);
-        else if (epi == SILGPU_EPI_RELU || epi == SILGPU_EPI_BIAS_RELU) v = fmaxf(v, 0.0f);
-        Cp[int64_t(row) * p.ldc + col] = v;
+      for (int j = 0; j < C::TN; ++j) {
+        const int col = n0 + wn * C::TN * MI + j * MI + lm;
+        if (EDGE && col >= N) continue;
+        crow[col] = apply_epi(acc[i][j][r], row, col, p.ep);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -551,19 +572,12 @@ __global__ __launch_bounds__(256) void gemv_t_k(const float *__restrict__ x,
 
 // Applies an epilogue to a [M x N] block of C in place (GEMV paths).
 __global__ __launch_bounds__(256) void epilogue_k(float *__restrict__ C, int64_t ldc,
-                                                  int64_t M, int64_t N,
-                                                  const float *__restrict__ bias,
-                                                  int64_t bias_len, int epi) {
+                                                  int64_t M, int64_t N, epi_args ep) {
   const int64_t total = M * N;
   for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total;
        i += int64_t(gridDim.x) * 256) {
     const int64_t m = i / N, n = i % N;
-    float v = C[m * ldc + n];
-    if (epi == SILGPU_EPI_BIAS || epi == SILGPU_EPI_BIAS_SIGMOID || epi == SILGPU_EPI_BIAS_RELU)
-      v += bias[n % bias_len];
-    if (epi == SILGPU_EPI_BIAS_SIGMOID) v = sigmoidf_dev(v);
-    else if (epi == SILGPU_EPI_RELU || epi == SILGPU_EPI_BIAS_RELU) v = fmaxf(v, 0.0f);
-    C[m * ldc + n] = v;
+    C[m * ldc + n] = apply_epi(C[m * ldc + n], m, n, ep);
   }
 }
 
@@ -621,8 +635,7 @@ template <bool VEC>
 __global__ __launch_bounds__(256) void splitk_reduce_k(const float *__restrict__ ws, int splits,
                                                        int64_t M, int64_t N,
                                                        float *__restrict__ C, int64_t ldc,
-                                                       const float *__restrict__ bias,
-                                                       int64_t bias_len, int epi) {
+                                                       epi_args ep) {
   const int64_t per = VEC ? 4 : 1;
   const int64_t total = M * N / per;
   const int64_t plane = M * N;
@@ -643,14 +656,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_k(const float *__restrict__
       }
     }
 #pragma unroll
-    for (int j = 0; j < (VEC ? 4 : 1); ++j) {
-      float x = v[j];
-      if (epi == SILGPU_EPI_BIAS || epi == SILGPU_EPI_BIAS_SIGMOID || epi == SILGPU_EPI_BIAS_RELU)
-        x += bias[(n + j) % bias_len];
-      if (epi == SILGPU_EPI_BIAS_SIGMOID) x = sigmoidf_dev(x);
-      else if (epi == SILGPU_EPI_RELU || epi == SILGPU_EPI_BIAS_RELU) x = fmaxf(x, 0.0f);
-      v[j] = x;
-    }
+    for (int j = 0; j < (VEC ? 4 : 1); ++j) v[j] = apply_epi(v[j], m, n + j, ep);
     if constexpr (VEC)
       *reinterpret_cast<float4 *>(C + m * ldc + n) = make_float4(v[0], v[1], v[2], v[3]);
     else
@@ -776,10 +782,10 @@ int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, boo
     if (g > 65536) g = 65536;
     if (v4)
       splitk_reduce_k<true><<<static_cast<unsigned>(g), 256, 0, c->stream>>>(
-          a.ws, launched, a.M, a.N, a.C, a.ldc, a.bias, a.bias_len, a.epi);
+          a.ws, launched, a.M, a.N, a.C, a.ldc, a.ep);
     else
       splitk_reduce_k<false><<<static_cast<unsigned>(g), 256, 0, c->stream>>>(
-          a.ws, launched, a.M, a.N, a.C, a.ldc, a.bias, a.bias_len, a.epi);
+          a.ws, launched, a.M, a.N, a.C, a.ldc, a.ep);
     SILGPU_LAUNCH_CHECK("splitk_reduce_k");
   }
   return SILGPU_OK;
@@ -833,16 +839,16 @@ int launch_gemv_t(const float *x, int64_t incx, const float *R, int64_t ldr, flo
   return SILGPU_OK;
 }
 
-int apply_epilogue(float *C, int64_t ldc, int64_t M, int64_t N, const float *bias,
-                   int64_t bias_len, int epi, context *c) {
-  if (epi == SILGPU_EPI_NONE) return SILGPU_OK;
+int apply_epilogue(float *C, int64_t ldc, int64_t M, int64_t N, const epi_args &ep,
+                   context *c) {
+  if (ep.epi == SILGPU_EPI_NONE && !ep.use_scale && !ep.res) return SILGPU_OK;
   int64_t g = cdiv(M * N, 256);
   if (g > 4096) g = 4096;
-  epilogue_k<<<static_cast<unsigned>(g), 256, 0, c->stream>>>(C, ldc, M, N, bias, bias_len,
-                                                                epi);
+  epilogue_k<<<static_cast<unsigned>(g), 256, 0, c->stream>>>(C, ldc, M, N, ep);
   SILGPU_LAUNCH_CHECK("epilogue_k");
   return SILGPU_OK;
 }
+
 
 }  // namespace
 }  // namespace silgpu
@@ -869,71 +875,115 @@ namespace {
 
 // Shared body of silgpu_sgemm / silgpu_sgemm_tuned.  `forced` (tuning only)
 // skips the vector-product routing and the shape heuristic.
-int sgemm_impl(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const float *d_A,
-               int64_t lda, int64_t stride_a, const float *d_B, int64_t ldb, int64_t stride_b,
-               float *d_C, int64_t ldc, int64_t stride_c, int64_t batch, const float *d_bias,
-               int64_t bias_len, int epilogue, const plan *forced) {
-  SILGPU_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "silgpu_sgemm: negative extent");
+int gemm_impl(const silgpu_gemm_desc &d, const plan *forced) {
+  const int64_t M = d.M, N = d.N, K = d.K;
+  SILGPU_REQUIRE(M >= 0 && N >= 0 && K >= 0 && d.batch_outer >= 0 && d.batch_inner >= 0,
+                 "silgpu_gemm: negative extent");
   SILGPU_REQUIRE(M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX,
-                 "silgpu_sgemm: extent exceeds int32");
-  SILGPU_REQUIRE(epilogue >= SILGPU_EPI_NONE && epilogue <= SILGPU_EPI_BIAS_RELU,
-                 "silgpu_sgemm: unknown epilogue %d", epilogue);
+                 "silgpu_gemm: extent exceeds int32");
+  SILGPU_REQUIRE(d.epilogue >= SILGPU_EPI_NONE && d.epilogue <= SILGPU_EPI_BIAS_RELU,
+                 "silgpu_gemm: unknown epilogue %d", d.epilogue);
+  const int64_t batch = d.batch_outer * d.batch_inner;
   if (M == 0 || N == 0 || batch == 0) return SILGPU_OK;
-  const bool ta = trans_a != 0, tb = trans_b != 0;
-  SILGPU_REQUIRE(lda >= (ta ? M : K) && lda >= 1, "silgpu_sgemm: lda %lld too small",
-                 (long long)lda);
-  SILGPU_REQUIRE(ldb >= (tb ? K : N) && ldb >= 1, "silgpu_sgemm: ldb %lld too small",
-                 (long long)ldb);
-  SILGPU_REQUIRE(ldc >= N, "silgpu_sgemm: ldc %lld < N %lld", (long long)ldc, (long long)N);
-  SILGPU_REQUIRE(batch <= 65535, "silgpu_sgemm: batch %lld exceeds the grid", (long long)batch);
-  const bool uses_bias = epilogue == SILGPU_EPI_BIAS || epilogue == SILGPU_EPI_BIAS_SIGMOID ||
-                         epilogue == SILGPU_EPI_BIAS_RELU;
-  SILGPU_REQUIRE(!uses_bias || (d_bias && bias_len > 0),
-                 "silgpu_sgemm: bias epilogue without bias");
-  SILGPU_REQUIRE(d_C != nullptr && (K == 0 || (d_A && d_B)), "silgpu_sgemm: null pointer");
+  const bool ta = d.trans_a != 0, tb = d.trans_b != 0;
+  SILGPU_REQUIRE(d.lda >= (ta ? M : K) && d.lda >= 1, "silgpu_gemm: lda %lld too small",
+                 (long long)d.lda);
+  SILGPU_REQUIRE(d.ldb >= (tb ? K : N) && d.ldb >= 1, "silgpu_gemm: ldb %lld too small",
+                 (long long)d.ldb);
+  SILGPU_REQUIRE(d.ldc >= N, "silgpu_gemm: ldc %lld < N %lld", (long long)d.ldc, (long long)N);
+  SILGPU_REQUIRE(batch <= 65535 && d.batch_inner <= INT32_MAX,
+                 "silgpu_gemm: batch %lld exceeds the grid", (long long)batch);
+  const bool uses_bias = d.epilogue == SILGPU_EPI_BIAS || d.epilogue == SILGPU_EPI_BIAS_SIGMOID ||
+                         d.epilogue == SILGPU_EPI_BIAS_RELU;
+  SILGPU_REQUIRE(!uses_bias || (d.bias && d.bias_len > 0),
+                 "silgpu_gemm: bias epilogue without bias");
+  SILGPU_REQUIRE(!d.residual || (batch == 1 && d.ldr >= N),
+                 "silgpu_gemm: a residual needs batch 1 and ldr >= N");
+  SILGPU_REQUIRE(d.C != nullptr && (K == 0 || (d.A && d.B)), "silgpu_gemm: null pointer");
   SILGPU_CTX(c);
+
+  epi_args ep{};
+  ep.bias = d.bias;
+  ep.bias_len = d.bias_len > 0 ? d.bias_len : 1;
+  ep.res = d.residual;
+  ep.ldr = d.ldr;
+  ep.scale = d.scale;
+  ep.offset = d.scale_offset;
+  ep.epi = d.epilogue;
+  ep.use_scale = d.use_scale != 0;
 
   // Vector products (the reference routes M == 1 to sgemv, include/array.h:2675-2676).
   if (!forced && batch == 1 && K > 0 && (M == 1 || N == 1)) {
     int rc;
     if (M == 1 && !tb && !ta) {
       // y = x * B with x = A[0..K) contiguous and B [K][N].
-      rc = launch_gemv_n(d_A, d_B, ldb, d_C, N, K, c);
+      rc = launch_gemv_n(d.A, d.B, d.ldb, d.C, N, K, c);
       if (rc != SILGPU_OK) return rc;
-      return apply_epilogue(d_C, ldc, 1, N, d_bias, bias_len, epilogue, c);
+      return apply_epilogue(d.C, d.ldc, 1, N, ep, c);
     } else if (M == 1 && tb) {
       // y[n] = sum_k x[k] * B[n*ldb + k]
-      rc = launch_gemv_t(d_A, ta ? lda : 1, d_B, ldb, d_C, 1, N, K, c);
+      rc = launch_gemv_t(d.A, ta ? d.lda : 1, d.B, d.ldb, d.C, 1, N, K, c);
       if (rc != SILGPU_OK) return rc;
-      return apply_epilogue(d_C, ldc, 1, N, d_bias, bias_len, epilogue, c);
+      return apply_epilogue(d.C, d.ldc, 1, N, ep, c);
     } else if (N == 1 && !ta) {
       // y[m] = sum_k A[m*lda + k] * b[k], b[k] = B[k*ldb] (non-trans) or B[k] (trans)
-      rc = launch_gemv_t(d_B, tb ? 1 : ldb, d_A, lda, d_C, ldc, M, K, c);
+      rc = launch_gemv_t(d.B, tb ? 1 : d.ldb, d.A, d.lda, d.C, d.ldc, M, K, c);
       if (rc != SILGPU_OK) return rc;
-      return apply_epilogue(d_C, ldc, M, 1, d_bias, bias_len, epilogue, c);
+      return apply_epilogue(d.C, d.ldc, M, 1, ep, c);
     }
   }
 
   gemm_args a{};
-  a.A = d_A;
-  a.B = d_B;
-  a.C = d_C;
-  a.bias = d_bias;
-  a.lda = lda;
-  a.ldb = ldb;
-  a.ldc = ldc;
-  a.sA = stride_a;
-  a.sB = stride_b;
-  a.sC = stride_c;
-  a.bias_len = bias_len > 0 ? bias_len : 1;
+  a.A = d.A;
+  a.B = d.B;
+  a.C = d.C;
+  a.lda = d.lda;
+  a.ldb = d.ldb;
+  a.ldc = d.ldc;
+  a.sA = d.stride_a_inner;
+  a.sB = d.stride_b_inner;
+  a.sC = d.stride_c_inner;
+  a.sA2 = d.stride_a_outer;
+  a.sB2 = d.stride_b_outer;
+  a.sC2 = d.stride_c_outer;
+  a.binner = static_cast<int>(d.batch_inner);
   a.M = static_cast<int>(M);
   a.N = static_cast<int>(N);
   a.K = static_cast<int>(K);
-  a.epi = epilogue;
-  const bool vec = aligned16(d_A) && aligned16(d_B) && lda % 4 == 0 && ldb % 4 == 0 &&
+  a.ep = ep;
+  const bool vec = aligned16(d.A) && aligned16(d.B) && d.lda % 4 == 0 && d.ldb % 4 == 0 &&
                    (ta ? M % 4 == 0 : K % 4 == 0) && (tb ? K % 4 == 0 : N % 4 == 0) &&
-                   (batch == 1 || (stride_a % 4 == 0 && stride_b % 4 == 0));
+                   (batch == 1 || (d.stride_a_inner % 4 == 0 && d.stride_b_inner % 4 == 0 &&
+                                   d.stride_a_outer % 4 == 0 && d.stride_b_outer % 4 == 0));
   return run_sgemm(a, batch, forced ? *forced : choose_plan(M, N, K, batch), ta, tb, vec, c);
+}
+
+silgpu_gemm_desc plain_desc(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                            const float *d_A, int64_t lda, int64_t stride_a, const float *d_B,
+                            int64_t ldb, int64_t stride_b, float *d_C, int64_t ldc,
+                            int64_t stride_c, int64_t batch, const float *d_bias,
+                            int64_t bias_len, int epilogue) {
+  silgpu_gemm_desc d{};
+  d.trans_a = trans_a;
+  d.trans_b = trans_b;
+  d.M = M;
+  d.N = N;
+  d.K = K;
+  d.A = d_A;
+  d.lda = lda;
+  d.B = d_B;
+  d.ldb = ldb;
+  d.C = d_C;
+  d.ldc = ldc;
+  d.batch_outer = batch > 0 ? 1 : 0;
+  d.batch_inner = batch;
+  d.stride_a_inner = stride_a;
+  d.stride_b_inner = stride_b;
+  d.stride_c_inner = stride_c;
+  d.epilogue = epilogue;
+  d.bias = d_bias;
+  d.bias_len = bias_len;
+  return d;
 }
 
 }  // namespace
@@ -944,8 +994,10 @@ int silgpu_sgemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, cons
                  int64_t lda, int64_t stride_a, const float *d_B, int64_t ldb,
                  int64_t stride_b, float *d_C, int64_t ldc, int64_t stride_c, int64_t batch,
                  const float *d_bias, int64_t bias_len, int epilogue) {
-  return sgemm_impl(trans_a, trans_b, M, N, K, d_A, lda, stride_a, d_B, ldb, stride_b, d_C, ldc,
-                    stride_c, batch, d_bias, bias_len, epilogue, nullptr);
+  SILGPU_REQUIRE(batch >= 0, "silgpu_sgemm: negative batch");
+  return gemm_impl(plain_desc(trans_a, trans_b, M, N, K, d_A, lda, stride_a, d_B, ldb, stride_b,
+                              d_C, ldc, stride_c, batch, d_bias, bias_len, epilogue),
+                   nullptr);
 }
 
 int silgpu_sgemm_tuned(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
@@ -957,10 +1009,16 @@ int silgpu_sgemm_tuned(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K
                  "silgpu_sgemm_tuned: unknown tile configuration %d", tile);
   SILGPU_REQUIRE(splits >= 1 && splits <= 256, "silgpu_sgemm_tuned: splits %d not in [1, 256]",
                  splits);
+  SILGPU_REQUIRE(batch >= 0, "silgpu_sgemm_tuned: negative batch");
   plan pl{tile, splits};
-  return sgemm_impl(trans_a, trans_b, M, N, K, d_A, lda, stride_a, d_B, ldb, stride_b, d_C, ldc,
-                    stride_c, batch, d_bias, bias_len, epilogue, &pl);
+  return gemm_impl(plain_desc(trans_a, trans_b, M, N, K, d_A, lda, stride_a, d_B, ldb, stride_b,
+                              d_C, ldc, stride_c, batch, d_bias, bias_len, epilogue),
+                   &pl);
 }
 
+int silgpu_gemm(const silgpu_gemm_desc *desc) {
+  SILGPU_REQUIRE(desc != nullptr, "silgpu_gemm: null descriptor");
+  return gemm_impl(*desc, nullptr);
+}
 
 }  // extern "C"

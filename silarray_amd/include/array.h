@@ -25,6 +25,7 @@
 #include <iterator>
 #include <limits>
 #include <memory>
+#include <optional>
 #include <numeric>
 #include <random>
 #include <ranges>
@@ -114,6 +115,12 @@ struct node {
   size_t axis = 0;    // sum_axis
   size_t view_off = 0;  // view: element offset into inputs[0]'s contiguous result
   int epilogue = 0;     // linear: epilogue fused by the lowering (relu)
+  // Folded into a product's epilogue by the lowering: a scalar affine node
+  // of the graph (v = fmaf(v, scale, scale_offset), rounded as that node
+  // rounds) and a residual add (v + residual, after bias and activation).
+  bool use_scale = false;
+  float scale = 1.0f, scale_offset = 0.0f;
+  std::shared_ptr<node> residual;
 
   static std::shared_ptr<node> leaf(const storage &s, const shape_type &sh, const strides_type &st) {
     auto n = std::make_shared<node>();
@@ -1601,6 +1608,36 @@ inline gemm_operand operand2d(node *n, const shape_type &as2d) {
   return {c, as2d[1], false};
 }
 
+// Descriptor of a single (batch 1) product with n's fused scale.
+inline silgpu_gemm_desc product_desc(size_t M, size_t N, size_t K, const gemm_operand &A,
+                                     const gemm_operand &B, size_t ldc, const node *n) {
+  silgpu_gemm_desc d{};
+  d.trans_a = A.trans;
+  d.trans_b = B.trans;
+  d.M = int64_t(M);
+  d.N = int64_t(N);
+  d.K = int64_t(K);
+  d.lda = int64_t(A.ld);
+  d.ldb = int64_t(B.ld);
+  d.ldc = int64_t(ldc);
+  d.batch_outer = d.batch_inner = 1;
+  d.epilogue = SILGPU_EPI_NONE;
+  d.use_scale = n->use_scale;
+  d.scale = n->scale;
+  d.scale_offset = n->scale_offset;
+  return d;
+}
+
+// The residual operand fused into n's epilogue (a 2-D view with unit column
+// stride, already evaluated), kept alive in `keep` until the launch.
+inline void add_residual(silgpu_gemm_desc &d, const node *n, std::optional<array<float>> &keep) {
+  if (!n->residual) return;
+  node *x = n->residual.get();
+  if (!x->evaluated) throw std::runtime_error("array: residual operand not evaluated.");
+  keep = as_array(x);
+  d.ldr = int64_t(x->strides[0]);
+}
+
 inline void eval_dot(node *n) {
   node *l = n->inputs[0].get(), *r = n->inputs[1].get();
   // 1-D operands: v . m -> {1,K}.{K,N}; m . v -> {M,K}.{K,1}; v . v -> {1,K}.{K,1}
@@ -1622,8 +1659,11 @@ inline void eval_dot(node *n) {
     B = operand2d(r, {K, N});
   }
   auto out = new_output(n->shape);
-  gpu::gemm_(A.arr.storage_ref(), B.arr.storage_ref(), out, M, N, K, A.ld, B.ld, A.trans,
-             B.trans, 1, 0, 0, 0, nullptr, 0, SILGPU_EPI_NONE);
+  auto d = product_desc(M, N, K, A, B, N, n);
+  std::optional<array<float>> res;
+  add_residual(d, n, res);
+  gpu::gemm(d, A.arr.storage_ref(), B.arr.storage_ref(), out, nullptr,
+            res ? &res->storage_ref() : nullptr);
   finish(n, std::move(out));
 }
 
@@ -1638,11 +1678,15 @@ inline void eval_linear(node *n, bool with_sigmoid) {
     // Bias read as bias[col % bias_len] in the GEMM epilogue
     // (include/gpu_kernels.metal:506-542).
     auto bias = contiguous(b);
-    gpu::gemm_(A.arr.storage_ref(), B.arr.storage_ref(), out, M, N, K, A.ld, B.ld, A.trans,
-               B.trans, 1, 0, 0, 0, &bias.storage_ref(), bl,
-               with_sigmoid ? SILGPU_EPI_BIAS_SIGMOID
-               : n->epilogue == SILGPU_EPI_BIAS_RELU ? SILGPU_EPI_BIAS_RELU
-                                                      : SILGPU_EPI_BIAS);
+    auto d = product_desc(M, N, K, A, B, N, n);
+    d.epilogue = with_sigmoid ? SILGPU_EPI_BIAS_SIGMOID
+                 : n->epilogue == SILGPU_EPI_BIAS_RELU ? SILGPU_EPI_BIAS_RELU
+                                                        : SILGPU_EPI_BIAS;
+    d.bias_len = int64_t(bl);
+    std::optional<array<float>> res;
+    add_residual(d, n, res);
+    gpu::gemm(d, A.arr.storage_ref(), B.arr.storage_ref(), out, &bias.storage_ref(),
+              res ? &res->storage_ref() : nullptr);
     finish(n, std::move(out));
     return;
   }
@@ -1706,41 +1750,72 @@ inline void eval_batched(node *n) {
     r = rc.get();
     mat_layout(r, K, N, ldb, tb);
   }
-  // Fold leading axes from the innermost outwards while both operands
-  // stride them uniformly (stride[d] == stride[d+1] * extent[d+1]).
-  size_t inner = L;  // axes [inner, L) form the batch
-  size_t batch = 1;
+  // Fold the leading axes into at most two batch groups, each a run of
+  // axes that both operands stride uniformly (stride[d] == stride[d+1] *
+  // extent[d+1]): [inner, L) is the inner batch, [outer_begin, inner) the
+  // outer one; any axes left before outer_begin are looped over.  A
+  // [batch, heads, seq, dim] view split out of one [batch*seq, 3*heads*dim]
+  // array is one launch: heads are the inner group, batches the outer.
+  auto uniform = [&](size_t d) {
+    return l->strides[d] == l->strides[d + 1] * l->shape[d + 1] &&
+           r->strides[d] == r->strides[d + 1] * r->shape[d + 1];
+  };
+  size_t inner = L, outer_begin = L;
+  size_t binner = 1, bouter = 1;
   if (L > 0) {
     inner = L - 1;
-    batch = n->shape[L - 1];
-    while (inner > 0) {
-      const size_t d = inner - 1;
-      const bool ul = l->strides[d] == l->strides[d + 1] * l->shape[d + 1];
-      const bool ur = r->strides[d] == r->strides[d + 1] * r->shape[d + 1];
-      if (!ul || !ur) break;
-      batch *= n->shape[d];
-      inner = d;
+    binner = n->shape[L - 1];
+    while (inner > 0 && uniform(inner - 1)) binner *= n->shape[--inner];
+    outer_begin = inner;
+    if (inner > 0) {
+      outer_begin = inner - 1;
+      bouter = n->shape[inner - 1];
+      while (outer_begin > 0 && uniform(outer_begin - 1)) bouter *= n->shape[--outer_begin];
+      if (bouter * binner > 65535) {  // grid limit: loop over the outer group instead
+        outer_begin = inner;
+        bouter = 1;
+      }
     }
   }
-  const size_t sa = L > 0 ? l->strides[L - 1] : 0, sb = L > 0 ? r->strides[L - 1] : 0;
+  silgpu_gemm_desc d{};
+  d.trans_a = ta;
+  d.trans_b = tb;
+  d.M = int64_t(M);
+  d.N = int64_t(N);
+  d.K = int64_t(K);
+  d.lda = int64_t(lda);
+  d.ldb = int64_t(ldb);
+  d.ldc = int64_t(N);
+  d.batch_outer = int64_t(bouter);
+  d.batch_inner = int64_t(binner);
+  d.stride_a_inner = L > 0 ? int64_t(l->strides[L - 1]) : 0;
+  d.stride_b_inner = L > 0 ? int64_t(r->strides[L - 1]) : 0;
+  d.stride_c_inner = int64_t(M * N);
+  d.stride_a_outer = inner > 0 ? int64_t(l->strides[inner - 1]) : 0;
+  d.stride_b_outer = inner > 0 ? int64_t(r->strides[inner - 1]) : 0;
+  d.stride_c_outer = int64_t(binner * M * N);
+  d.epilogue = SILGPU_EPI_NONE;
+  d.use_scale = n->use_scale;
+  d.scale = n->scale;
+  d.scale_offset = n->scale_offset;
   auto out = new_output(n->shape);
-  size_t outer = 1;
-  for (size_t d = 0; d < inner; d++) outer *= n->shape[d];
-  for (size_t o = 0; o < outer; o++) {
+  size_t loops = 1;
+  for (size_t a = 0; a < outer_begin; a++) loops *= n->shape[a];
+  const size_t per_loop = bouter * binner * M * N;
+  for (size_t o = 0; o < loops; o++) {
     size_t rem = o, offa = 0, offb = 0;
-    for (size_t d = inner; d-- > 0;) {
-      const size_t idx = rem % n->shape[d];
-      rem /= n->shape[d];
-      offa += idx * l->strides[d];
-      offb += idx * r->strides[d];
+    for (size_t a = outer_begin; a-- > 0;) {
+      const size_t idx = rem % n->shape[a];
+      rem /= n->shape[a];
+      offa += idx * l->strides[a];
+      offb += idx * r->strides[a];
     }
     storage A = l->data, B = r->data, C = out;
     A.off += offa;
     B.off += offb;
-    C.off += o * batch * M * N;
-    C.len = batch * M * N;
-    gpu::gemm_(A, B, C, M, N, K, lda, ldb, ta, tb, batch, sa, sb, M * N, nullptr, 0,
-               SILGPU_EPI_NONE);
+    C.off += o * per_loop;
+    C.len = per_loop;
+    gpu::gemm(d, A, B, C);
   }
   finish(n, std::move(out));
 }
@@ -1861,23 +1936,95 @@ inline void evaluate(const std::vector<node *> &roots) {
       }
     }
   const std::unordered_set<node *> root_set(roots.begin(), roots.end());
-  // relu(linear(x, W, b)) with the linear node used only there: the relu
-  // runs in the GEMM epilogue and the relu node takes the product's result.
-  std::unordered_set<node *> relu_fused;
+  std::unordered_map<node *, size_t> pos;
+  for (size_t i = 0; i < order.size(); i++) pos[order[i]] = i;
+  // c is consumed only by p inside this graph, is not requested itself and
+  // no array outside the graph holds it.
+  auto single_use = [&](node *c, node *p) {
+    if (c->evaluated || root_set.count(c)) return false;
+    auto it = consumers.find(c);
+    if (it == consumers.end() || it->second != 1) return false;
+    for (uint8_t i = 0; i < p->num_inputs; i++)
+      if (p->inputs[i].get() == c) return p->inputs[i].use_count() == 1;
+    return false;
+  };
+  auto bias_vector = [](node *lin) {
+    node *b = lin->inputs[2].get();
+    return shape_count(b->shape) > 0 && b->shape.size() <= 1;
+  };
+  // Nodes whose result is another node's output (alias[n]): the lowering
+  // folds them into the epilogue of the product they consume.
+  std::unordered_map<node *, node *> alias;
+  std::unordered_set<node *> materialize;  // operands a fused epilogue reads
+  //  relu(linear(x, W, b)): the relu runs in the GEMM epilogue.
   for (node *n : order) {
     if (n->operation != op::relu) continue;
     node *c = n->inputs[0].get();
-    if (c->evaluated || c->operation != op::linear || root_set.count(c)) continue;
-    if (consumers[c] != 1 || n->inputs[0].use_count() != 1) continue;
-    if (shape_count(c->inputs[2]->shape) == 0 || c->inputs[2]->shape.size() > 1) continue;
+    if (c->operation != op::linear || !single_use(c, n) || !bias_vector(c)) continue;
     c->epilogue = SILGPU_EPI_BIAS_RELU;
-    relu_fused.insert(n);
+    alias[n] = c;
+  }
+  //  product op host-scalar (and scalar op product): the node's fmaf runs in
+  //  the epilogue of dot / batched_dot, with the scale and offset the
+  //  program builder would use, so the result is bit-identical.
+  for (node *n : order) {
+    if (!is_binary(n->operation) || n->operation == op::pow) continue;
+    node *a = n->inputs[0].get(), *b = n->inputs[1].get();
+    auto is_product = [](node *x) {
+      return x->operation == op::dot || x->operation == op::batched_dot;
+    };
+    float s = 0.0f, scale = 1.0f, offset = 0.0f;
+    node *c = nullptr;
+    if (is_product(a) && host_scalar(b, s)) {
+      c = a;
+      switch (n->operation) {
+        case op::add: offset = 0.0f + s; break;
+        case op::sub: offset = 0.0f - s; break;
+        case op::mul: scale = 1.0f * s; offset = 0.0f * s; break;
+        default: scale = 1.0f / s; offset = 0.0f / s; break;  // div
+      }
+    } else if (n->operation != op::div && is_product(b) && host_scalar(a, s)) {
+      c = b;
+      switch (n->operation) {
+        case op::add: offset = 0.0f + s; break;
+        case op::sub: scale = -1.0f; offset = s - 0.0f; break;
+        default: scale = 1.0f * s; offset = 0.0f * s; break;  // mul
+      }
+    }
+    if (!c || c->use_scale || c->shape != n->shape || !single_use(c, n)) continue;
+    c->use_scale = true;
+    c->scale = scale;
+    c->scale_offset = offset;
+    alias[n] = c;
+  }
+  //  x + product (either side): the add runs after the product's epilogue,
+  //  reading x (a 2-D array with unit column stride computed before the
+  //  product) as the residual.
+  for (node *n : order) {
+    if (n->operation != op::add || alias.count(n) || n->shape.size() != 2) continue;
+    for (int side = 0; side < 2; side++) {
+      node *p = n->inputs[side].get(), *x = n->inputs[1 - side].get();
+      node *c = alias.count(p) ? alias[p] : p;
+      const bool ok_op = (c->operation == op::dot && c->inputs[0]->shape.size() == 2 &&
+                          c->inputs[1]->shape.size() == 2) ||
+                         ((c->operation == op::linear || c->operation == op::linear_sigmoid) &&
+                          bias_vector(c));
+      if (!ok_op || c->evaluated || c->residual || c->shape != n->shape) continue;
+      if (!single_use(p, n) || x == c || x->shape != n->shape) continue;
+      if (x->strides.size() != 2 || x->strides[1] != 1 || x->strides[0] < n->shape[1]) continue;
+      if (!x->evaluated && !(pos.count(x) && pos.count(c) && pos[x] < pos[c])) continue;
+      c->residual = n->inputs[1 - side];
+      materialize.insert(x);
+      alias[n] = c;
+      break;
+    }
   }
   // A node is computed inside its consumer's program when it is elementwise,
   // has exactly one consumer, that consumer is elementwise, it is not a root
   // and no array outside the graph holds it.
   auto fusable = [&](node *c) {
     if (c->evaluated || root_set.count(c) || !is_elementwise(c->operation)) return false;
+    if (materialize.count(c) || alias.count(c)) return false;
     auto it = consumers.find(c);
     if (it == consumers.end() || it->second != 1) return false;
     if (!is_elementwise(parent[c]->operation)) return false;
@@ -1889,8 +2036,9 @@ inline void evaluate(const std::vector<node *> &roots) {
   };
   for (node *n : order) {
     if (n->evaluated) continue;
-    if (relu_fused.count(n)) {
-      node *c = n->inputs[0].get();
+    if (auto it = alias.find(n); it != alias.end()) {
+      node *c = it->second;
+      if (!c->evaluated) throw std::runtime_error("array: fused product not evaluated.");
       n->data = c->data;
       n->strides = c->strides;
       n->evaluated = true;
@@ -1930,6 +2078,7 @@ inline void evaluate(const std::vector<node *> &roots) {
   for (node *n : order) {
     for (auto &i : n->inputs) i.reset();
     n->num_inputs = 0;
+    n->residual.reset();
   }
 }
 

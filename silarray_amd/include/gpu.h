@@ -213,6 +213,18 @@ class gpu {
               "sgemm");
   }
 
+  // silgpu_gemm with its pointers taken from storages: two-level batch
+  // strides and the fused scale / residual epilogue of the eval lowering.
+  static void gemm(silgpu_gemm_desc d, const storage &A, const storage &B, storage &C,
+                   const storage *bias = nullptr, const storage *residual = nullptr) {
+    d.A = A.dev_in<float>();
+    d.B = B.dev_in<float>();
+    d.bias = bias ? bias->dev_in<float>() : nullptr;
+    d.residual = residual ? residual->dev_in<float>() : nullptr;
+    d.C = C.dev_out<float>();
+    launched_(silgpu_gemm(&d), "gemm");
+  }
+
   // Fused elementwise program (the lowering target of sil::eval).
   static void program(const silgpu_program &p, storage &OUT) {
     launched_(silgpu_program_f32(&p, OUT.dev_out<float>()), "program");

@@ -451,6 +451,52 @@ TEST_CASE("product with the transpose of a lazy matrix") {
   CHECK(ok);
 }
 
+TEST_CASE("scalar and residual nodes fused into products stay bit-exact") {
+  // Each fused graph is compared with the same graph evaluated with the
+  // intermediate held by an array (held nodes are never fused).
+  auto x = random({70, 48}) - 0.5f;
+  auto W = random({48, 33}) - 0.5f;
+  auto b = random({33}) - 0.5f;
+  auto r = random({70, 33}) - 0.5f;
+  auto q = random({2, 3, 5, 8}) - 0.5f, k = random({2, 3, 8, 5}) - 0.5f;
+  eval(x, W, b, r, q, k);
+  auto same = [](const array<float> &a, const array<float> &c) {
+    if (a.shape() != c.shape()) return false;
+    const float *pa = a.buffer_data(), *pc = c.buffer_data();
+    for (size_t i = 0; i < a.element_count(); i++)
+      if (std::memcmp(&pa[i], &pc[i], sizeof(float)) != 0) return false;
+    return true;
+  };
+  {  // dot * s, s - dot, dot / s
+    auto f1 = x.dot(W) * 0.3f, f2 = 1.5f - x.dot(W), f3 = x.dot(W) / 7.0f;
+    eval(f1, f2, f3);
+    auto held = x.dot(W);
+    eval(held);
+    auto u1 = held * 0.3f, u2 = 1.5f - held, u3 = held / 7.0f;
+    eval(u1, u2, u3);
+    CHECK(same(f1, u1) && same(f2, u2) && same(f3, u3));
+  }
+  {  // batched_dot * s over a two-level batch
+    auto f = q.batched_dot(k) * 0.125f;
+    eval(f);
+    auto held = q.batched_dot(k);
+    eval(held);
+    auto u = held * 0.125f;
+    eval(u);
+    CHECK(same(f, u));
+  }
+  {  // r + linear, linear + r, r + relu(linear), r + dot
+    auto f1 = r + x.linear(W, b), f2 = x.linear(W, b) + r, f3 = r + x.linear(W, b).relu();
+    auto f4 = r + x.dot(W);
+    eval(f1, f2, f3, f4);
+    auto h1 = x.linear(W, b), h3 = x.linear(W, b).relu(), h4 = x.dot(W);
+    eval(h1, h3, h4);
+    auto u1 = r + h1, u2 = h1 + r, u3 = r + h3, u4 = r + h4;
+    eval(u1, u2, u3, u4);
+    CHECK(same(f1, u1) && same(f2, u2) && same(f3, u3) && same(f4, u4));
+  }
+}
+
 TEST_CASE("lazy views feed strided batched products") {
   // qkv [B*S, 3*H*dh] split into heads by view/permute/select, as an
   // attention block does; every product reads its operand in place.

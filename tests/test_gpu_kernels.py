@@ -587,3 +587,67 @@ def test_sgemm_tuned_configs(native, oracle, tile, splits, M, N, K, ta, tb, epi)
         C64 = np.maximum(C64, 0)
     ok, nw, el = gemm_tolerance_ok(Cg, C64, Cabs, K)
     assert ok, (nw, el)
+
+
+# ---- silgpu_gemm: two-level batch, fused scale / residual ----------------------------
+
+def test_gemm_two_level_batch_head_split(native, oracle):
+    """Q K^T for every (batch, head) of a [B*S, 3*H*dh] qkv array in one launch:
+    A and B are strided head views (outer stride per batch, inner per head)."""
+    announce("gemm two-level batch")
+    B_, S, H, dh = 3, 40, 4, 16
+    D = H * dh
+    g = rng(2100)
+    qkv = g.normal(0, 1, (B_ * S, 3 * D)).astype(np.float32)
+    dq, dc = up(native, qkv), empty(native, B_ * H * S * S)
+    base = native.vp(dq).value
+    native.gemm(0, 1, S, S, dh, base, 3 * D, base + 4 * D, 3 * D, dc, S,
+                batch_outer=B_, batch_inner=H, strides_a=(S * 3 * D, dh),
+                strides_b=(S * 3 * D, dh), strides_c=(H * S * S, S * S))
+    got = down(native, dc, (B_, H, S, S))
+    q = qkv.reshape(B_, S, 3, H, dh)[:, :, 0].transpose(0, 2, 1, 3).astype(np.float64)
+    k = qkv.reshape(B_, S, 3, H, dh)[:, :, 1].transpose(0, 2, 1, 3).astype(np.float64)
+    ref = q @ k.transpose(0, 1, 3, 2)
+    refabs = np.abs(q) @ np.abs(k.transpose(0, 1, 3, 2))
+    assert np.all(np.abs(got - ref) <= 1e-5 * math.sqrt(dh) * refabs + 1e-30)
+
+
+@pytest.mark.parametrize("M,N,K", [(100, 130, 200), (256, 256, 4096), (1, 300, 257),
+                                   (512, 512, 96)])
+def test_gemm_fused_epilogue_bit_exact(native, oracle, M, N, K):
+    """scale -> bias -> relu -> residual fused into the product equals the
+    same fp32 steps run as separate kernels (affine fma, bias add, relu,
+    residual add), bit for bit, on every GEMM path (MFMA tiles, split K,
+    GEMV for M == 1)."""
+    announce(f"gemm fused epilogue {M}x{N}x{K}")
+    g = rng(2200 + M + K)
+    A = g.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = g.uniform(-1, 1, (K, N)).astype(np.float32)
+    bias = g.normal(0, 1, N).astype(np.float32)
+    ldr = N + 3
+    R = g.normal(0, 1, (M, ldr)).astype(np.float32)
+    s = np.float32(0.125 + 1.0 / 3.0)
+    off = np.float32(0.0) * s
+    dA, dB, db, dR = up(native, A), up(native, B), up(native, bias), up(native, R)
+    fused, plain = empty(native, M * N), empty(native, M * N)
+    native.gemm(0, 0, M, N, K, dA, K, dB, N, fused, N, epi=native.EPI_BIAS_RELU,
+                scale=(float(s), float(off)), bias=db, bias_len=N, residual=dR, ldr=ldr)
+    native.sgemm(0, 0, M, N, K, dA, K, 0, dB, N, 0, plain, N, 0)
+    t1, t2, t3 = empty(native, M * N), empty(native, M * N), empty(native, M * N)
+    native.affine_f32(plain, t1, M * N, float(s), float(off))
+    native.binary_f32(ADD, t1, M * N, db, N, t2, M * N)
+    native.unary_f32(native.RELU, t2, t3, M * N)
+    Rc = up(native, np.ascontiguousarray(R[:, :N]))
+    out = empty(native, M * N)
+    native.binary_f32(ADD, t3, M * N, Rc, M * N, out, M * N)
+    assert np.array_equal(down(native, fused, (M, N)), down(native, out, (M, N)))
+
+
+def test_gemm_desc_validation(native):
+    announce("gemm descriptor validation")
+    dA, dC = empty(native, 64), empty(native, 64)
+    with pytest.raises(native.SilGpuError, match="residual"):
+        native.gemm(0, 0, 4, 4, 4, dA, 4, dA, 4, dC, 4, batch_outer=2, batch_inner=1,
+                    residual=dA, ldr=4)
+    with pytest.raises(native.SilGpuError, match="ldc"):
+        native.gemm(0, 0, 4, 8, 4, dA, 4, dA, 8, dC, 4)
