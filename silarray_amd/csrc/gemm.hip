@@ -354,6 +354,169 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
   }
 }
 
+// ---- SGEMM with LDS-direct operand loads (256 x 256 x 16 tiles) ------------
+//
+// Full tiles only (M, N multiples of 256, K range a multiple of 16, 16-byte
+// aligned operands): every lane's 16-byte global_load_lds_dwordx4 stays in
+// bounds, so no lane needs masking.  The load engine writes each wave's 64 x
+// 16 bytes to one contiguous 1 KB LDS window (lane L at 16 L), with no
+// staging registers and no ds_write; the layout is chosen through which
+// global chunk each lane fetches:
+//   - an operand contiguous in K (A, or B transposed): a window holds 16
+//     rows x 16 k; the 16-byte chunk of (row rr, k quad kq) sits at position
+//     rr*4 + (kq ^ ((rr/4) & 3)), which makes the 16x16x4 fragment reads
+//     (16 rows x 4 k per instruction) touch 64 distinct banks;
+//   - an operand contiguous in M or N (A transposed, or B): one window per
+//     k row, pitch kDtlPitch = 272 floats so the 4 k rows a fragment read
+//     touches fall on disjoint 16-bank groups.
+// Eight waves (2 x 4) own 128 x 64 of C each; the next K tile's loads are
+// issued before the current tile is multiplied, and one s_waitcnt + barrier
+// ends each tile.
+constexpr int kDtlTile = 256, kDtlBK = 16, kDtlPitch = 272;
+constexpr int kDtlWin = 16;                              // windows per operand and tile
+constexpr int kDtlStage = 2 * kDtlWin * kDtlPitch;  // floats: two operands, the larger layout
+constexpr int kDtlLdsBytes = 2 * kDtlStage * 4;
+
+__device__ __forceinline__ void dtl16(const float *src, float *lds_dst) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                   (__attribute__((address_space(3))) void *)lds_dst, 16, 0, 0);
+}
+
+// Per-lane source pointer and LDS window offset of window w (0..15) of one
+// operand tile.  KCONTIG: rows x0 + 16w .. +15 of a [rows][K] operand;
+// otherwise k row w of a [K][cols] operand at columns x0 ...
+template <bool KCONTIG>
+__device__ __forceinline__ const float *dtl_src(const float *base, int64_t ld, int x0, int w,
+                                                int lane) {
+  if constexpr (KCONTIG) {
+    const int rr = lane / 4, kq = (lane % 4) ^ ((rr / 4) & 3);
+    return base + int64_t(x0 + 16 * w + rr) * ld + 4 * kq;
+  } else {
+    return base + int64_t(w) * ld + x0 + 4 * lane;
+  }
+}
+template <bool KCONTIG>
+__device__ __forceinline__ int dtl_window(int w) {
+  return KCONTIG ? w * 256 : w * kDtlPitch;
+}
+// LDS offset (floats) of element (x, k) of a stage's operand tile.
+template <bool KCONTIG>
+__device__ __forceinline__ int dtl_elem(int x, int k) {
+  if constexpr (KCONTIG)
+    return (x / 16) * 256 + ((x % 16) * 4 + ((k / 4) ^ (((x % 16) / 4) & 3))) * 4 + (k % 4);
+  else
+    return k * kDtlPitch + x;
+}
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(512) void sgemm_dtl_k(gemm_args p) {
+  using F = mfma<16>;
+  constexpr int TM = 8, TN = 4;  // 16 x 16 blocks per wave: 128 x 64
+  constexpr bool AK = !TA, BKc = TB;  // operand contiguous in K
+  extern __shared__ float lds[];
+  const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+  const int wm = wave / 4, wn = wave % 4;
+  int tm, tn;
+  tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int m0 = tm * kDtlTile, n0 = tn * kDtlTile;
+  const int64_t zo = blockIdx.z / p.binner, zi = blockIdx.z % p.binner;
+  const float *__restrict__ A = p.A + zo * p.sA2 + zi * p.sA;
+  const float *__restrict__ B = p.B + zo * p.sB2 + zi * p.sB;
+  float *__restrict__ Cp = p.C + zo * p.sC2 + zi * p.sC;
+  const int M = p.M, N = p.N;
+  const int kbeg = blockIdx.y * p.klen;
+  const int kend = min(p.K, kbeg + p.klen);
+  const int KT = kend > kbeg ? (kend - kbeg) / kDtlBK : 0;  // K % 16 == 0 on this path
+  // Windows wave and wave + 8 of each operand.
+  const float *a_src0 = dtl_src<AK>(A, p.lda, m0, wave, lane);
+  const float *a_src1 = dtl_src<AK>(A, p.lda, m0, wave + 8, lane);
+  const float *b_src0 = dtl_src<BKc>(B, p.ldb, n0, wave, lane);
+  const float *b_src1 = dtl_src<BKc>(B, p.ldb, n0, wave + 8, lane);
+  // Advance of one K tile for each operand.
+  const int64_t a_step = AK ? kDtlBK : int64_t(kDtlBK) * p.lda;
+  const int64_t b_step = BKc ? kDtlBK : int64_t(kDtlBK) * p.ldb;
+  constexpr int kAOff = 0, kBOff = kDtlWin * (AK ? 256 : kDtlPitch);
+  auto issue = [&](int kt, int stage) {
+    float *S = lds + stage * kDtlStage;
+    const int64_t k = int64_t(kbeg / kDtlBK + kt);
+    dtl16(a_src0 + k * a_step, S + kAOff + dtl_window<AK>(wave));
+    dtl16(a_src1 + k * a_step, S + kAOff + dtl_window<AK>(wave + 8));
+    dtl16(b_src0 + k * b_step, S + kBOff + dtl_window<BKc>(wave));
+    dtl16(b_src1 + k * b_step, S + kBOff + dtl_window<BKc>(wave + 8));
+  };
+  typename F::acc_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < F::R; ++r) acc[i][j][r] = 0.0f;
+  const int lm = lane % 16, kl = lane / 16;
+  const int xa = wm * TM * 16 + lm, xb = wn * TN * 16 + lm;
+  if (KT > 0) {
+    issue(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < KT) issue(kt + 1, cur ^ 1);
+    const float *Sa = lds + cur * kDtlStage + kAOff;
+    const float *Sb = lds + cur * kDtlStage + kBOff;
+    float a[2][TM], b[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a[0][i] = Sa[dtl_elem<AK>(xa + 16 * i, kl)];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) b[0][j] = Sb[dtl_elem<BKc>(xb + 16 * j, kl)];
+#pragma unroll
+    for (int st = 0; st < kDtlBK / 4; ++st) {
+      const int cf = st & 1, nf = cf ^ 1;
+      if (st + 1 < kDtlBK / 4) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) a[nf][i] = Sa[dtl_elem<AK>(xa + 16 * i, 4 * (st + 1) + kl)];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) b[nf][j] = Sb[dtl_elem<BKc>(xb + 16 * j, 4 * (st + 1) + kl)];
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = F::run(a[cf][i], b[cf][j], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the next tile's loads have landed in LDS
+    __syncthreads();
+  }
+  if (gridDim.y > 1) {
+    float *W = p.ws + int64_t(blockIdx.y) * M * N;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int r = 0; r < F::R; ++r) {
+        const int row = m0 + wm * TM * 16 + i * 16 + F::row(lane, r);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          W[int64_t(row) * N + n0 + wn * TN * 16 + j * 16 + lm] = acc[i][j][r];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int r = 0; r < F::R; ++r) {
+      const int row = m0 + wm * TM * 16 + i * 16 + F::row(lane, r);
+      float *__restrict__ crow = Cp + int64_t(row) * p.ldc;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn * TN * 16 + j * 16 + lm;
+        crow[col] = apply_epi(acc[i][j][r], row, col, p.ep);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // ---- GEMV: y[1 x N] = x[1 x K] * B[K x N] -----------------------------------
 //
 // HBM-bound: B (K*N floats) is read once.  Pass 1: workgroup (ct, ks) covers
@@ -607,11 +770,39 @@ int launch_cfg(const gemm_args &a, int64_t batch, int splits, hipStream_t s) {
   return splits;  // >= 1: the number of K splits actually launched
 }
 
+template <bool TA, bool TB>
+int launch_dtl(const gemm_args &a, int64_t batch, int splits, hipStream_t s) {
+  auto kern = sgemm_dtl_k<TA, TB>;
+  static bool attr_done = false;
+  if (!attr_done) {
+    SILGPU_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         kDtlLdsBytes));
+    attr_done = true;
+  }
+  gemm_args g = a;
+  g.tiles_m = static_cast<int>(a.M / kDtlTile);
+  g.tiles_n = static_cast<int>(a.N / kDtlTile);
+  g.klen = static_cast<int>(cdiv(cdiv(a.K, splits), kDtlBK) * kDtlBK);
+  if (g.klen < kDtlBK) g.klen = kDtlBK;
+  splits = static_cast<int>(a.K > 0 ? cdiv(a.K, g.klen) : 1);
+  dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(splits),
+            static_cast<unsigned>(batch));
+  kern<<<grid, 512, kDtlLdsBytes, s>>>(g);
+  SILGPU_LAUNCH_CHECK("sgemm_dtl_k");
+  return splits;
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int MI, bool TA, bool TB>
 int launch_tb(const gemm_args &a, int64_t batch, int splits, bool vec, hipStream_t s) {
   // Every split's K range is a multiple of BK except possibly the last, and
   // that one is too when K is.
   const bool edge = (a.M % BM) || (a.N % BN) || (a.K % BK);
+  // Full 256 x 256 tiles of 16-byte aligned operands: LDS-direct loads.
+  if constexpr (BM == kDtlTile && BN == kDtlTile) {
+    if (vec && a.M % kDtlTile == 0 && a.N % kDtlTile == 0 && a.K % kDtlBK == 0)
+      return launch_dtl<TA, TB>(a, batch, splits, s);
+  }
   if (vec) {
     return edge ? launch_cfg<BM, BN, BK, WM, WN, MI, TA, TB, true, true>(a, batch, splits, s)
                 : launch_cfg<BM, BN, BK, WM, WN, MI, TA, TB, true, false>(a, batch, splits, s);

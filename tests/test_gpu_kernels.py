@@ -651,3 +651,30 @@ def test_gemm_desc_validation(native):
                     residual=dA, ldr=4)
     with pytest.raises(native.SilGpuError, match="ldc"):
         native.gemm(0, 0, 4, 8, 4, dA, 4, dA, 8, dC, 4)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_sgemm_lds_direct_batched(native, oracle, ta, tb):
+    """Full 256 x 256 tiles take the LDS-direct kernel: batched, strided
+    (padded leading dimensions), every transpose, bias + relu epilogue."""
+    announce(f"sgemm lds-direct batched ta={ta} tb={tb}")
+    M, N, K, batch = 256, 512, 80, 3
+    g = rng(2300 + 2 * ta + tb)
+    lda = (M if ta else K) + 4
+    ldb = (K if tb else N) + 8
+    rows_a, rows_b = (K if ta else M), (N if tb else K)
+    A = g.uniform(-1, 1, (batch, rows_a, lda)).astype(np.float32)
+    B = g.uniform(-1, 1, (batch, rows_b, ldb)).astype(np.float32)
+    bias = g.normal(0, 1, N).astype(np.float32)
+    dA, dB, db, dC = up(native, A), up(native, B), up(native, bias), empty(native, batch * M * N)
+    native.sgemm_tuned(ta, tb, M, N, K, dA, lda, rows_a * lda, dB, ldb, rows_b * ldb, dC, N,
+                       M * N, batch, db, N, native.EPI_BIAS_RELU, tile=5, splits=1)
+    Cg = down(native, dC, (batch, M, N))
+    for z in range(batch):
+        a = A[z][:, :M] if ta else A[z][:, :K]
+        b = B[z][:, :K] if tb else B[z][:, :N]
+        C64, Cabs = oracle.sgemm_f64(np.ascontiguousarray(a), np.ascontiguousarray(b), ta=ta,
+                                     tb=tb, with_abs=True)
+        ref = np.maximum(C64 + bias, 0)
+        ok, nw, el = gemm_tolerance_ok(Cg[z], ref, Cabs + np.abs(bias), K)
+        assert ok, (z, nw, el)
