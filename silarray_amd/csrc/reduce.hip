@@ -29,6 +29,7 @@ constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
 constexpr int kUnroll = 8;          // 16-byte loads in flight per thread
 constexpr int kFullBlocks = 2048;   // pass-1 workgroups for a full reduction
+constexpr int kFinishLoads = 8;     // partials in flight per thread in pass 2
 
 enum { R_SUM = 0, R_MIN = 1, R_MAX = 2 };
 
@@ -151,8 +152,19 @@ template <int R>
 __global__ __launch_bounds__(kBlock) void reduce_finish_k(
     const typename racc<R>::T *__restrict__ partial, int np, float *__restrict__ out) {
   using T = typename racc<R>::T;
+  // Groups of kFinishLoads partials per thread are loaded together (one
+  // memory latency per group rather than per partial).
   T f = racc<R>::init();
-  for (int j = threadIdx.x; j < np; j += kBlock) f = racc<R>::merge(f, partial[j]);
+  for (int j0 = threadIdx.x; j0 < np; j0 += kFinishLoads * kBlock) {
+    T v[kFinishLoads];
+#pragma unroll
+    for (int g = 0; g < kFinishLoads; ++g) {
+      const int j = j0 + g * kBlock;
+      v[g] = j < np ? partial[j] : racc<R>::init();
+    }
+#pragma unroll
+    for (int g = 0; g < kFinishLoads; ++g) f = racc<R>::merge(f, v[g]);
+  }
   f = block_merge<R>(f);
   if (threadIdx.x == 0) out[0] = static_cast<float>(f);
 }
@@ -228,6 +240,7 @@ __global__ __launch_bounds__(kBlock) void row_sum_finish_k(const double *__restr
   const int64_t r = int64_t(blockIdx.x) * kBlock + threadIdx.x;
   if (r >= rows) return;
   double f = 0.0;
+#pragma unroll 8
   for (int64_t j = 0; j < chunks; ++j) f += partial[r * chunks + j];
   out[r] = static_cast<float>(f);
 }
@@ -285,6 +298,7 @@ __global__ __launch_bounds__(kBlock) void axis_sum_finish_k(const double *__rest
   const int64_t j = int64_t(blockIdx.x) * kBlock + threadIdx.x;
   if (j >= count) return;
   double f = 0.0;
+#pragma unroll 8
   for (int64_t s = 0; s < splits; ++s) f += partial[j * splits + s];
   out[j] = static_cast<float>(f);
 }
@@ -391,7 +405,16 @@ __global__ __launch_bounds__(kBlock) void argmax_finish_k(const vi *__restrict__
                                                           int32_t *__restrict__ out) {
   const int64_t r = blockIdx.x;
   vi f{NAN, 0, kNoIndex};
-  for (int64_t j = threadIdx.x; j < chunks; j += kBlock) f = better(f, partial[r * chunks + j]);
+  for (int64_t j0 = threadIdx.x; j0 < chunks; j0 += kFinishLoads * kBlock) {
+    vi v[kFinishLoads];
+#pragma unroll
+    for (int g = 0; g < kFinishLoads; ++g) {
+      const int64_t j = j0 + g * kBlock;
+      v[g] = j < chunks ? partial[r * chunks + j] : vi{NAN, 0, kNoIndex};
+    }
+#pragma unroll
+    for (int g = 0; g < kFinishLoads; ++g) f = better(f, v[g]);
+  }
   f = block_best(f);
   if (threadIdx.x == 0) out[r] = static_cast<int32_t>(f.i == kNoIndex ? 0 : f.i);
 }
