@@ -354,71 +354,92 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
   }
 }
 
-// ---- SGEMM with LDS-direct operand loads (256 x 256 x 16 tiles) ------------
+// ---- SGEMM with LDS-direct operand loads (BT x BT x 16 tiles, BT 256 or 128)
 //
-// Full tiles only (M, N multiples of 256, K range a multiple of 16, 16-byte
+// Full tiles only (M, N multiples of BT, K range a multiple of 16, 16-byte
 // aligned operands): every lane's 16-byte global_load_lds_dwordx4 stays in
 // bounds, so no lane needs masking.  The load engine writes each wave's 64 x
 // 16 bytes to one contiguous 1 KB LDS window (lane L at 16 L), with no
 // staging registers and no ds_write; the layout is chosen through which
-// global chunk each lane fetches:
-//   - an operand contiguous in K (A, or B transposed): a window holds 16
-//     rows x 16 k; the 16-byte chunk of (row rr, k quad kq) sits at position
-//     rr*4 + (kq ^ ((rr/4) & 3)), which makes the 16x16x4 fragment reads
-//     (16 rows x 4 k per instruction) touch 64 distinct banks;
-//   - an operand contiguous in M or N (A transposed, or B): one window per
-//     k row, pitch kDtlPitch = 272 floats so the 4 k rows a fragment read
-//     touches fall on disjoint 16-bank groups.
-// Eight waves (2 x 4) own 128 x 64 of C each; the next K tile's loads are
-// issued before the current tile is multiplied, and one s_waitcnt + barrier
-// ends each tile.
-constexpr int kDtlTile = 256, kDtlBK = 16, kDtlPitch = 272;
-constexpr int kDtlWin = 16;                              // windows per operand and tile
-constexpr int kDtlStage = 2 * kDtlWin * kDtlPitch;  // floats: two operands, the larger layout
-constexpr int kDtlLdsBytes = 2 * kDtlStage * 4;
+// global chunk each lane fetches.  An operand tile (BT x 16) takes BT/16
+// windows either way:
+//   - contiguous in K (A, or B transposed): a window holds 16 rows x 16 k;
+//     the 16-byte chunk of (row rr, k quad kq) sits at position
+//     rr*4 + (kq ^ ((rr/4) & 3));
+//   - contiguous in M or N (A transposed, or B), BT = 256: one k row per
+//     window, pitch 272 floats;
+//   - contiguous in M or N, BT = 128: two k rows per window (lanes 0-31 the
+//     even row, 32-63 the odd row with its chunk index XOR 4), pitch 288.
+// Each makes the 16x16x4 fragment reads (16 rows x 4 k per instruction)
+// touch 64 distinct banks; tests/test_gemm_layout.py checks placement and
+// banks.  BT = 256: 8 waves (2 x 4) of 128 x 64; BT = 128: 4 waves (2 x 2)
+// of 64 x 64.  The next K tile's loads are issued before the current tile is
+// multiplied, and one s_waitcnt + barrier ends each tile.
+constexpr int kDtlBK = 16;
+
+template <int BT>
+struct dtl_cfg {
+  static constexpr int WM = 2, WN = BT == 256 ? 4 : 2;
+  static constexpr int kThreads = WM * WN * kWave;
+  static constexpr int TM = BT / WM / 16, TN = BT / WN / 16;  // 16x16 blocks per wave
+  static constexpr int kWin = BT / 16;                        // windows per operand tile
+  static constexpr int kPitch = BT == 256 ? 272 : 288;        // M/N-contiguous window pitch
+  static constexpr int kOperand = kWin * kPitch;              // floats (>= the K-contiguous 256)
+  static constexpr int kStage = 2 * kOperand;
+  static constexpr int kLdsBytes = 2 * kStage * 4;
+  static_assert(kWin % (WM * WN) == 0, "windows per wave");
+};
 
 __device__ __forceinline__ void dtl16(const float *src, float *lds_dst) {
   __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
                                    (__attribute__((address_space(3))) void *)lds_dst, 16, 0, 0);
 }
 
-// Per-lane source pointer and LDS window offset of window w (0..15) of one
-// operand tile.  KCONTIG: rows x0 + 16w .. +15 of a [rows][K] operand;
-// otherwise k row w of a [K][cols] operand at columns x0 ...
-template <bool KCONTIG>
+// Source of lane `lane` for window w of an operand tile starting at x0
+// (rows x0.. of a [rows][K] operand when KCONTIG, else columns x0.. of a
+// [K][cols] operand; k relative to the tile).
+template <bool KCONTIG, int BT>
 __device__ __forceinline__ const float *dtl_src(const float *base, int64_t ld, int x0, int w,
                                                 int lane) {
   if constexpr (KCONTIG) {
     const int rr = lane / 4, kq = (lane % 4) ^ ((rr / 4) & 3);
     return base + int64_t(x0 + 16 * w + rr) * ld + 4 * kq;
-  } else {
+  } else if constexpr (BT == 256) {
     return base + int64_t(w) * ld + x0 + 4 * lane;
+  } else {
+    const int par = lane / 32, c = (lane % 32) ^ (4 * par);
+    return base + int64_t(2 * w + par) * ld + x0 + 4 * c;
   }
 }
-template <bool KCONTIG>
+template <bool KCONTIG, int BT>
 __device__ __forceinline__ int dtl_window(int w) {
-  return KCONTIG ? w * 256 : w * kDtlPitch;
+  return KCONTIG ? w * 256 : w * dtl_cfg<BT>::kPitch;
 }
-// LDS offset (floats) of element (x, k) of a stage's operand tile.
-template <bool KCONTIG>
+// LDS offset (floats) of element (x, k) of an operand tile.
+template <bool KCONTIG, int BT>
 __device__ __forceinline__ int dtl_elem(int x, int k) {
-  if constexpr (KCONTIG)
+  if constexpr (KCONTIG) {
     return (x / 16) * 256 + ((x % 16) * 4 + ((k / 4) ^ (((x % 16) / 4) & 3))) * 4 + (k % 4);
-  else
-    return k * kDtlPitch + x;
+  } else if constexpr (BT == 256) {
+    return k * dtl_cfg<BT>::kPitch + x;
+  } else {
+    const int par = k % 2;
+    return (k / 2) * dtl_cfg<BT>::kPitch + (32 * par + ((x / 4) ^ (4 * par))) * 4 + (x % 4);
+  }
 }
 
-template <bool TA, bool TB>
-__global__ __launch_bounds__(512) void sgemm_dtl_k(gemm_args p) {
+template <int BT, bool TA, bool TB>
+__global__ __launch_bounds__(dtl_cfg<BT>::kThreads) void sgemm_dtl_k(gemm_args p) {
+  using D = dtl_cfg<BT>;
   using F = mfma<16>;
-  constexpr int TM = 8, TN = 4;  // 16 x 16 blocks per wave: 128 x 64
+  constexpr int TM = D::TM, TN = D::TN, NW = D::WM * D::WN, WPW = D::kWin / NW;
   constexpr bool AK = !TA, BKc = TB;  // operand contiguous in K
   extern __shared__ float lds[];
   const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
-  const int wm = wave / 4, wn = wave % 4;
+  const int wm = wave / D::WN, wn = wave % D::WN;
   int tm, tn;
   tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-  const int m0 = tm * kDtlTile, n0 = tn * kDtlTile;
+  const int m0 = tm * BT, n0 = tn * BT;
   const int64_t zo = blockIdx.z / p.binner, zi = blockIdx.z % p.binner;
   const float *__restrict__ A = p.A + zo * p.sA2 + zi * p.sA;
   const float *__restrict__ B = p.B + zo * p.sB2 + zi * p.sB;
@@ -427,22 +448,25 @@ __global__ __launch_bounds__(512) void sgemm_dtl_k(gemm_args p) {
   const int kbeg = blockIdx.y * p.klen;
   const int kend = min(p.K, kbeg + p.klen);
   const int KT = kend > kbeg ? (kend - kbeg) / kDtlBK : 0;  // K % 16 == 0 on this path
-  // Windows wave and wave + 8 of each operand.
-  const float *a_src0 = dtl_src<AK>(A, p.lda, m0, wave, lane);
-  const float *a_src1 = dtl_src<AK>(A, p.lda, m0, wave + 8, lane);
-  const float *b_src0 = dtl_src<BKc>(B, p.ldb, n0, wave, lane);
-  const float *b_src1 = dtl_src<BKc>(B, p.ldb, n0, wave + 8, lane);
+  // This wave loads windows wave + q*NW, q < WPW, of each operand.
+  const float *a_src[WPW], *b_src[WPW];
+#pragma unroll
+  for (int q = 0; q < WPW; ++q) {
+    a_src[q] = dtl_src<AK, BT>(A, p.lda, m0, wave + q * NW, lane);
+    b_src[q] = dtl_src<BKc, BT>(B, p.ldb, n0, wave + q * NW, lane);
+  }
   // Advance of one K tile for each operand.
   const int64_t a_step = AK ? kDtlBK : int64_t(kDtlBK) * p.lda;
   const int64_t b_step = BKc ? kDtlBK : int64_t(kDtlBK) * p.ldb;
-  constexpr int kAOff = 0, kBOff = kDtlWin * (AK ? 256 : kDtlPitch);
+  constexpr int kBOff = D::kOperand;
   auto issue = [&](int kt, int stage) {
-    float *S = lds + stage * kDtlStage;
+    float *S = lds + stage * D::kStage;
     const int64_t k = int64_t(kbeg / kDtlBK + kt);
-    dtl16(a_src0 + k * a_step, S + kAOff + dtl_window<AK>(wave));
-    dtl16(a_src1 + k * a_step, S + kAOff + dtl_window<AK>(wave + 8));
-    dtl16(b_src0 + k * b_step, S + kBOff + dtl_window<BKc>(wave));
-    dtl16(b_src1 + k * b_step, S + kBOff + dtl_window<BKc>(wave + 8));
+#pragma unroll
+    for (int q = 0; q < WPW; ++q) {
+      dtl16(a_src[q] + k * a_step, S + dtl_window<AK, BT>(wave + q * NW));
+      dtl16(b_src[q] + k * b_step, S + kBOff + dtl_window<BKc, BT>(wave + q * NW));
+    }
   };
   typename F::acc_t acc[TM][TN];
 #pragma unroll
@@ -461,21 +485,23 @@ __global__ __launch_bounds__(512) void sgemm_dtl_k(gemm_args p) {
   for (int kt = 0; kt < KT; ++kt) {
     const int cur = kt & 1;
     if (kt + 1 < KT) issue(kt + 1, cur ^ 1);
-    const float *Sa = lds + cur * kDtlStage + kAOff;
-    const float *Sb = lds + cur * kDtlStage + kBOff;
+    const float *Sa = lds + cur * D::kStage;
+    const float *Sb = Sa + kBOff;
     float a[2][TM], b[2][TN];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) a[0][i] = Sa[dtl_elem<AK>(xa + 16 * i, kl)];
+    for (int i = 0; i < TM; ++i) a[0][i] = Sa[dtl_elem<AK, BT>(xa + 16 * i, kl)];
 #pragma unroll
-    for (int j = 0; j < TN; ++j) b[0][j] = Sb[dtl_elem<BKc>(xb + 16 * j, kl)];
+    for (int j = 0; j < TN; ++j) b[0][j] = Sb[dtl_elem<BKc, BT>(xb + 16 * j, kl)];
 #pragma unroll
     for (int st = 0; st < kDtlBK / 4; ++st) {
       const int cf = st & 1, nf = cf ^ 1;
       if (st + 1 < kDtlBK / 4) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i) a[nf][i] = Sa[dtl_elem<AK>(xa + 16 * i, 4 * (st + 1) + kl)];
+        for (int i = 0; i < TM; ++i)
+          a[nf][i] = Sa[dtl_elem<AK, BT>(xa + 16 * i, 4 * (st + 1) + kl)];
 #pragma unroll
-        for (int j = 0; j < TN; ++j) b[nf][j] = Sb[dtl_elem<BKc>(xb + 16 * j, 4 * (st + 1) + kl)];
+        for (int j = 0; j < TN; ++j)
+          b[nf][j] = Sb[dtl_elem<BKc, BT>(xb + 16 * j, 4 * (st + 1) + kl)];
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
@@ -770,25 +796,26 @@ int launch_cfg(const gemm_args &a, int64_t batch, int splits, hipStream_t s) {
   return splits;  // >= 1: the number of K splits actually launched
 }
 
-template <bool TA, bool TB>
+template <int BT, bool TA, bool TB>
 int launch_dtl(const gemm_args &a, int64_t batch, int splits, hipStream_t s) {
-  auto kern = sgemm_dtl_k<TA, TB>;
+  using D = dtl_cfg<BT>;
+  auto kern = sgemm_dtl_k<BT, TA, TB>;
   static bool attr_done = false;
   if (!attr_done) {
     SILGPU_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                          hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         kDtlLdsBytes));
+                                         D::kLdsBytes));
     attr_done = true;
   }
   gemm_args g = a;
-  g.tiles_m = static_cast<int>(a.M / kDtlTile);
-  g.tiles_n = static_cast<int>(a.N / kDtlTile);
+  g.tiles_m = static_cast<int>(a.M / BT);
+  g.tiles_n = static_cast<int>(a.N / BT);
   g.klen = static_cast<int>(cdiv(cdiv(a.K, splits), kDtlBK) * kDtlBK);
   if (g.klen < kDtlBK) g.klen = kDtlBK;
   splits = static_cast<int>(a.K > 0 ? cdiv(a.K, g.klen) : 1);
   dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(splits),
             static_cast<unsigned>(batch));
-  kern<<<grid, 512, kDtlLdsBytes, s>>>(g);
+  kern<<<grid, D::kThreads, D::kLdsBytes, s>>>(g);
   SILGPU_LAUNCH_CHECK("sgemm_dtl_k");
   return splits;
 }
@@ -798,10 +825,10 @@ int launch_tb(const gemm_args &a, int64_t batch, int splits, bool vec, hipStream
   // Every split's K range is a multiple of BK except possibly the last, and
   // that one is too when K is.
   const bool edge = (a.M % BM) || (a.N % BN) || (a.K % BK);
-  // Full 256 x 256 tiles of 16-byte aligned operands: LDS-direct loads.
-  if constexpr (BM == kDtlTile && BN == kDtlTile) {
-    if (vec && a.M % kDtlTile == 0 && a.N % kDtlTile == 0 && a.K % kDtlBK == 0)
-      return launch_dtl<TA, TB>(a, batch, splits, s);
+  // Full square tiles of 16-byte aligned operands: LDS-direct loads.
+  if constexpr (BM == BN && (BM == 256 || BM == 128)) {
+    if (vec && a.M % BM == 0 && a.N % BN == 0 && a.K % kDtlBK == 0)
+      return launch_dtl<BM, TA, TB>(a, batch, splits, s);
   }
   if (vec) {
     return edge ? launch_cfg<BM, BN, BK, WM, WN, MI, TA, TB, true, true>(a, batch, splits, s)
