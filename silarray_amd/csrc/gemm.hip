@@ -924,20 +924,21 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch) {
   }
   // Predicted time of each (tile, K split): every CU runs ceil(WG / 256)
   // workgroups, min(that, occupancy) of them at once; a SIMD holding a
-  // single wavefront reaches 0.8 of the rate it reaches with two or more.
-  // eff is the measured fraction of fp32 MFMA peak of each tile at large K,
-  // and the K loop reaches half its rate at klen = kK0.  Split-K adds the
-  // partial-sum pass.  Fitted to a tile/split sweep of square and
-  // transformer-block shapes on MI355X.
+  // single wavefront reaches kSingleWave of the rate it reaches with two or
+  // more.  eff is the fraction of fp32 MFMA peak each tile reaches at large
+  // K, and the K loop reaches half its rate at klen = kK0.  Split-K adds the
+  // partial-sum pass: one launch plus (splits + 1) M x N fp32 passes, whose
+  // partials mostly come back from the last-level cache.  Fitted to a
+  // tile/split sweep of square and transformer-block shapes on MI355X.
   struct cand {
     int tile, bm, bn, bk, waves, occupancy;
     double eff;
   };
-  static const cand cands[] = {{TILE_256x256, 256, 256, 16, 8, 1, 0.88},
-                               {TILE_128x128, 128, 128, 16, 4, 3, 0.86},
-                               {TILE_128x64, 128, 64, 16, 4, 5, 0.88},
-                               {TILE_64x64, 64, 64, 16, 4, 8, 0.74}};
-  constexpr double kK0 = 128.0, kSingleWave = 0.8;
+  static const cand cands[] = {{TILE_256x256, 256, 256, 16, 8, 1, 0.87},
+                               {TILE_128x128, 128, 128, 16, 4, 3, 0.84},
+                               {TILE_128x64, 128, 64, 16, 4, 5, 0.75},
+                               {TILE_64x64, 64, 64, 16, 4, 8, 0.64}};
+  constexpr double kK0 = 64.0, kSingleWave = 0.76, kReduceBw = 2.0e13, kLaunch = 4.0e-6;
   const double rate_cu = 157.3e12 / 256.0;
   plan best{TILE_128x128, 1};
   double best_t = 1e30;
@@ -953,7 +954,7 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch) {
                                                                 : kSingleWave * per_simd;
       double t = double(per_cu) * 2.0 * cd.bm * cd.bn * klen /
                  (rate_cu * cd.eff * f * (klen / (klen + kK0)));
-      if (sp > 1) t += double(sp) * double(M) * double(N) * 8.0 / 5.0e12 + 4.0e-6;
+      if (sp > 1) t += double(sp + 1) * double(M) * double(N) * 4.0 / kReduceBw + kLaunch;
       if (t < best_t * 0.999) {
         best_t = t;
         best = plan{cd.tile, sp};
