@@ -354,40 +354,55 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
   }
 }
 
-// ---- SGEMM with LDS-direct operand loads (BT x BT x 16 tiles, BT 256 or 128)
+// ---- SGEMM with LDS-direct operand loads (BT x BT x BK tiles, BT 256 or 128)
 //
-// Full tiles only (M, N multiples of BT, K range a multiple of 16, 16-byte
+// Full tiles only (M, N multiples of BT, K range a multiple of BK, 16-byte
 // aligned operands): every lane's 16-byte global_load_lds_dwordx4 stays in
 // bounds, so no lane needs masking.  The load engine writes each wave's 64 x
 // 16 bytes to one contiguous 1 KB LDS window (lane L at 16 L), with no
 // staging registers and no ds_write; the layout is chosen through which
-// global chunk each lane fetches.  An operand tile (BT x 16) takes BT/16
-// windows either way:
-//   - contiguous in K (A, or B transposed): a window holds 16 rows x 16 k;
-//     the 16-byte chunk of (row rr, k quad kq) sits at position
-//     rr*4 + (kq ^ ((rr/4) & 3));
+// global chunk each lane fetches.  An operand tile (BT x BK) takes
+// BT * BK / 256 windows either way:
+//   - contiguous in K (A, or B transposed): a window holds 16 rows x 16 k,
+//     window kh * BT/16 + rg holding rows 16 rg.. and k 16 kh..; the 16-byte
+//     chunk of (row rr, k quad kq) sits at position rr*4 + (kq ^ ((rr/2) & 3));
 //   - contiguous in M or N (A transposed, or B), BT = 256: one k row per
-//     window, pitch 272 floats;
+//     window, pitch 260 floats;
 //   - contiguous in M or N, BT = 128: two k rows per window (lanes 0-31 the
-//     even row, 32-63 the odd row with its chunk index XOR 4), pitch 288.
-// Each makes the 16x16x4 fragment reads (16 rows x 4 k per instruction)
-// touch 64 distinct banks; tests/test_gemm_layout.py checks placement and
-// banks.  BT = 256: 8 waves (2 x 4) of 128 x 64; BT = 128: 4 waves (2 x 2)
-// of 64 x 64.  The next K tile's loads are issued before the current tile is
-// multiplied, and one s_waitcnt + barrier ends each tile.
-constexpr int kDtlBK = 16;
+//     even row, 32-63 the odd row), pitch 264.
+// MFMA step j of a 16-deep k block puts k = 4g + j in the k slot g = lane/16
+// of both operands (any assignment of k to slots sums the same products), so
+// a K-contiguous operand is read with one ds_read_b128 per 16-row block and
+// k block -- lane (r, g) takes k = 4g .. 4g+3 of row r, one value for each of
+// the four steps -- and an M/N-contiguous one with one ds_read_b32 per block
+// and step.  LDS on gfx950 serves ds_read_b32 one half-wave per pass over 32
+// banks and ds_read_b128 16 lanes per pass (equal lane bit 5 and equal
+// parity of lane bits 2-4) over 64 banks, as measured with the bank-conflict
+// counter; the swizzle and pitches make every read conflict-free under that
+// model (tests/test_gemm_layout.py).  BT = 256: 8 waves (2 x 4) of 128 x 64;
+// BT = 128: 4 waves (2 x 2) of 64 x 64.  The next K tile's loads are issued
+// before the current tile is multiplied, and one s_waitcnt + barrier ends
+// each tile; BK = 32 halves the barriers per flop (two 256 x 32 stages take
+// 130 KB of the 160 KB LDS).
+constexpr int kDtlBK = 16;  // K granularity of the path (BK = 16 or 32)
 
-template <int BT>
+template <int BT, int BK>
 struct dtl_cfg {
   static constexpr int WM = 2, WN = BT == 256 ? 4 : 2;
   static constexpr int kThreads = WM * WN * kWave;
   static constexpr int TM = BT / WM / 16, TN = BT / WN / 16;  // 16x16 blocks per wave
-  static constexpr int kWin = BT / 16;                        // windows per operand tile
-  static constexpr int kPitch = BT == 256 ? 272 : 288;        // M/N-contiguous window pitch
+  static constexpr int kWin = BT * BK / 256;                  // windows per operand tile
+  static constexpr int kPitch = BT == 256 ? 260 : 264;        // M/N-contiguous window pitch
   static constexpr int kOperand = kWin * kPitch;              // floats (>= the K-contiguous 256)
   static constexpr int kStage = 2 * kOperand;
-  static constexpr int kLdsBytes = 2 * kStage * 4;
-  static_assert(kWin % (WM * WN) == 0, "windows per wave");
+  static constexpr int kLdsBytes = 2 * kStage * 4;  // static, two arrays of kStage floats
+  // Waves per SIMD the register allocation aims at: one 8-wave workgroup per
+  // CU (LDS allows no second) for BT = 256, three 4-wave workgroups for 128.
+  // Without it the compiler squeezes the 256 tile toward three waves and
+  // serialises the first fragment reads of every K tile.
+  static constexpr int kWavesPerEU = BT == 256 ? 2 : 3;
+  static_assert(BK % kDtlBK == 0 && kWin % (WM * WN) == 0, "windows per wave");
+  static_assert(kLdsBytes <= 160 * 1024, "LDS");
 };
 
 __device__ __forceinline__ void dtl16(const float *src, float *lds_dst) {
@@ -402,39 +417,45 @@ template <bool KCONTIG, int BT>
 __device__ __forceinline__ const float *dtl_src(const float *base, int64_t ld, int x0, int w,
                                                 int lane) {
   if constexpr (KCONTIG) {
-    const int rr = lane / 4, kq = (lane % 4) ^ ((rr / 4) & 3);
-    return base + int64_t(x0 + 16 * w + rr) * ld + 4 * kq;
+    const int rr = lane / 4, kq = (lane % 4) ^ ((rr / 2) & 3);
+    const int rg = w % (BT / 16), kh = w / (BT / 16);
+    return base + int64_t(x0 + 16 * rg + rr) * ld + 16 * kh + 4 * kq;
   } else if constexpr (BT == 256) {
     return base + int64_t(w) * ld + x0 + 4 * lane;
   } else {
-    const int par = lane / 32, c = (lane % 32) ^ (4 * par);
-    return base + int64_t(2 * w + par) * ld + x0 + 4 * c;
+    return base + int64_t(2 * w + lane / 32) * ld + x0 + 4 * (lane % 32);
   }
 }
 template <bool KCONTIG, int BT>
 __device__ __forceinline__ int dtl_window(int w) {
-  return KCONTIG ? w * 256 : w * dtl_cfg<BT>::kPitch;
+  return KCONTIG ? w * 256 : w * dtl_cfg<BT, kDtlBK>::kPitch;
 }
 // LDS offset (floats) of element (x, k) of an operand tile.
 template <bool KCONTIG, int BT>
 __device__ __forceinline__ int dtl_elem(int x, int k) {
   if constexpr (KCONTIG) {
-    return (x / 16) * 256 + ((x % 16) * 4 + ((k / 4) ^ (((x % 16) / 4) & 3))) * 4 + (k % 4);
+    return ((k / 16) * (BT / 16) + x / 16) * 256 +
+           ((x % 16) * 4 + (((k % 16) / 4) ^ (((x % 16) / 2) & 3))) * 4 + (k % 4);
   } else if constexpr (BT == 256) {
-    return k * dtl_cfg<BT>::kPitch + x;
+    return k * dtl_cfg<BT, kDtlBK>::kPitch + x;
   } else {
-    const int par = k % 2;
-    return (k / 2) * dtl_cfg<BT>::kPitch + (32 * par + ((x / 4) ^ (4 * par))) * 4 + (x % 4);
+    return (k / 2) * dtl_cfg<BT, kDtlBK>::kPitch + 128 * (k % 2) + x;
   }
 }
 
-template <int BT, bool TA, bool TB>
-__global__ __launch_bounds__(dtl_cfg<BT>::kThreads) void sgemm_dtl_k(gemm_args p) {
-  using D = dtl_cfg<BT>;
+template <int BT, int BK, bool TA, bool TB>
+__global__ __launch_bounds__((dtl_cfg<BT, BK>::kThreads))
+__attribute__((amdgpu_waves_per_eu(dtl_cfg<BT, BK>::kWavesPerEU,
+                                   dtl_cfg<BT, BK>::kWavesPerEU))) void sgemm_dtl_k(gemm_args p) {
+  using D = dtl_cfg<BT, BK>;
   using F = mfma<16>;
   constexpr int TM = D::TM, TN = D::TN, NW = D::WM * D::WN, WPW = D::kWin / NW;
   constexpr bool AK = !TA, BKc = TB;  // operand contiguous in K
-  extern __shared__ float lds[];
+  // Two stages as two LDS objects: alias analysis then sees that the loads
+  // into one stage cannot touch the fragment reads from the other, and the
+  // compiler adds no wait for the prefetch before those reads.
+  __shared__ __attribute__((aligned(16))) float lds0[D::kStage];
+  __shared__ __attribute__((aligned(16))) float lds1[D::kStage];
   const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
   const int wm = wave / D::WN, wn = wave % D::WN;
   int tm, tn;
@@ -447,7 +468,7 @@ __global__ __launch_bounds__(dtl_cfg<BT>::kThreads) void sgemm_dtl_k(gemm_args p
   const int M = p.M, N = p.N;
   const int kbeg = blockIdx.y * p.klen;
   const int kend = min(p.K, kbeg + p.klen);
-  const int KT = kend > kbeg ? (kend - kbeg) / kDtlBK : 0;  // K % 16 == 0 on this path
+  const int KT = kend > kbeg ? (kend - kbeg) / BK : 0;  // K % BK == 0 on this path
   // This wave loads windows wave + q*NW, q < WPW, of each operand.
   const float *a_src[WPW], *b_src[WPW];
 #pragma unroll
@@ -456,12 +477,11 @@ __global__ __launch_bounds__(dtl_cfg<BT>::kThreads) void sgemm_dtl_k(gemm_args p
     b_src[q] = dtl_src<BKc, BT>(B, p.ldb, n0, wave + q * NW, lane);
   }
   // Advance of one K tile for each operand.
-  const int64_t a_step = AK ? kDtlBK : int64_t(kDtlBK) * p.lda;
-  const int64_t b_step = BKc ? kDtlBK : int64_t(kDtlBK) * p.ldb;
+  const int64_t a_step = AK ? BK : int64_t(BK) * p.lda;
+  const int64_t b_step = BKc ? BK : int64_t(BK) * p.ldb;
   constexpr int kBOff = D::kOperand;
-  auto issue = [&](int kt, int stage) {
-    float *S = lds + stage * D::kStage;
-    const int64_t k = int64_t(kbeg / kDtlBK + kt);
+  auto issue = [&](int kt, float *S) {
+    const int64_t k = int64_t(kbeg / BK + kt);
 #pragma unroll
     for (int q = 0; q < WPW; ++q) {
       dtl16(a_src[q] + k * a_step, S + dtl_window<AK, BT>(wave + q * NW));
@@ -475,42 +495,88 @@ __global__ __launch_bounds__(dtl_cfg<BT>::kThreads) void sgemm_dtl_k(gemm_args p
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < F::R; ++r) acc[i][j][r] = 0.0f;
-  const int lm = lane % 16, kl = lane / 16;
+  const int lm = lane % 16, kg = lane / 16;
   const int xa = wm * TM * 16 + lm, xb = wn * TN * 16 + lm;
+  // Fragments.  K-contiguous operand: four floats (steps 0-3) per 16-row
+  // block, double-buffered over k blocks; M/N-contiguous: one float per block
+  // for one step, double-buffered over steps.
+  constexpr int kSteps = BK / 4, kBlocks = BK / 16;
+  float a4[2][AK ? TM : 1][4], b4[2][BKc ? TN : 1][4];
+  float a1[2][AK ? 1 : TM], b1[2][BKc ? 1 : TN];
+  auto read4 = [](float (&dst)[4], const float *src) {
+    const float4 v = *reinterpret_cast<const float4 *>(src);
+    dst[0] = v.x;
+    dst[1] = v.y;
+    dst[2] = v.z;
+    dst[3] = v.w;
+  };
+  // Reads for k block kh (K-contiguous operands) or step st (M/N-contiguous).
+  auto read_block = [&](const float *Sa, const float *Sb, int kh) {
+    if constexpr (AK) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        read4(a4[kh & 1][i], Sa + dtl_elem<true, BT>(xa + 16 * i, 16 * kh + 4 * kg));
+    }
+    if constexpr (BKc) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        read4(b4[kh & 1][j], Sb + dtl_elem<true, BT>(xb + 16 * j, 16 * kh + 4 * kg));
+    }
+  };
+  auto read_step = [&](const float *Sa, const float *Sb, int st) {
+    const int k = 16 * (st / 4) + 4 * kg + st % 4;
+    if constexpr (!AK) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) a1[st & 1][i] = Sa[dtl_elem<false, BT>(xa + 16 * i, k)];
+    }
+    if constexpr (!BKc) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) b1[st & 1][j] = Sb[dtl_elem<false, BT>(xb + 16 * j, k)];
+    }
+  };
+  auto fa = [&](int st, int i) -> float {
+    if constexpr (AK) return a4[(st / 4) & 1][i][st % 4];
+    else return a1[st & 1][i];
+  };
+  auto fb = [&](int st, int j) -> float {
+    if constexpr (BKc) return b4[(st / 4) & 1][j][st % 4];
+    else return b1[st & 1][j];
+  };
   if (KT > 0) {
-    issue(0, 0);
+    issue(0, lds0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) issue(kt + 1, cur ^ 1);
-    const float *Sa = lds + cur * D::kStage;
+  // One K tile: fragments from stage Sa while the next tile loads into Snext.
+  auto tile = [&](const float *Sa, float *Snext, int kt) {
+    if (kt + 1 < KT) issue(kt + 1, Snext);
     const float *Sb = Sa + kBOff;
-    float a[2][TM], b[2][TN];
+    read_block(Sa, Sb, 0);
+    read_step(Sa, Sb, 0);
+    __builtin_amdgcn_sched_barrier(0);  // all first-step reads in flight together
 #pragma unroll
-    for (int i = 0; i < TM; ++i) a[0][i] = Sa[dtl_elem<AK, BT>(xa + 16 * i, kl)];
+    for (int st = 0; st < kSteps; ++st) {
+      // Row block 0 first: the wait for this step's fragments (the compiler
+      // waits for all outstanding LDS reads) then comes before the next
+      // reads are issued, and the remaining MFMAs of the step cover them.
 #pragma unroll
-    for (int j = 0; j < TN; ++j) b[0][j] = Sb[dtl_elem<BKc, BT>(xb + 16 * j, kl)];
+      for (int j = 0; j < TN; ++j) acc[0][j] = F::run(fa(st, 0), fb(st, j), acc[0][j]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (st + 1 < kSteps) read_step(Sa, Sb, st + 1);
+      if (st % 4 == 0 && st / 4 + 1 < kBlocks) read_block(Sa, Sb, st / 4 + 1);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int st = 0; st < kDtlBK / 4; ++st) {
-      const int cf = st & 1, nf = cf ^ 1;
-      if (st + 1 < kDtlBK / 4) {
+      for (int i = 1; i < TM; ++i)
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-          a[nf][i] = Sa[dtl_elem<AK, BT>(xa + 16 * i, 4 * (st + 1) + kl)];
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          b[nf][j] = Sb[dtl_elem<BKc, BT>(xb + 16 * j, 4 * (st + 1) + kl)];
-      }
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = F::run(a[cf][i], b[cf][j], acc[i][j]);
+        for (int j = 0; j < TN; ++j) acc[i][j] = F::run(fa(st, i), fb(st, j), acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
     }
     __builtin_amdgcn_s_waitcnt(0);  // the next tile's loads have landed in LDS
     __syncthreads();
+  };
+  for (int kt = 0; kt < KT; kt += 2) {
+    tile(lds0, lds1, kt);
+    if (kt + 1 < KT) tile(lds1, lds0, kt + 1);
   }
   if (gridDim.y > 1) {
     float *W = p.ws + int64_t(blockIdx.y) * M * N;
@@ -796,26 +862,19 @@ int launch_cfg(const gemm_args &a, int64_t batch, int splits, hipStream_t s) {
   return splits;  // >= 1: the number of K splits actually launched
 }
 
-template <int BT, bool TA, bool TB>
+template <int BT, int BK, bool TA, bool TB>
 int launch_dtl(const gemm_args &a, int64_t batch, int splits, hipStream_t s) {
-  using D = dtl_cfg<BT>;
-  auto kern = sgemm_dtl_k<BT, TA, TB>;
-  static bool attr_done = false;
-  if (!attr_done) {
-    SILGPU_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         D::kLdsBytes));
-    attr_done = true;
-  }
+  using D = dtl_cfg<BT, BK>;
+  auto kern = sgemm_dtl_k<BT, BK, TA, TB>;
   gemm_args g = a;
   g.tiles_m = static_cast<int>(a.M / BT);
   g.tiles_n = static_cast<int>(a.N / BT);
-  g.klen = static_cast<int>(cdiv(cdiv(a.K, splits), kDtlBK) * kDtlBK);
-  if (g.klen < kDtlBK) g.klen = kDtlBK;
+  g.klen = static_cast<int>(cdiv(cdiv(a.K, splits), BK) * BK);
+  if (g.klen < BK) g.klen = BK;
   splits = static_cast<int>(a.K > 0 ? cdiv(a.K, g.klen) : 1);
   dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(splits),
             static_cast<unsigned>(batch));
-  kern<<<grid, D::kThreads, D::kLdsBytes, s>>>(g);
+  kern<<<grid, D::kThreads, 0, s>>>(g);
   SILGPU_LAUNCH_CHECK("sgemm_dtl_k");
   return splits;
 }
@@ -827,8 +886,12 @@ int launch_tb(const gemm_args &a, int64_t batch, int splits, bool vec, hipStream
   const bool edge = (a.M % BM) || (a.N % BN) || (a.K % BK);
   // Full square tiles of 16-byte aligned operands: LDS-direct loads.
   if constexpr (BM == BN && (BM == 256 || BM == 128)) {
-    if (vec && a.M % BM == 0 && a.N % BN == 0 && a.K % kDtlBK == 0)
-      return launch_dtl<BM, TA, TB>(a, batch, splits, s);
+    if (vec && a.M % BM == 0 && a.N % BN == 0 && a.K % kDtlBK == 0) {
+      if constexpr (BM == 256) {
+        if (a.K % 32 == 0) return launch_dtl<BM, 32, TA, TB>(a, batch, splits, s);
+      }
+      return launch_dtl<BM, kDtlBK, TA, TB>(a, batch, splits, s);
+    }
   }
   if (vec) {
     return edge ? launch_cfg<BM, BN, BK, WM, WN, MI, TA, TB, true, true>(a, batch, splits, s)

@@ -653,14 +653,18 @@ def test_gemm_desc_validation(native):
         native.gemm(0, 0, 4, 8, 4, dA, 4, dA, 8, dC, 4)
 
 
+@pytest.mark.parametrize("K,splits", [(80, 1), (96, 1), (96, 3), (80, 3)])
 @pytest.mark.parametrize("tile", [5, 1])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-def test_sgemm_lds_direct_batched(native, oracle, ta, tb, tile):
+def test_sgemm_lds_direct_batched(native, oracle, ta, tb, tile, K, splits):
     """Full 256 x 256 (tile 5) and 128 x 128 (tile 1) tiles take the
     LDS-direct kernel: batched, strided (padded leading dimensions), every
-    transpose, bias + relu epilogue."""
-    announce(f"sgemm lds-direct batched tile={tile} ta={ta} tb={tb}")
-    M, N, K, batch = 256, 512, 80, 3
+    transpose, bias + relu epilogue.  The 256 tile runs K tiles of 32 when
+    K % 32 == 0 (K = 96) and of 16 otherwise (K = 80); splits = 3 adds the
+    split-K partial pass (K ranges 32 + 32 + 32 and 32 + 32 + 16; split K
+    runs unbatched)."""
+    announce(f"sgemm lds-direct batched tile={tile} ta={ta} tb={tb} K={K} splits={splits}")
+    M, N, batch = 256, 512, (3 if splits == 1 else 1)
     g = rng(2300 + 2 * ta + tb)
     lda = (M if ta else K) + 4
     ldb = (K if tb else N) + 8
@@ -670,7 +674,7 @@ def test_sgemm_lds_direct_batched(native, oracle, ta, tb, tile):
     bias = g.normal(0, 1, N).astype(np.float32)
     dA, dB, db, dC = up(native, A), up(native, B), up(native, bias), empty(native, batch * M * N)
     native.sgemm_tuned(ta, tb, M, N, K, dA, lda, rows_a * lda, dB, ldb, rows_b * ldb, dC, N,
-                       M * N, batch, db, N, native.EPI_BIAS_RELU, tile=tile, splits=1)
+                       M * N, batch, db, N, native.EPI_BIAS_RELU, tile=tile, splits=splits)
     Cg = down(native, dC, (batch, M, N))
     for z in range(batch):
         a = A[z][:, :M] if ta else A[z][:, :K]
