@@ -386,21 +386,24 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
 // 130 KB of the 160 KB LDS).
 constexpr int kDtlBK = 16;  // K granularity of the path (BK = 16 or 32)
 
-template <int BT, int BK>
+// NW waves per workgroup in a 2 x NW/2 grid: BT = 256 with 8 waves (128 x 64
+// each, two waves per SIMD) or 4 waves (128 x 128, one wave per SIMD with 256
+// accumulators per lane); BT = 128 with 4 waves of 64 x 64.
+template <int BT, int BK, int NW = BT == 256 ? 8 : 4, int NS = 2>
 struct dtl_cfg {
-  static constexpr int WM = 2, WN = BT == 256 ? 4 : 2;
+  static constexpr int WM = 2, WN = NW / 2;
   static constexpr int kThreads = WM * WN * kWave;
   static constexpr int TM = BT / WM / 16, TN = BT / WN / 16;  // 16x16 blocks per wave
   static constexpr int kWin = BT * BK / 256;                  // windows per operand tile
   static constexpr int kPitch = BT == 256 ? 260 : 264;        // M/N-contiguous window pitch
   static constexpr int kOperand = kWin * kPitch;              // floats (>= the K-contiguous 256)
   static constexpr int kStage = 2 * kOperand;
-  static constexpr int kLdsBytes = 2 * kStage * 4;  // static, two arrays of kStage floats
+  static constexpr int kLdsBytes = NS * kStage * 4;  // static, NS arrays of kStage floats
   // Waves per SIMD the register allocation aims at: one 8-wave workgroup per
   // CU (LDS allows no second) for BT = 256, three 4-wave workgroups for 128.
   // Without it the compiler squeezes the 256 tile toward three waves and
   // serialises the first fragment reads of every K tile.
-  static constexpr int kWavesPerEU = BT == 256 ? 2 : 3;
+  static constexpr int kWavesPerEU = BT == 256 ? NW / 4 : 3;
   static_assert(BK % kDtlBK == 0 && kWin % (WM * WN) == 0, "windows per wave");
   static_assert(kLdsBytes <= 160 * 1024, "LDS");
 };
@@ -443,19 +446,30 @@ __device__ __forceinline__ int dtl_elem(int x, int k) {
   }
 }
 
-template <int BT, int BK, bool TA, bool TB>
-__global__ __launch_bounds__((dtl_cfg<BT, BK>::kThreads))
-__attribute__((amdgpu_waves_per_eu(dtl_cfg<BT, BK>::kWavesPerEU,
-                                   dtl_cfg<BT, BK>::kWavesPerEU))) void sgemm_dtl_k(gemm_args p) {
-  using D = dtl_cfg<BT, BK>;
+// s_waitcnt vmcnt(N) lgkmcnt(0), expcnt not waited (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
+}
+
+template <int BT, int BK, int NWV, int NS, bool TA, bool TB>
+__global__ __launch_bounds__((dtl_cfg<BT, BK, NWV, NS>::kThreads))
+__attribute__((amdgpu_waves_per_eu(dtl_cfg<BT, BK, NWV, NS>::kWavesPerEU,
+                                   dtl_cfg<BT, BK, NWV, NS>::kWavesPerEU))) void sgemm_dtl_k(gemm_args p) {
+  using D = dtl_cfg<BT, BK, NWV, NS>;
+  static_assert(NS == 2 || NS == 4, "stages");
   using F = mfma<16>;
   constexpr int TM = D::TM, TN = D::TN, NW = D::WM * D::WN, WPW = D::kWin / NW;
   constexpr bool AK = !TA, BKc = TB;  // operand contiguous in K
-  // Two stages as two LDS objects: alias analysis then sees that the loads
-  // into one stage cannot touch the fragment reads from the other, and the
-  // compiler adds no wait for the prefetch before those reads.
+  // NS stages as NS LDS objects: alias analysis then sees that the loads
+  // into one stage cannot touch the fragment reads from another, and the
+  // compiler adds no wait for the prefetch before those reads.  Tile kt
+  // reads stage kt % NS and issues the loads of tile kt + NS - 1.
   __shared__ __attribute__((aligned(16))) float lds0[D::kStage];
   __shared__ __attribute__((aligned(16))) float lds1[D::kStage];
+  __shared__ __attribute__((aligned(16))) float lds2[NS > 2 ? D::kStage : 4];
+  __shared__ __attribute__((aligned(16))) float lds3[NS > 2 ? D::kStage : 4];
   const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
   const int wm = wave / D::WN, wn = wave % D::WN;
   int tm, tn;
@@ -542,18 +556,51 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BT, BK>::kWavesPerEU,
     if constexpr (BKc) return b4[(st / 4) & 1][j][st % 4];
     else return b1[st & 1][j];
   };
+  // Waits until this wave's loads of tile `next` have landed, leaving the
+  // loads of the tiles after it (at most NS - 2, kDma instructions each) in
+  // flight, then the barrier makes every wave's loads visible.
+  constexpr int kDma = 2 * WPW;
+  auto land = [&](int next) {
+    if constexpr (NS == 2) {
+      wait_vm_lgkm0<0>();
+    } else {
+      const int after = min(KT - 1, next + NS - 2) - next;
+      if (after >= 2)
+        wait_vm_lgkm0<2 * kDma>();
+      else if (after == 1)
+        wait_vm_lgkm0<kDma>();
+      else
+        wait_vm_lgkm0<0>();
+    }
+    // The barrier as an opaque instruction: the compiler puts a full
+    // s_waitcnt 0 before every s_barrier it sees on this target, and a
+    // workgroup fence waits for the LDS-direct loads too (they write LDS), so
+    // either would also wait for the prefetch of the tiles after `next`.  The
+    // waits above have landed this wave's part of tile `next` in LDS and
+    // completed its reads of the stage the next loads overwrite; the
+    // "memory" clobber keeps the compiler from moving LDS accesses across.
+    asm volatile("s_barrier" ::: "memory");
+  };
   if (KT > 0) {
     issue(0, lds0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    if constexpr (NS == 4) {
+      if (1 < KT) issue(1, lds1);
+      if (2 < KT) issue(2, lds2);
+    }
+    land(0);
   }
-  // One K tile: fragments from stage Sa while the next tile loads into Snext.
+  // One K tile: fragments from stage Sa while tile kt + NS - 1 loads into
+  // Snext (the stage the previous tile read).  The loads are issued after the
+  // first fragment reads: where the compiler cannot tell the stages apart
+  // (at the loop head) it waits for all loads before reading, and then those
+  // are loads issued one tile or more earlier, not the ones just issued.
   auto tile = [&](const float *Sa, float *Snext, int kt) {
-    if (kt + 1 < KT) issue(kt + 1, Snext);
     const float *Sb = Sa + kBOff;
     read_block(Sa, Sb, 0);
     read_step(Sa, Sb, 0);
     __builtin_amdgcn_sched_barrier(0);  // all first-step reads in flight together
+    if (kt + NS - 1 < KT) issue(kt + NS - 1, Snext);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) {
       // Row block 0 first: the wait for this step's fragments (the compiler
@@ -571,12 +618,20 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BT, BK>::kWavesPerEU,
         for (int j = 0; j < TN; ++j) acc[i][j] = F::run(fa(st, i), fb(st, j), acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_s_waitcnt(0);  // the next tile's loads have landed in LDS
-    __syncthreads();
+    land(kt + 1);
   };
-  for (int kt = 0; kt < KT; kt += 2) {
-    tile(lds0, lds1, kt);
-    if (kt + 1 < KT) tile(lds1, lds0, kt + 1);
+  if constexpr (NS == 2) {
+    for (int kt = 0; kt < KT; kt += 2) {
+      tile(lds0, lds1, kt);
+      if (kt + 1 < KT) tile(lds1, lds0, kt + 1);
+    }
+  } else {
+    for (int kt = 0; kt < KT; kt += 4) {
+      tile(lds0, lds3, kt);
+      if (kt + 1 < KT) tile(lds1, lds0, kt + 1);
+      if (kt + 2 < KT) tile(lds2, lds1, kt + 2);
+      if (kt + 3 < KT) tile(lds3, lds2, kt + 3);
+    }
   }
   if (gridDim.y > 1) {
     float *W = p.ws + int64_t(blockIdx.y) * M * N;
@@ -862,10 +917,10 @@ int launch_cfg(const gemm_args &a, int64_t batch, int splits, hipStream_t s) {
   return splits;  // >= 1: the number of K splits actually launched
 }
 
-template <int BT, int BK, bool TA, bool TB>
+template <int BT, int BK, int NWV, int NS, bool TA, bool TB>
 int launch_dtl(const gemm_args &a, int64_t batch, int splits, hipStream_t s) {
-  using D = dtl_cfg<BT, BK>;
-  auto kern = sgemm_dtl_k<BT, BK, TA, TB>;
+  using D = dtl_cfg<BT, BK, NWV, NS>;
+  auto kern = sgemm_dtl_k<BT, BK, NWV, NS, TA, TB>;
   gemm_args g = a;
   g.tiles_m = static_cast<int>(a.M / BT);
   g.tiles_n = static_cast<int>(a.N / BT);
@@ -888,9 +943,10 @@ int launch_tb(const gemm_args &a, int64_t batch, int splits, bool vec, hipStream
   if constexpr (BM == BN && (BM == 256 || BM == 128)) {
     if (vec && a.M % BM == 0 && a.N % BN == 0 && a.K % kDtlBK == 0) {
       if constexpr (BM == 256) {
-        if (a.K % 32 == 0) return launch_dtl<BM, 32, TA, TB>(a, batch, splits, s);
-      }
-      return launch_dtl<BM, kDtlBK, TA, TB>(a, batch, splits, s);
+        if (a.K % 32 == 0) return launch_dtl<BM, 32, 8, 2, TA, TB>(a, batch, splits, s);
+        return launch_dtl<BM, kDtlBK, 8, 4, TA, TB>(a, batch, splits, s);
+      } else
+        return launch_dtl<BM, kDtlBK, 4, 2, TA, TB>(a, batch, splits, s);
     }
   }
   if (vec) {
