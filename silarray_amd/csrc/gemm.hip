@@ -116,7 +116,7 @@ struct gemm_args {
   epi_args ep;
   // Split K: workgroup row blockIdx.y covers K range [y*klen, (y+1)*klen)
   // (klen a multiple of BK).  With gridDim.y > 1 raw accumulators go to
-  // ws[y][M][N] and splitk_reduce_k applies the epilogue.
+  // ws[y][M][N] and splitk_sum_k applies the epilogue.
   int klen;
   float *ws;
 };
@@ -351,6 +351,209 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
       }
     }
     __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// ---- small-M SGEMM (M <= 32) -----------------------------------------------
+//
+// C = A * B with at most 32 rows of A is bound by reading B once (2M flops per
+// B element; at M = 32 about 15 flop/byte, below the fp32 ridge).  A
+// wavefront computes a 32 x 32Q block of C as Q accumulator sets of the
+// 32x32x2 MFMA: lane (c = lane % 32, s = lane / 32) supplies A row c and B
+// columns n0 + Q c + q (q < Q) of set q, so B (row-major [K][N]) arrives as
+// one Q-float vector load per k row straight into the MFMA operand registers
+// -- no LDS staging -- and 32 lanes read 128Q contiguous bytes of a row.  The
+// k values of a 16-deep chunk are assigned to the two k slots as
+// k = k0 + 8 s + j at MFMA step j < 8 (any assignment of k to slots adds the
+// same products), so lane s reads A[c][k0 + 8s .. k0 + 8s + 7], 32
+// contiguous bytes.  The four wavefronts of a workgroup take interleaved
+// chunks of the workgroup's K range and add their accumulators through LDS;
+// workgroups along grid y take disjoint K ranges (split K) and write raw
+// partial planes ws[y][M][N] that splitk_sum_k adds.  Rows >= M and columns
+// >= N read clamped in-range addresses and are never stored; k >= K reads as
+// zero in both operands.
+// TB: B is [N][K] (k contiguous): lane column n reads 8 consecutive k.
+// VA: A rows 16-byte aligned (lda % 4 == 0): two float4 loads per chunk.
+// VB (TB only): B rows 16-byte aligned: two float4 loads per column.
+constexpr int kSkWaves = 4;
+constexpr int kSkChunk = 16;  // k values per chunk (8 MFMA steps x 2 slots)
+
+template <int Q>
+struct vecf;
+template <>
+struct vecf<1> {
+  typedef float t;
+  __device__ static float get(t v, int) { return v; }
+};
+template <>
+struct vecf<2> {
+  typedef float2 t;
+  __device__ static float get(t v, int q) { return q == 0 ? v.x : v.y; }
+};
+template <>
+struct vecf<4> {
+  typedef float4 t;
+  __device__ static float get(t v, int q) {
+    return q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w;
+  }
+};
+
+template <int Q, bool TB, bool VA, bool VB>
+struct skinny_chunk {
+  float a[8];
+  float b[Q][8];
+
+  // Loads chunk k0 (k0 + 16 <= kend unless MASK).  arow: A row of this lane
+  // (clamped); bcol: first B column of this lane (clamped so the Q columns
+  // are in range).
+  template <bool MASK>
+  __device__ __forceinline__ void load(const float *__restrict__ A, int64_t lda,
+                                       const float *__restrict__ B, int64_t ldb, int arow,
+                                       int bcol, int k0, int s, int kend) {
+    const int kb = k0 + 8 * s;
+    const float *ap = A + int64_t(arow) * lda;
+    if constexpr (VA && !MASK) {
+      const float4 x0 = *reinterpret_cast<const float4 *>(ap + kb);
+      const float4 x1 = *reinterpret_cast<const float4 *>(ap + kb + 4);
+      a[0] = x0.x; a[1] = x0.y; a[2] = x0.z; a[3] = x0.w;
+      a[4] = x1.x; a[5] = x1.y; a[6] = x1.z; a[7] = x1.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int k = kb + j;
+        const float v = ap[MASK ? min(k, kend - 1) : k];
+        a[j] = (!MASK || k < kend) ? v : 0.0f;
+      }
+    }
+    if constexpr (!TB) {
+      typedef typename vecf<Q>::t V;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int k = kb + j;
+        const V v = *reinterpret_cast<const V *>(B + int64_t(MASK ? min(k, kend - 1) : k) * ldb +
+                                                 bcol);
+#pragma unroll
+        for (int q = 0; q < Q; ++q) b[q][j] = (!MASK || k < kend) ? vecf<Q>::get(v, q) : 0.0f;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        const float *bp = B + int64_t(bcol + q) * ldb;
+        if constexpr (VB && !MASK) {
+          const float4 x0 = *reinterpret_cast<const float4 *>(bp + kb);
+          const float4 x1 = *reinterpret_cast<const float4 *>(bp + kb + 4);
+          b[q][0] = x0.x; b[q][1] = x0.y; b[q][2] = x0.z; b[q][3] = x0.w;
+          b[q][4] = x1.x; b[q][5] = x1.y; b[q][6] = x1.z; b[q][7] = x1.w;
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int k = kb + j;
+            const float v = bp[MASK ? min(k, kend - 1) : k];
+            b[q][j] = (!MASK || k < kend) ? v : 0.0f;
+          }
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void mma(floatx16 (&acc)[Q]) const {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int q = 0; q < Q; ++q)
+        acc[q] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[j], b[q][j], acc[q], 0, 0, 0);
+  }
+};
+
+template <int Q, bool TB, bool VA, bool VB>
+__global__ __launch_bounds__(kSkWaves *kWave) void sgemm_skinny_k(gemm_args p) {
+  constexpr int U = Q == 4 ? 2 : 4;  // chunks in flight per wavefront
+  constexpr int STRIDE = kSkChunk * kSkWaves;
+  static_assert(16 % kSkWaves == 0 && kSkWaves * Q * 16 * kWave * 4 <= 65536, "LDS");
+  __shared__ float red[kSkWaves][Q * 16][kWave];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int c = lane % 32, s = lane / 32;
+  const int M = p.M, N = p.N, K = p.K;
+  const int n0 = blockIdx.x * (32 * Q);
+  const int arow = min(c, M - 1);
+  int bcol = n0 + Q * c;
+  if (bcol + Q > N) bcol = 0;  // whole vector out of range (N % Q == 0 when Q > 1)
+  const int kbeg = blockIdx.y * p.klen;
+  const int kend = min(K, kbeg + p.klen);
+
+  floatx16 acc[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[q][r] = 0.0f;
+
+  // This wavefront's chunks start at k0 + i * STRIDE; the first nf are full.
+  // Software pipeline: U chunks are in flight while the oldest is multiplied.
+  const int k0 = kbeg + kSkChunk * wave;
+  const int nf = kend - k0 >= kSkChunk ? (kend - k0 - kSkChunk) / STRIDE + 1 : 0;
+  skinny_chunk<Q, TB, VA, VB> ch[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (u < nf)
+      ch[u].template load<false>(p.A, p.lda, p.B, p.ldb, arow, bcol, k0 + u * STRIDE, s, kend);
+  int i = 0;
+  for (; i + U <= nf; i += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      ch[u].mma(acc);
+      if (i + u + U < nf)
+        ch[u].template load<false>(p.A, p.lda, p.B, p.ldb, arow, bcol,
+                                   k0 + (i + u + U) * STRIDE, s, kend);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (i + u < nf) ch[u].mma(acc);
+  const int kt = k0 + nf * STRIDE;  // a partial last chunk, if any
+  if (kt < kend) {
+    skinny_chunk<Q, TB, VA, VB> t;
+    t.template load<true>(p.A, p.lda, p.B, p.ldb, arow, bcol, kt, s, kend);
+    t.mma(acc);
+  }
+
+  // Add the wavefronts' accumulators: every wavefront parks its sets in LDS,
+  // then wavefront w finishes registers RPW w .. RPW w + RPW - 1 of every
+  // set; register r of lane (c, s) is row 8 (r / 4) + 4 s + r % 4, column
+  // n0 + Q c + q -- for Q = 4 one float4 of C per row.
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[wave][q * 16 + r][lane] = acc[q][r];
+  __syncthreads();
+  const bool split = gridDim.y > 1;
+  float *W = split ? p.ws + int64_t(blockIdx.y) * M * N : p.C;
+  const int64_t ldw = split ? N : p.ldc;
+  const int col = n0 + Q * c;
+  if (col >= N) return;
+  const bool vst = Q == 4 && (ldw & 3) == 0 && aligned16_dev(W);
+  constexpr int RPW = 16 / kSkWaves;
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int r = RPW * wave + i;
+    const int row = 8 * (r / 4) + 4 * s + r % 4;
+    if (row >= M) continue;
+    float v[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      v[q] = red[0][q * 16 + r][lane];
+#pragma unroll
+      for (int w = 1; w < kSkWaves; ++w) v[q] += red[w][q * 16 + r][lane];
+      if (!split) v[q] = apply_epi(v[q], row, col + q, p.ep);
+    }
+    float *dst = W + int64_t(row) * ldw + col;
+    if constexpr (Q == 4) {
+      if (vst) {
+        *reinterpret_cast<float4 *>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+        continue;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < Q; ++q) dst[q] = v[q];
   }
 }
 
@@ -965,40 +1168,71 @@ int launch_tiles(const gemm_args &a, int64_t batch, int splits, bool ta, bool tb
   return launch_tb<BM, BN, BK, WM, WN, MI, true, true>(a, batch, splits, vec, s);
 }
 
-// Sums the K-split partials ws[s][M][N] in split order and applies the
-// epilogue: C[m*ldc + n] = epi(sum_s ws[s][m][n]).  One element (or one
-// float4 when rows allow) per thread.
-template <bool VEC>
-__global__ __launch_bounds__(256) void splitk_reduce_k(const float *__restrict__ ws, int splits,
-                                                       int64_t M, int64_t N,
-                                                       float *__restrict__ C, int64_t ldc,
-                                                       epi_args ep) {
-  const int64_t per = VEC ? 4 : 1;
-  const int64_t total = M * N / per;
+// Adds the K-split partial planes ws[s][M][N] (s < splits) and applies the
+// epilogue: C[m*ldc + n] = epi(sum_s ws[s][m][n]).  A thread owns one output
+// group (4 floats when VEC: N % 4 == 0, else 1) and keeps 8 plane loads in
+// flight.  DEEP (many splits, few outputs): the four wavefronts of a
+// workgroup share 64 groups and take planes w, w + 4, ..., then add their
+// sums through LDS; otherwise each thread walks every plane of its group.
+constexpr int kSumWaves = 4;  // 256 threads
+
+template <bool VEC, bool DEEP>
+__global__ __launch_bounds__(256) void splitk_sum_k(const float *__restrict__ ws, int splits,
+                                                    int64_t M, int64_t N,
+                                                    float *__restrict__ C, int64_t ldc,
+                                                    epi_args ep) {
+  constexpr int P = VEC ? 4 : 1;
+  constexpr int G = 8;
+  typedef typename vecf<P>::t V;
   const int64_t plane = M * N;
-  for (int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x; t < total;
-       t += int64_t(gridDim.x) * 256) {
-    const int64_t e = t * per;
-    const int64_t m = e / N, n = e % N;
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int sp = 0; sp < splits; ++sp) {
-      if constexpr (VEC) {
-        float4 q = *reinterpret_cast<const float4 *>(ws + sp * plane + e);
-        v[0] += q.x;
-        v[1] += q.y;
-        v[2] += q.z;
-        v[3] += q.w;
-      } else {
-        v[0] += ws[sp * plane + e];
-      }
-    }
+  const int64_t groups = plane / P;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int64_t gi = DEEP ? int64_t(blockIdx.x) * kWave + lane
+                          : int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int ds = DEEP ? kSumWaves : 1;
+  float v[P];
 #pragma unroll
-    for (int j = 0; j < (VEC ? 4 : 1); ++j) v[j] = apply_epi(v[j], m, n + j, ep);
-    if constexpr (VEC)
-      *reinterpret_cast<float4 *>(C + m * ldc + n) = make_float4(v[0], v[1], v[2], v[3]);
-    else
-      C[m * ldc + n] = v[0];
+  for (int q = 0; q < P; ++q) v[q] = 0.0f;
+  if (gi < groups) {
+    const float *src = ws + gi * P;
+    int sp = DEEP ? wave : 0;
+    for (; sp + (G - 1) * ds < splits; sp += G * ds) {
+      V x[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        x[g] = *reinterpret_cast<const V *>(src + int64_t(sp + g * ds) * plane);
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int q = 0; q < P; ++q) v[q] += vecf<P>::get(x[g], q);
+    }
+    for (; sp < splits; sp += ds) {
+      const V x = *reinterpret_cast<const V *>(src + int64_t(sp) * plane);
+#pragma unroll
+      for (int q = 0; q < P; ++q) v[q] += vecf<P>::get(x, q);
+    }
   }
+  if constexpr (DEEP) {
+    __shared__ float red[kSumWaves - 1][P][kWave];
+    if (wave > 0)
+#pragma unroll
+      for (int q = 0; q < P; ++q) red[wave - 1][q][lane] = v[q];
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 0; w < kSumWaves - 1; ++w)
+#pragma unroll
+      for (int q = 0; q < P; ++q) v[q] += red[w][q][lane];
+  }
+  if (gi >= groups) return;
+  const int64_t e = gi * P, m = e / N, n = e % N;
+#pragma unroll
+  for (int q = 0; q < P; ++q) v[q] = apply_epi(v[q], m, n + q, ep);
+  float *dst = C + m * ldc + n;
+  if constexpr (VEC)
+    *reinterpret_cast<float4 *>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+  else
+    dst[0] = v[0];
 }
 
 // Tile configurations (BM x BN, waves WM x WN; BK = 16, 32 for 32x128).
@@ -1008,7 +1242,12 @@ enum tile_cfg {
   TILE_64x64 = 2,
   TILE_32x128 = 3,
   TILE_128x64 = 4,
-  TILE_256x256 = 5
+  TILE_256x256 = 5,
+  // M <= 32 (batch 1, A not transposed): sgemm_skinny_k with 32Q columns per
+  // workgroup; TILE_SKINNY (the automatic choice) is Q = 1.
+  TILE_SKINNY = 6,
+  TILE_SKINNY_Q2 = 7,
+  TILE_SKINNY_Q4 = 8
 };
 
 struct plan {
@@ -1029,18 +1268,24 @@ struct plan {
 // K, and the split term the partial tiles' HBM round trip plus the reduce
 // launch.  M <= 32 uses the 32x128 tile with enough K splits for
 // ~256 workgroups.
+// The 32x128 tile for M <= 32, K split for about 256 workgroups.
+plan small_m_tiles(int64_t M, int64_t N, int64_t K, int64_t batch) {
+  plan p{TILE_32x128, 1};
+  if (batch == 1) {
+    int64_t sp = cdiv(256, cdiv(M, 32) * cdiv(N, 128));
+    if (sp > K / 256) sp = K / 256;
+    if (sp > 64) sp = 64;
+    if (sp > 1) p.splits = static_cast<int>(sp);
+  }
+  return p;
+}
+
 plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch) {
   auto tiles = [&](int bm, int bn) { return cdiv(M, bm) * cdiv(N, bn) * batch; };
-  if (M <= 32) {
-    plan p{TILE_32x128, 1};
-    if (batch == 1) {
-      int64_t sp = cdiv(256, tiles(32, 128));
-      if (sp > K / 256) sp = K / 256;
-      if (sp > 64) sp = 64;
-      if (sp > 1) p.splits = static_cast<int>(sp);
-    }
-    return p;
-  }
+  // M <= 32: the small-M kernel (splits chosen at launch), or where it does
+  // not apply (batched, A transposed) the 32x128 tile.
+  if (M <= 32 && batch == 1) return plan{TILE_SKINNY, 0};
+  if (M <= 32) return small_m_tiles(M, N, K, batch);
   // Predicted time of each (tile, K split): every CU runs ceil(WG / 256)
   // workgroups, min(that, occupancy) of them at once; a SIMD holding a
   // single wavefront reaches kSingleWave of the rate it reaches with two or
@@ -1083,10 +1328,77 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch) {
   return best;
 }
 
+template <int Q, bool TB, bool VA, bool VB>
+void launch_skinny_k(const gemm_args &g, dim3 grid, hipStream_t s) {
+  sgemm_skinny_k<Q, TB, VA, VB><<<grid, kSkWaves * kWave, 0, s>>>(g);
+}
+
+template <int Q, bool TB>
+int launch_skinny_q(const gemm_args &a, int splits, bool va, bool vb, hipStream_t s) {
+  gemm_args g = a;
+  constexpr int64_t kStep = int64_t(kSkChunk) * kSkWaves;
+  g.klen = static_cast<int>(cdiv(cdiv(a.K, splits), kStep) * kStep);
+  if (g.klen < kStep) g.klen = static_cast<int>(kStep);
+  splits = static_cast<int>(a.K > 0 ? cdiv(a.K, g.klen) : 1);
+  dim3 grid(static_cast<unsigned>(cdiv(a.N, 32 * Q)), static_cast<unsigned>(splits));
+  if (!TB || !vb) {
+    if (va) launch_skinny_k<Q, TB, true, false>(g, grid, s);
+    else launch_skinny_k<Q, TB, false, false>(g, grid, s);
+  } else {
+    if (va) launch_skinny_k<Q, TB, true, true>(g, grid, s);
+    else launch_skinny_k<Q, TB, false, true>(g, grid, s);
+  }
+  SILGPU_LAUNCH_CHECK("sgemm_skinny_k");
+  return splits;
+}
+
+// K splits for the small-M kernel: about one workgroup per CU (measured best
+// on MI355X for M <= 32 at N, K in 768..4096), each K range at least 128
+// deep.
+int skinny_splits(int64_t M, int64_t N, int64_t K, int Q) {
+  (void)M;
+  int64_t sp = 256 / cdiv(N, 32 * Q);
+  if (sp > K / 128) sp = K / 128;
+  if (sp > 65535) sp = 65535;
+  return sp < 1 ? 1 : static_cast<int>(sp);
+}
+
+// Column-group width of the small-M kernel for `tile`: Q > 1 needs N % Q == 0
+// and, without trans_b, 16-byte-aligned B rows.
+int skinny_q(const gemm_args &a, int tile, bool tb) {
+  int Q = tile == TILE_SKINNY_Q2 ? 2 : tile == TILE_SKINNY_Q4 ? 4 : 1;
+  while (Q > 1 && (a.N % Q != 0 || (!tb && !(a.ldb % Q == 0 && aligned16(a.B))))) Q /= 2;
+  return Q;
+}
+
+// Launches the small-M kernel with column-group width Q; returns the number
+// of K splits launched.
+int launch_skinny(const gemm_args &a, int Q, int splits, bool tb, hipStream_t s) {
+  const bool va = a.lda % 4 == 0 && aligned16(a.A);
+  const bool bvec = a.ldb % 4 == 0 && aligned16(a.B);
+  if (Q == 4)
+    return tb ? launch_skinny_q<4, true>(a, splits, va, bvec, s)
+              : launch_skinny_q<4, false>(a, splits, va, bvec, s);
+  if (Q == 2)
+    return tb ? launch_skinny_q<2, true>(a, splits, va, bvec, s)
+              : launch_skinny_q<2, false>(a, splits, va, bvec, s);
+  return tb ? launch_skinny_q<1, true>(a, splits, va, bvec, s)
+            : launch_skinny_q<1, false>(a, splits, va, bvec, s);
+}
+
 int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, bool vec,
               context *c) {
   gemm_args a = a0;
+  const bool skinny = pl.tile >= TILE_SKINNY && a.M <= 32 && batch == 1 && !ta;
+  if (pl.tile >= TILE_SKINNY && !skinny)
+    pl = pl.splits >= 1 ? plan{TILE_32x128, pl.splits} : small_m_tiles(a.M, a.N, a.K, batch);
   int splits = pl.splits;
+  int q = 1;
+  if (skinny) {
+    q = skinny_q(a, pl.tile, tb);
+    if (splits < 1) splits = skinny_splits(a.M, a.N, a.K, q);
+  }
+  if (splits < 1) splits = 1;
   if (batch != 1 || a.K == 0) splits = 1;
   if (splits > 1) {
     size_t need = size_t(splits) * size_t(a.M) * size_t(a.N) * sizeof(float);
@@ -1095,36 +1407,46 @@ int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, boo
     a.ws = static_cast<float *>(c->workspace);
   }
   int launched;
-  switch (pl.tile) {
-    case TILE_64x64:
-      launched = launch_tiles<64, 64, 16, 2, 2, 16>(a, batch, splits, ta, tb, vec, c->stream);
-      break;
-    case TILE_32x128:
-      launched = launch_tiles<32, 128, 32, 1, 4, 16>(a, batch, splits, ta, tb, vec, c->stream);
-      break;
-    case TILE_128x64:
-      launched = launch_tiles<128, 64, 16, 2, 2, 16>(a, batch, splits, ta, tb, vec, c->stream);
-      break;
-    case TILE_256x256:
-      launched = launch_tiles<256, 256, 16, 2, 4, 16>(a, batch, splits, ta, tb, vec, c->stream);
-      break;
-    default:
-      launched = launch_tiles<128, 128, 16, 2, 2, 16>(a, batch, splits, ta, tb, vec, c->stream);
-      break;
+  if (skinny) {
+    launched = launch_skinny(a, q, splits, tb, c->stream);
+  } else {
+    switch (pl.tile) {
+      case TILE_64x64:
+        launched = launch_tiles<64, 64, 16, 2, 2, 16>(a, batch, splits, ta, tb, vec, c->stream);
+        break;
+      case TILE_32x128:
+        launched = launch_tiles<32, 128, 32, 1, 4, 16>(a, batch, splits, ta, tb, vec, c->stream);
+        break;
+      case TILE_128x64:
+        launched = launch_tiles<128, 64, 16, 2, 2, 16>(a, batch, splits, ta, tb, vec, c->stream);
+        break;
+      case TILE_256x256:
+        launched = launch_tiles<256, 256, 16, 2, 4, 16>(a, batch, splits, ta, tb, vec, c->stream);
+        break;
+      default:
+        launched = launch_tiles<128, 128, 16, 2, 2, 16>(a, batch, splits, ta, tb, vec, c->stream);
+        break;
+    }
   }
   if (launched < 0) return launched;
   if (launched > 1) {
     const bool v4 = a.N % 4 == 0 && a.ldc % 4 == 0 && aligned16(a.C);
-    const int64_t work = a.M * int64_t(a.N) / (v4 ? 4 : 1);
-    int64_t g = cdiv(work, 256);
-    if (g > 65536) g = 65536;
-    if (v4)
-      splitk_reduce_k<true><<<static_cast<unsigned>(g), 256, 0, c->stream>>>(
-          a.ws, launched, a.M, a.N, a.C, a.ldc, a.ep);
+    const int64_t groups = a.M * int64_t(a.N) / (v4 ? 4 : 1);
+    const bool deep = launched >= 8 && groups < 65536;
+    const unsigned g = static_cast<unsigned>(cdiv(groups, deep ? kWave : 256));
+    if (v4 && deep)
+      splitk_sum_k<true, true><<<g, 256, 0, c->stream>>>(a.ws, launched, a.M, a.N, a.C, a.ldc,
+                                                         a.ep);
+    else if (v4)
+      splitk_sum_k<true, false><<<g, 256, 0, c->stream>>>(a.ws, launched, a.M, a.N, a.C,
+                                                          a.ldc, a.ep);
+    else if (deep)
+      splitk_sum_k<false, true><<<g, 256, 0, c->stream>>>(a.ws, launched, a.M, a.N, a.C,
+                                                          a.ldc, a.ep);
     else
-      splitk_reduce_k<false><<<static_cast<unsigned>(g), 256, 0, c->stream>>>(
-          a.ws, launched, a.M, a.N, a.C, a.ldc, a.ep);
-    SILGPU_LAUNCH_CHECK("splitk_reduce_k");
+      splitk_sum_k<false, false><<<g, 256, 0, c->stream>>>(a.ws, launched, a.M, a.N, a.C,
+                                                           a.ldc, a.ep);
+    SILGPU_LAUNCH_CHECK("splitk_sum_k");
   }
   return SILGPU_OK;
 }
@@ -1343,7 +1665,7 @@ int silgpu_sgemm_tuned(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K
                        int64_t ldb, int64_t stride_b, float *d_C, int64_t ldc, int64_t stride_c,
                        int64_t batch, const float *d_bias, int64_t bias_len, int epilogue,
                        int tile, int splits) {
-  SILGPU_REQUIRE(tile >= TILE_128x128 && tile <= TILE_256x256,
+  SILGPU_REQUIRE(tile >= TILE_128x128 && tile <= TILE_SKINNY_Q4,
                  "silgpu_sgemm_tuned: unknown tile configuration %d", tile);
   SILGPU_REQUIRE(splits >= 1 && splits <= 256, "silgpu_sgemm_tuned: splits %d not in [1, 256]",
                  splits);

@@ -74,6 +74,9 @@ context *ctx();
   if (!c) return SILGPU_ERR_NODEVICE
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+__device__ __forceinline__ bool aligned16_dev(const void *p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

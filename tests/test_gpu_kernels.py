@@ -560,7 +560,7 @@ def test_small_batch_config(native, oracle):
     assert ok, (nw, el)
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("splits", [1, 3, 8])
 @pytest.mark.parametrize("M,N,K,ta,tb,epi", [(33, 70, 200, 0, 0, 0), (128, 256, 512, 0, 0, 2),
                                              (100, 130, 1000, 1, 0, 1), (64, 96, 777, 0, 1, 4),
@@ -586,6 +586,52 @@ def test_sgemm_tuned_configs(native, oracle, tile, splits, M, N, K, ta, tb, epi)
     if epi in (3, 4):
         C64 = np.maximum(C64, 0)
     ok, nw, el = gemm_tolerance_ok(Cg, C64, Cabs, K)
+    assert ok, (nw, el)
+
+
+SKINNY_CASES = [
+    # M, N, K, tb, lda_pad, ldb_pad, ldc_pad, epi
+    (32, 768, 4096, 0, 0, 0, 0, 0), (32, 768, 4096, 1, 0, 0, 0, 2), (2, 4096, 768, 0, 0, 0, 0, 1),
+    (31, 130, 100, 0, 1, 0, 3, 4), (5, 7, 15, 0, 0, 0, 0, 0), (16, 64, 1, 0, 0, 0, 0, 3),
+    (17, 96, 333, 1, 0, 1, 0, 1), (32, 100, 200, 1, 2, 2, 1, 2), (3, 260, 1000, 0, 0, 2, 4, 0),
+    (32, 4096, 64, 0, 0, 0, 0, 1), (8, 36, 4100, 1, 3, 0, 0, 0),
+]
+
+
+@pytest.mark.parametrize("tile,splits", [(6, 0), (6, 1), (6, 5), (6, 64), (7, 3), (8, 2),
+                                         (8, 17)])
+@pytest.mark.parametrize("M,N,K,tb,lpa,lpb,lpc,epi", SKINNY_CASES)
+def test_sgemm_small_m(native, oracle, tile, splits, M, N, K, tb, lpa, lpb, lpc, epi):
+    """The small-M kernel (M <= 32) through silgpu_sgemm_tuned with forced
+    column-group widths and K splits (0 = the library's choice): padded lda /
+    ldb (unaligned rows take the scalar loads), ldc > N, both B layouts, every
+    epilogue, K not a multiple of the 16-deep chunk."""
+    announce(f"sgemm small-M tile={tile} splits={splits} {M}x{N}x{K} tb={tb} "
+             f"pads=({lpa},{lpb},{lpc}) epi={epi}")
+    g = rng(4100 + M + 3 * N + K + tb)
+    lda, ldb, ldc = K + lpa, (K if tb else N) + lpb, N + lpc
+    A = g.uniform(-1, 1, (M, lda)).astype(np.float32)
+    B = g.uniform(-1, 1, ((N if tb else K), ldb)).astype(np.float32)
+    bias_len = N if epi in (1, 2, 4) else 0
+    bias = g.normal(0, 1, max(bias_len, 1)).astype(np.float32)
+    dA, dB, dC = up(native, A), up(native, B), empty(native, M * ldc)
+    dbias = up(native, bias) if bias_len else None
+    if splits == 0:
+        native.sgemm(0, tb, M, N, K, dA, lda, 0, dB, ldb, 0, dC, ldc, 0, 1, dbias, bias_len,
+                     epi)
+    else:
+        native.sgemm_tuned(0, tb, M, N, K, dA, lda, 0, dB, ldb, 0, dC, ldc, 0, 1, dbias,
+                           bias_len, epi, tile=tile, splits=splits)
+    Cg = down(native, dC, (M, ldc))[:, :N]
+    Bv = B[:, :K] if tb else B[:, :N]
+    C64, Cabs = oracle.sgemm_f64(A[:, :K], Bv, tb=bool(tb), with_abs=True)
+    if bias_len:
+        C64, Cabs = C64 + bias, Cabs + np.abs(bias)
+    if epi == 2:
+        C64, Cabs = 1 / (1 + np.exp(-C64)), Cabs / 4 + 1e-7
+    if epi in (3, 4):
+        C64 = np.maximum(C64, 0)
+    ok, nw, el = gemm_tolerance_ok(Cg, C64, Cabs, max(K, 1))
     assert ok, (nw, el)
 
 
