@@ -263,6 +263,8 @@ GRAPH_BENCH = ROOT / "silarray_amd" / "bench" / "bench_graph"
 # The reference's published sil-gpu times for its single-head transformer
 # block on an Apple M1 Pro (bench/README.md:196-199), keyed by (seq, d_model).
 REF_TRANSFORMER_MS = {(256, 512): 1.53, (256, 768): 2.30, (256, 1024): 2.93, (512, 1024): 5.32}
+# The reference's training step on an M1 Pro (bench/README.md:187-188), by batch.
+REF_TRAIN_MS = {64: 1.11, 128: 1.51}
 
 
 def bench_graphs(timeout: float = 300.0) -> list[dict]:
@@ -275,7 +277,8 @@ def bench_graphs(timeout: float = 300.0) -> list[dict]:
     if not GRAPH_BENCH.exists():
         raise RuntimeError(f"{GRAPH_BENCH} is not built (run __graft_entry__.build())")
     out = []
-    for argv in (["encoder", "10"], ["transformer"], ["mlp"], ["chain", str(64 << 20), "20"]):
+    for argv in (["encoder", "10"], ["transformer"], ["mlp"], ["train"],
+                 ["chain", str(64 << 20), "20"]):
         log(f"bench_graph {' '.join(argv)}")
         proc = subprocess.run([str(GRAPH_BENCH), *argv], capture_output=True, text=True,
                               timeout=timeout)
@@ -407,6 +410,8 @@ def main():
                 key = f"transformer_block_seq{r['seq']}_d{r['d_model']}"
             elif w == "mlp_linear_sigmoid":
                 key = f"mlp_linear_sigmoid_batch{r['batch']}"
+            elif w == "train_step":
+                key = f"train_step_768x2048_batch{r['batch']}"
             else:
                 key = f"{w}_64M_api"
             if "gemm_tflops" in r:
@@ -418,6 +423,8 @@ def main():
             ref = REF_TRANSFORMER_MS.get((r.get("seq"), r.get("d_model")))
             if w == "transformer_block" and ref is not None:
                 e["reference_m1pro_ms"] = ref
+            if w == "train_step" and r["batch"] in REF_TRAIN_MS:
+                e["reference_m1pro_ms"] = REF_TRAIN_MS[r["batch"]]
             secondary[key] = e
 
     cpu = None

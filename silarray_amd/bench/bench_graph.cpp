@@ -10,6 +10,13 @@
 //                                             the parity test
 //   bench_graph transformer [seq d ff] [reps] the reference's single-head block
 //   bench_graph mlp [batch] [reps]            the reference's linear_sigmoid MLP
+//   bench_graph train [batch] [reps]          the reference's training step:
+//                                             768 -> 2048 -> 768 sigmoid MLP,
+//                                             forward, MSE gradient, backward,
+//                                             SGD update, one sil::eval
+//   bench_graph train-dump B D H DIR          one training step on seeded
+//                                             inputs, written to DIR (raw
+//                                             float32) for the parity test
 //
 // Each timed iteration is sil::eval + wait, the reference's convention
 // (bench/bench_common.h:42-68); the median of `reps` iterations is reported
@@ -181,6 +188,53 @@ double mlp_ms(size_t batch, int reps) {
   });
 }
 
+// The reference's training benchmark (bench/composite/bench_train.cpp:20-58):
+// a D -> H -> D MLP with sigmoid activations, MSE loss gradient, manual
+// backward through sigmoid_backward, transposed products and sum(0), and an
+// SGD update of all four parameters evaluated as one graph.
+struct train_step {
+  array<float> W1, b1, W2, b2, x, Y;
+  float lr = 0.01f;
+  size_t B, D, H;
+
+  train_step(size_t batch, size_t d, size_t h, uint64_t seed) : B(batch), D(d), H(h) {
+    rng g(seed);
+    W1 = filled({D, H}, g, 0, true) * (1.0f / std::sqrt(float(D)));
+    b1 = filled({H}, g, 0.1f);
+    W2 = filled({H, D}, g, 0, true) * (1.0f / std::sqrt(float(H)));
+    b2 = filled({D}, g, 0.1f);
+    x = filled({B, D}, g, 0, true);
+    Y = filled({B, D}, g, 0, true);
+    eval(W1, W2);
+  }
+
+  // One step; leaves the updated parameters unevaluated in W1 .. b2.
+  void step() {
+    auto two = array<float>(2.0f);
+    auto inv_n = array<float>(1.0f / static_cast<float>(B * D));
+    auto neg_lr = array<float>(-lr);
+    auto n1 = x.linear(W1, b1);
+    auto o1 = n1.sigmoid();
+    auto n2 = o1.linear(W2, b2);
+    auto o2 = n2.sigmoid();
+    auto dout = (o2 - Y) * two * inv_n;
+    dout = n2.sigmoid_backward(dout);
+    auto dW2 = o1.transpose().dot(dout);
+    auto db2 = dout.sum(0);
+    auto dout1 = dout.dot(W2.transpose());
+    dout1 = n1.sigmoid_backward(dout1);
+    auto dW1 = x.transpose().dot(dout1);
+    auto db1 = dout1.sum(0);
+    W1 = W1 + dW1 * neg_lr;
+    b1 = b1 + db1 * neg_lr;
+    W2 = W2 + dW2 * neg_lr;
+    b2 = b2 + db2 * neg_lr;
+  }
+
+  // Six products of 2*B*D*H flops each (two forward, four backward).
+  double gemm_flops() const { return 12.0 * double(B) * double(D) * double(H); }
+};
+
 void write_raw(const std::string &path, const array<float> &a) {
   std::ofstream f(path, std::ios::binary);
   const float *p = a.buffer_data();
@@ -288,7 +342,52 @@ int main(int argc, char **argv) {
       }
       return 0;
     }
-    std::fprintf(stderr, "usage: bench_graph chain|encoder|encoder-dump|transformer|mlp ...\n");
+    if (mode == "train") {
+      // argv: [batch [reps]]; default: the reference's batches 64 and 128
+      // (bench/composite/bench_train.cpp:60-64).
+      std::vector<size_t> batches = {64, 128};
+      if (argc >= 3) batches = {std::strtoull(argv[2], nullptr, 10)};
+      const int reps = argc > 3 ? std::atoi(argv[3]) : 20;
+      if (reps < 1 || batches[0] == 0) throw std::runtime_error("batch and reps must be >= 1");
+      for (size_t b : batches) {
+        train_step t(b, 768, 2048, 2027);
+        synchronize();
+        const double ms = median_ms(reps, [&] {
+          t.step();
+          eval(t.W1, t.b1, t.W2, t.b2);
+          synchronize();
+        });
+        std::printf("{\"workload\": \"train_step\", \"batch\": %zu, \"D\": 768, \"H\": 2048, "
+                    "\"ms\": %.4f, \"gemm_tflops\": %.2f}\n",
+                    b, ms, t.gemm_flops() / (ms * 1e-3) / 1e12);
+      }
+      return 0;
+    }
+    if (mode == "train-dump") {
+      if (argc < 6) throw std::runtime_error("train-dump needs B D H DIR");
+      const size_t B = std::strtoull(argv[2], nullptr, 10), D = std::strtoull(argv[3], nullptr, 10),
+                   H = std::strtoull(argv[4], nullptr, 10);
+      if (B == 0 || D == 0 || H == 0) throw std::runtime_error("B, D and H must be >= 1");
+      const std::string dir = argv[5];
+      train_step t(B, D, H, 2027);
+      write_raw(dir + "/x.bin", t.x);
+      write_raw(dir + "/Y.bin", t.Y);
+      write_raw(dir + "/W1.bin", t.W1);
+      write_raw(dir + "/b1.bin", t.b1);
+      write_raw(dir + "/W2.bin", t.W2);
+      write_raw(dir + "/b2.bin", t.b2);
+      t.step();
+      eval(t.W1, t.b1, t.W2, t.b2);
+      write_raw(dir + "/W1_new.bin", t.W1);
+      write_raw(dir + "/b1_new.bin", t.b1);
+      write_raw(dir + "/W2_new.bin", t.W2);
+      write_raw(dir + "/b2_new.bin", t.b2);
+      std::printf("{\"dumped\": \"%s\"}\n", dir.c_str());
+      return 0;
+    }
+    std::fprintf(stderr,
+                 "usage: bench_graph chain|encoder|encoder-dump|transformer|mlp|train|train-dump "
+                 "...\n");
     return 2;
   } catch (std::exception &ex) {
     std::fprintf(stderr, "bench_graph: %s\n", ex.what());

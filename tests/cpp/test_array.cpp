@@ -611,4 +611,43 @@ TEST_CASE("host writes after device use are uploaded") {
   CHECK(s1 == 8192.0f && s2 == 8194.0f);
 }
 
+// The reference's two-layer network on XOR (test/test_2lnn.cpp:5-140), with a
+// fixed initialisation in place of sil::random.  A float32 numpy run of the
+// same 2000 epochs from this start reaches outputs {0.027, 0.971, 0.971,
+// 0.034} and loss 8.9e-4.
+TEST_CASE("2 layer NN learns xor (forward, sigmoid_backward, transposed dot, -=)") {
+  auto W1 = array<float>{{0.9f, -0.8f, 0.4f}, {0.7f, -0.9f, -0.5f}};
+  auto b1 = array<float>{-0.3f, 0.4f, 0.2f};
+  auto W2 = array<float>({3, 1}, std::vector<float>{0.8f, -0.7f, 0.5f});
+  auto b2 = array<float>{0.2f};
+  const auto X = array<float>{{0, 0}, {0, 1}, {1, 0}, {1, 1}};
+  const auto Y = array<float>{{0}, {1}, {1}, {0}};
+  const float lr = 0.5f;
+  float loss = 0.0f;
+  array<float> out;
+  for (int epoch = 0; epoch < 2000; epoch++) {
+    auto net1 = X.linear(W1, b1);
+    auto out1 = net1.sigmoid();
+    auto net2 = out1.linear(W2, b2);
+    out = net2.sigmoid();
+    loss = out.mean_square_error(Y);
+    auto dout = 1.0f * (2 * (out - Y));
+    dout = net2.sigmoid_backward(dout);
+    auto dout1 = dout.dot(W2.transpose());
+    auto dW2 = out1.transpose().dot(dout);
+    auto db2 = dout.sum(0);
+    dout = net1.sigmoid_backward(dout1);
+    auto dW1 = X.transpose().dot(dout);
+    auto db1 = dout.sum(0);
+    W1 -= dW1 * lr;
+    b1 -= db1 * lr;
+    W2 -= dW2 * lr;
+    b2 -= db2 * lr;
+  }
+  CHECK(loss < 2e-3f);
+  const float expect[] = {0.027f, 0.971f, 0.971f, 0.034f};
+  for (size_t i = 0; i < 4; i++) CHECK(is_close((out[i, 0]), expect[i], 5e-3f));
+  CHECK(array_equal(where<float>(out > 0.5f, 1, 0), {{0}, {1}, {1}, {0}}));
+}
+
 int main(int argc, char **argv) { return harness::run(argc, argv); }

@@ -94,3 +94,71 @@ def test_chain_and_encoder_report_json():
                          capture_output=True, text=True, timeout=120, check=True).stdout
     rec = json.loads(out.strip().splitlines()[-1])
     assert rec["workload"] == "encoder_block" and rec["ms"] > 0
+
+
+def _sigmoid(x):
+    return 1.0 / (1.0 + np.exp(-x))
+
+
+def train_step_f64(p, B, D, lr=0.01):
+    """Float64 restatement of one step of the reference's training benchmark
+    (bench/composite/bench_train.cpp:39-58): D -> H -> D sigmoid MLP, MSE
+    gradient (o2 - Y) * 2 / (B D), sigmoid_backward = dout * s * (1 - s)
+    (include/gpu_kernels.metal:1469-1477), SGD with learning rate lr."""
+    x, Y = p["x"].reshape(B, D), p["Y"].reshape(B, D)
+    W1, W2 = p["W1"].reshape(D, -1), p["W2"].reshape(-1, D)
+    b1, b2 = p["b1"], p["b2"]
+    n1 = x @ W1 + b1
+    o1 = _sigmoid(n1)
+    n2 = o1 @ W2 + b2
+    o2 = _sigmoid(n2)
+    dout = (o2 - Y) * 2.0 * (1.0 / (B * D))
+    s2 = _sigmoid(n2)
+    dout = dout * s2 * (1.0 - s2)
+    dW2, db2 = o1.T @ dout, dout.sum(axis=0)
+    dout1 = dout @ W2.T
+    s1 = _sigmoid(n1)
+    dout1 = dout1 * s1 * (1.0 - s1)
+    dW1, db1 = x.T @ dout1, dout1.sum(axis=0)
+    return {"W1": W1 - lr * dW1, "b1": b1 - lr * db1, "W2": W2 - lr * dW2, "b2": b2 - lr * db2,
+            "dW1": dW1, "db1": db1, "dW2": dW2, "db2": db2}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dims", [(64, 768, 2048), (5, 33, 70), (32, 4, 3)])
+def test_train_step_matches_f64(tmp_path, dims):
+    """One training step through sil::eval (linear, sigmoid, sigmoid_backward,
+    transposed products, sum(0), SGD update) against float64.  The update is
+    compared as the implied gradient (W - W_new) / lr, relative to the f64
+    gradient's scale, since lr * grad is far below W's own rounding."""
+    B, D, H = dims
+    print(f"train-dump {dims}", flush=True)
+    proc = subprocess.run([str(_bench()), "train-dump", str(B), str(D), str(H), str(tmp_path)],
+                          capture_output=True, text=True, timeout=120)
+    assert proc.returncode == 0, proc.stderr
+    p = {n: np.fromfile(tmp_path / f"{n}.bin", dtype=np.float32).astype(np.float64)
+         for n in ("x", "Y", "W1", "b1", "W2", "b2")}
+    ref = train_step_f64(p, B, D)
+    lr = 0.01
+    for name in ("W1", "b1", "W2", "b2"):
+        new = np.fromfile(tmp_path / f"{name}_new.bin", dtype=np.float32).astype(np.float64)
+        ref_new = ref[name].reshape(-1)
+        # the parameter itself: fp32 rounding of W - lr * grad
+        assert np.all(np.abs(new - ref_new) <= 2 * np.finfo(np.float32).eps * np.abs(ref_new)
+                      + 1e-4 * np.abs(ref["d" + name]).max() * lr + 1e-30), name
+        # the step: (W - W_new) / lr against the f64 gradient; the fp32
+        # subtraction W + (-lr * g) loses log2(|W| / |lr g|) bits of the step
+        g = (p[name] - new) / lr
+        gref = ref["d" + name].reshape(-1)
+        ulp_w = np.finfo(np.float32).eps * np.abs(p[name]).max()
+        tol = 1e-4 * np.abs(gref).max() + 2 * ulp_w / lr
+        assert np.abs(g - gref).max() <= tol, (name, np.abs(g - gref).max(), tol)
+
+
+@pytest.mark.gpu
+def test_train_reports_json():
+    print("bench_graph train (small)", flush=True)
+    out = subprocess.run([str(_bench()), "train", "16", "3"], capture_output=True, text=True,
+                         timeout=120, check=True).stdout
+    rec = json.loads(out.strip().splitlines()[-1])
+    assert rec["workload"] == "train_step" and rec["batch"] == 16 and rec["ms"] > 0
