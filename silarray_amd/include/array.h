@@ -121,6 +121,10 @@ struct node {
   bool use_scale = false;
   float scale = 1.0f, scale_offset = 0.0f;
   std::shared_ptr<node> residual;
+  // batched_dot: strides of the output layout when the lowering has the
+  // product write straight into a consumer's reordered layout (empty: the
+  // contiguous layout of `shape`).
+  strides_type out_strides;
 
   static std::shared_ptr<node> leaf(const storage &s, const shape_type &sh, const strides_type &st) {
     auto n = std::make_shared<node>();
@@ -1756,9 +1760,12 @@ inline void eval_batched(node *n) {
   // outer one; any axes left before outer_begin are looped over.  A
   // [batch, heads, seq, dim] view split out of one [batch*seq, 3*heads*dim]
   // array is one launch: heads are the inner group, batches the outer.
+  // C's strides: contiguous, or the reordered layout the lowering chose.
+  const strides_type cs = n->out_strides.empty() ? contiguous_strides(n->shape) : n->out_strides;
   auto uniform = [&](size_t d) {
     return l->strides[d] == l->strides[d + 1] * l->shape[d + 1] &&
-           r->strides[d] == r->strides[d + 1] * r->shape[d + 1];
+           r->strides[d] == r->strides[d + 1] * r->shape[d + 1] &&
+           cs[d] == cs[d + 1] * n->shape[d + 1];
   };
   size_t inner = L, outer_begin = L;
   size_t binner = 1, bouter = 1;
@@ -1785,15 +1792,15 @@ inline void eval_batched(node *n) {
   d.K = int64_t(K);
   d.lda = int64_t(lda);
   d.ldb = int64_t(ldb);
-  d.ldc = int64_t(N);
+  d.ldc = int64_t(cs[nd - 2]);
   d.batch_outer = int64_t(bouter);
   d.batch_inner = int64_t(binner);
   d.stride_a_inner = L > 0 ? int64_t(l->strides[L - 1]) : 0;
   d.stride_b_inner = L > 0 ? int64_t(r->strides[L - 1]) : 0;
-  d.stride_c_inner = int64_t(M * N);
+  d.stride_c_inner = L > 0 ? int64_t(cs[L - 1]) : 0;
   d.stride_a_outer = inner > 0 ? int64_t(l->strides[inner - 1]) : 0;
   d.stride_b_outer = inner > 0 ? int64_t(r->strides[inner - 1]) : 0;
-  d.stride_c_outer = int64_t(binner * M * N);
+  d.stride_c_outer = inner > 0 ? int64_t(cs[inner - 1]) : 0;
   d.epilogue = SILGPU_EPI_NONE;
   d.use_scale = n->use_scale;
   d.scale = n->scale;
@@ -1801,23 +1808,24 @@ inline void eval_batched(node *n) {
   auto out = new_output(n->shape);
   size_t loops = 1;
   for (size_t a = 0; a < outer_begin; a++) loops *= n->shape[a];
-  const size_t per_loop = bouter * binner * M * N;
   for (size_t o = 0; o < loops; o++) {
-    size_t rem = o, offa = 0, offb = 0;
+    size_t rem = o, offa = 0, offb = 0, offc = 0;
     for (size_t a = outer_begin; a-- > 0;) {
       const size_t idx = rem % n->shape[a];
       rem /= n->shape[a];
       offa += idx * l->strides[a];
       offb += idx * r->strides[a];
+      offc += idx * cs[a];
     }
     storage A = l->data, B = r->data, C = out;
     A.off += offa;
     B.off += offb;
-    C.off += o * per_loop;
-    C.len = per_loop;
+    C.off += offc;
+    C.len = out.len - offc;
     gpu::gemm(d, A, B, C);
   }
   finish(n, std::move(out));
+  n->strides = cs;
 }
 
 inline void eval_node_nonfused(node *n) {
@@ -2019,12 +2027,48 @@ inline void evaluate(const std::vector<node *> &roots) {
       break;
     }
   }
+  //  copy(view(batched_dot)) where the view only reorders the product's
+  //  axes and keeps its last one (attention's head merge,
+  //  ctx.permute({0, 2, 1, 3}) before a reshape): the product writes its
+  //  tiles straight into the copy's contiguous layout through ldc and batch
+  //  strides, and the copy and the view alias its output.
+  std::unordered_map<node *, node *> relayout;  // copy or view -> product
+  for (node *n : order) {
+    if (n->operation != op::copy || alias.count(n)) continue;
+    node *v = n->inputs[0].get();
+    if (v->operation != op::view || v->view_off != 0 || !single_use(v, n)) continue;
+    node *p = v->inputs[0].get();
+    if (p->operation != op::batched_dot || p->residual || !p->out_strides.empty()) continue;
+    if (!single_use(p, v) || v->shape.size() != p->shape.size()) continue;
+    const size_t nd = p->shape.size();
+    const auto ps = contiguous_strides(p->shape), ns = contiguous_strides(v->shape);
+    // perm[a] = the product axis that view axis a reads.
+    std::vector<size_t> perm(nd, nd);
+    bool ok = shape_count(p->shape) > 0;
+    std::vector<bool> used(nd, false);
+    for (size_t a = 0; ok && a < nd; a++) {
+      for (size_t b = 0; b < nd; b++)
+        if (!used[b] && ps[b] == v->strides[a] && p->shape[b] == v->shape[a] &&
+            (p->shape[b] > 1 || v->strides[a] == ps[b])) {
+          perm[a] = b;
+          used[b] = true;
+          break;
+        }
+      ok = perm[a] < nd;
+    }
+    if (!ok || perm[nd - 1] != nd - 1) continue;  // the product's rows stay unit-stride
+    strides_type os(nd);
+    for (size_t a = 0; a < nd; a++) os[perm[a]] = ns[a];
+    p->out_strides = os;
+    relayout[v] = p;
+    relayout[n] = p;
+  }
   // A node is computed inside its consumer's program when it is elementwise,
   // has exactly one consumer, that consumer is elementwise, it is not a root
   // and no array outside the graph holds it.
   auto fusable = [&](node *c) {
     if (c->evaluated || root_set.count(c) || !is_elementwise(c->operation)) return false;
-    if (materialize.count(c) || alias.count(c)) return false;
+    if (materialize.count(c) || alias.count(c) || relayout.count(c)) return false;
     auto it = consumers.find(c);
     if (it == consumers.end() || it->second != 1) return false;
     if (!is_elementwise(parent[c]->operation)) return false;
@@ -2041,6 +2085,15 @@ inline void evaluate(const std::vector<node *> &roots) {
       if (!c->evaluated) throw std::runtime_error("array: fused product not evaluated.");
       n->data = c->data;
       n->strides = c->strides;
+      n->evaluated = true;
+      continue;
+    }
+    if (auto it = relayout.find(n); it != relayout.end()) {
+      // The product's output is this node's contiguous layout.
+      node *c = it->second;
+      if (!c->evaluated) throw std::runtime_error("array: relaid product not evaluated.");
+      n->data = c->data;
+      n->strides = contiguous_strides(n->shape);
       n->evaluated = true;
       continue;
     }

@@ -534,6 +534,34 @@ TEST_CASE("lazy views feed strided batched products") {
   CHECK(ok);
 }
 
+TEST_CASE("head merge: the product writes the permuted layout, bit-identical") {
+  // ctx.permute({0, 2, 1, 3}).view(...) is lowered into the batched
+  // product's output strides (no copy kernel); the result must equal the
+  // copy of an evaluated ctx bit for bit, including edge tiles.
+  const size_t B = 2, S = 70, H = 3, dh = 24, D = H * dh;
+  auto qkv = random({B * S, 3 * D});
+  auto heads = qkv.view({B, S, 3, H, dh}).permute({2, 0, 3, 1, 4});
+  auto q = heads.select(0, 0), k = heads.select(0, 1), v = heads.select(0, 2);
+  auto build_ctx = [&] { return (q.batched_dot(k.permute({0, 1, 3, 2})) * 0.125f).batched_dot(v); };
+  auto fused = build_ctx().permute({0, 2, 1, 3}).view({B * S, D});
+  auto fused2 = build_ctx().permute({0, 2, 1, 3}).view({B * S, D}) * 2.0f;  // into a program
+  eval(fused, fused2);
+  auto ctx = build_ctx();
+  eval(ctx);  // evaluated first: the permute is copied afterwards
+  auto plain = ctx.permute({0, 2, 1, 3}).view({B * S, D});
+  eval(plain);
+  CHECK(fused.shape() == (shape_type{B * S, D}) && plain.shape() == fused.shape());
+  const float *a = std::as_const(fused).buffer_data(), *b = std::as_const(plain).buffer_data();
+  const float *c = std::as_const(fused2).buffer_data();
+  bool same = true, twice = true;
+  for (size_t i = 0; i < B * S * D; i++) {
+    same = same && std::memcmp(&a[i], &b[i], sizeof(float)) == 0;
+    twice = twice && c[i] == b[i] * 2.0f;
+  }
+  CHECK(same);
+  CHECK(twice);
+}
+
 HOST_CASE("view, permute and select on evaluated arrays") {
   auto m = array<int>({2, 3, 4}, iota_n(24));
   auto p = m.permute({2, 0, 1});
