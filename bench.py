@@ -357,13 +357,14 @@ def main():
         log(f"small_batch {r}")
         secondary["sgemm_32x768x4096"] = {
             "value": round(r["gbs"], 1), "unit": "GB/s", "tflops": round(r["tflops"], 2),
-            "us": round(r["us"], 2), "roofline": roofline("hbm", r["gbs"])}
+            "us": round(r["us"], 2),
+            "roofline": roofline("hbm", r["gbs"], load_traffic("sgemm_32x768x4096"))}
     if want("linear_sigmoid"):
         r = bench_linear_sigmoid(nat, g)
         log(f"linear_sigmoid {r}")
         secondary["linear_sigmoid_256x4096x4096"] = {
             "value": round(r["tflops"], 2), "unit": "TFLOP/s", "us": round(r["us"], 1),
-            "roofline": roofline("mfma", r["tflops"])}
+            "roofline": roofline("mfma", r["tflops"], load_traffic("linear_sigmoid_256x4096x4096"))}
     if want("rowops"):
         r = bench_rowops(nat, g)
         log(f"rowops {r}")
