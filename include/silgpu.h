@@ -305,6 +305,36 @@ typedef struct silgpu_gemm_desc {
 
 int silgpu_gemm(const silgpu_gemm_desc *desc);
 
+/* Fused attention: for every batch index b = (o, i) (o < batch_outer,
+ * i < batch_inner) and query row r < Sq,
+ *   O[b][r][:] = sum_j softmax_j(scale * Q[b][r] . K[b][j]) * V[b][j][:]
+ * over keys j < Sk, head dim D (16, 32, 64 or 128), every operand row-major
+ * with unit stride along D:  X[b][row][d] = X + o*stride_x_outer +
+ * i*stride_x_inner + row*ldx + d (16-byte aligned rows are read as float4,
+ * others element by element).  The scores are rounded as the product's
+ * fp32 result times `scale` (fmaf(acc, scale, 0)), the softmax subtracts the
+ * row maximum, and rows are normalised once at the end (online softmax), so
+ * results match the unfused graph within fp32 rounding, not bit for bit.
+ * No reference counterpart as one call: sil::eval lowers the reference
+ * graph dot/batched_dot -> scalar scale -> softmax -> dot/batched_dot
+ * (include/array.h:1360-1403, 1677-1709) onto it when the score matrix is
+ * used by nothing else, so the [Sq, Sk] scores never reach HBM. */
+typedef struct silgpu_attn_desc {
+  int64_t Sq, Sk, D;
+  int64_t batch_outer, batch_inner;
+  float scale;
+  const float *Q;
+  int64_t ldq, stride_q_outer, stride_q_inner;
+  const float *K;
+  int64_t ldk, stride_k_outer, stride_k_inner;
+  const float *V;
+  int64_t ldv, stride_v_outer, stride_v_inner;
+  float *O;
+  int64_t ldo, stride_o_outer, stride_o_inner;
+} silgpu_attn_desc;
+
+int silgpu_attention_f32(const silgpu_attn_desc *desc);
+
 /* y[1 x N] = x[1 x K] * B[K x N] (B row-major, ldb >= N).  Replaces gpu::sgemv
  * (include/gpu.h:549-574).  silgpu_sgemm routes M == 1 here as well. */
 int silgpu_sgemv(const float *d_x, const float *d_B, int64_t ldb, float *d_y, int64_t N,

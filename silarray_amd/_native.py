@@ -87,6 +87,20 @@ class GemmDesc(C.Structure):
                 ("residual", C.c_void_p), ("ldr", C.c_int64)]
 
 
+class AttnDesc(C.Structure):
+    """silgpu_attn_desc (include/silgpu.h)."""
+    _fields_ = [("Sq", C.c_int64), ("Sk", C.c_int64), ("D", C.c_int64),
+                ("batch_outer", C.c_int64), ("batch_inner", C.c_int64), ("scale", C.c_float),
+                ("Q", C.c_void_p), ("ldq", C.c_int64),
+                ("stride_q_outer", C.c_int64), ("stride_q_inner", C.c_int64),
+                ("K", C.c_void_p), ("ldk", C.c_int64),
+                ("stride_k_outer", C.c_int64), ("stride_k_inner", C.c_int64),
+                ("V", C.c_void_p), ("ldv", C.c_int64),
+                ("stride_v_outer", C.c_int64), ("stride_v_inner", C.c_int64),
+                ("O", C.c_void_p), ("ldo", C.c_int64),
+                ("stride_o_outer", C.c_int64), ("stride_o_inner", C.c_int64)]
+
+
 _SIGS = {
     "silgpu_last_error": (C.c_char_p, []),
     "silgpu_init": (_i, []),
@@ -125,6 +139,7 @@ _SIGS = {
                                 _vp, _i64, _i64, _i64, _vp, _i64, _i, _i, _i]),
     "silgpu_gemm": (_i, [C.POINTER(GemmDesc)]),
     "silgpu_sgemv": (_i, [_vp, _vp, _i64, _vp, _i64, _i64]),
+    "silgpu_attention_f32": (_i, [C.POINTER(AttnDesc)]),
     "silgpu_event_create": (_i, [C.POINTER(_vp)]),
     "silgpu_event_destroy": (_i, [_vp]),
     "silgpu_event_record": (_i, [_vp]),
@@ -343,6 +358,26 @@ def gemm(ta, tb, M, N, K, A, lda, B, ldb, Cm, ldc, batch_outer=1, batch_inner=1,
     d.residual = vp(residual).value if residual is not None else None
     d.ldr = ldr
     call("silgpu_gemm", C.byref(d))
+
+
+def attention(Sq, Sk, D, scale, Q, ldq, K, ldk, V, ldv, O, ldo, batch_outer=1, batch_inner=1,
+              strides_q=(0, 0), strides_k=(0, 0), strides_v=(0, 0), strides_o=(0, 0),
+              offsets=(0, 0, 0, 0)):
+    """silgpu_attention_f32; strides_x = (outer, inner) in elements; offsets
+    = element offsets of Q, K, V, O into their buffers."""
+    d = AttnDesc()
+    d.Sq, d.Sk, d.D, d.scale = Sq, Sk, D, scale
+    d.batch_outer, d.batch_inner = batch_outer, batch_inner
+    for name, buf, ld, st, off in (("Q", Q, ldq, strides_q, offsets[0]),
+                                   ("K", K, ldk, strides_k, offsets[1]),
+                                   ("V", V, ldv, strides_v, offsets[2]),
+                                   ("O", O, ldo, strides_o, offsets[3])):
+        p = vp(buf).value
+        setattr(d, name, (p + 4 * off) if p is not None else None)
+        setattr(d, "ld" + name.lower(), ld)
+        setattr(d, f"stride_{name.lower()}_outer", st[0])
+        setattr(d, f"stride_{name.lower()}_inner", st[1])
+    call("silgpu_attention_f32", C.byref(d))
 
 
 def sgemv(x, B, ldb, y, N, K):

@@ -26,7 +26,8 @@ BUILD = PKG / "_build"
 LIB = PKG / "libsilgpu.so"
 INCLUDE = ROOT / "include"
 
-HIP_SOURCES = ["runtime.hip", "elementwise.hip", "reduce.hip", "rowops.hip", "gemm.hip"]
+HIP_SOURCES = ["runtime.hip", "elementwise.hip", "reduce.hip", "rowops.hip", "gemm.hip",
+               "attention.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

@@ -54,19 +54,19 @@ __device__ __forceinline__ float4 apply4(float4 a, float4 b) {
 }
 
 // Both operands full length, 16-byte aligned: pure streaming.
-template <int OP>
+template <int OP, bool NT>
 __global__ __launch_bounds__(kBlock) void binary_full_vec(const float4 *__restrict__ a,
                                                           const float4 *__restrict__ b,
                                                           float4 *__restrict__ out,
                                                           int64_t n4) {
   int64_t stride = int64_t(gridDim.x) * kBlock;
   for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n4; i += stride)
-    out[i] = apply4<OP>(a[i], b[i]);
+    st4<NT>(out + i, apply4<OP>(ld4<NT>(a + i), ld4<NT>(b + i)));
 }
 
 // One side is a single value (scalar operand, the reference's B_length == 1
 // fast path, gpu_kernels.metal:891-893).  SCALAR_ON_B selects the side.
-template <int OP, bool SCALAR_ON_B>
+template <int OP, bool SCALAR_ON_B, bool NT>
 __global__ __launch_bounds__(kBlock) void binary_scalar_vec(const float4 *__restrict__ v,
                                                             const float *__restrict__ s,
                                                             float4 *__restrict__ out,
@@ -74,8 +74,10 @@ __global__ __launch_bounds__(kBlock) void binary_scalar_vec(const float4 *__rest
   float sv = s[0];
   float4 s4 = make_float4(sv, sv, sv, sv);
   int64_t stride = int64_t(gridDim.x) * kBlock;
-  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n4; i += stride)
-    out[i] = SCALAR_ON_B ? apply4<OP>(v[i], s4) : apply4<OP>(s4, v[i]);
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n4; i += stride) {
+    const float4 x = ld4<NT>(v + i);
+    st4<NT>(out + i, SCALAR_ON_B ? apply4<OP>(x, s4) : apply4<OP>(s4, x));
+  }
 }
 
 // Full-length operand against a repeating operand whose length is a multiple
@@ -140,22 +142,25 @@ int launch_binary_f32(const float *a, int64_t a_len, const float *b, int64_t b_l
   bool al = aligned16(a) && aligned16(b) && aligned16(out);
   if (al && n % 4 == 0) {
     int64_t n4 = n / 4;
+    const bool nt = n * 4 >= kStreamBytes;
+    const float4 *a4 = reinterpret_cast<const float4 *>(a);
+    const float4 *b4 = reinterpret_cast<const float4 *>(b);
+    float4 *o4 = reinterpret_cast<float4 *>(out);
     if (a_len == n && b_len == n) {
-      binary_full_vec<OP><<<grid_for(n4), kBlock, 0, s>>>(
-          reinterpret_cast<const float4 *>(a), reinterpret_cast<const float4 *>(b),
-          reinterpret_cast<float4 *>(out), n4);
+      if (nt) binary_full_vec<OP, true><<<grid_for(n4), kBlock, 0, s>>>(a4, b4, o4, n4);
+      else binary_full_vec<OP, false><<<grid_for(n4), kBlock, 0, s>>>(a4, b4, o4, n4);
       SILGPU_LAUNCH_CHECK("binary_full_vec");
       return SILGPU_OK;
     }
     if (a_len == n && b_len == 1) {
-      binary_scalar_vec<OP, true><<<grid_for(n4), kBlock, 0, s>>>(
-          reinterpret_cast<const float4 *>(a), b, reinterpret_cast<float4 *>(out), n4);
+      if (nt) binary_scalar_vec<OP, true, true><<<grid_for(n4), kBlock, 0, s>>>(a4, b, o4, n4);
+      else binary_scalar_vec<OP, true, false><<<grid_for(n4), kBlock, 0, s>>>(a4, b, o4, n4);
       SILGPU_LAUNCH_CHECK("binary_scalar_vec");
       return SILGPU_OK;
     }
     if (b_len == n && a_len == 1) {
-      binary_scalar_vec<OP, false><<<grid_for(n4), kBlock, 0, s>>>(
-          reinterpret_cast<const float4 *>(b), a, reinterpret_cast<float4 *>(out), n4);
+      if (nt) binary_scalar_vec<OP, false, true><<<grid_for(n4), kBlock, 0, s>>>(b4, a, o4, n4);
+      else binary_scalar_vec<OP, false, false><<<grid_for(n4), kBlock, 0, s>>>(b4, a, o4, n4);
       SILGPU_LAUNCH_CHECK("binary_scalar_vec");
       return SILGPU_OK;
     }
@@ -187,14 +192,14 @@ __device__ __forceinline__ float unary_f(float x) {
   else return fmaxf(x, 0.0f);
 }
 
-template <int OP>
+template <int OP, bool NT>
 __global__ __launch_bounds__(kBlock) void unary_vec(const float4 *__restrict__ in,
                                                     float4 *__restrict__ out, int64_t n4) {
   int64_t stride = int64_t(gridDim.x) * kBlock;
   for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n4; i += stride) {
-    float4 v = in[i];
-    out[i] = make_float4(unary_f<OP>(v.x), unary_f<OP>(v.y), unary_f<OP>(v.z),
-                         unary_f<OP>(v.w));
+    float4 v = ld4<NT>(in + i);
+    st4<NT>(out + i, make_float4(unary_f<OP>(v.x), unary_f<OP>(v.y), unary_f<OP>(v.z),
+                                 unary_f<OP>(v.w)));
   }
 }
 
@@ -209,8 +214,12 @@ __global__ __launch_bounds__(kBlock) void unary_scalar(const float *__restrict__
 template <int OP>
 int launch_unary(const float *in, float *out, int64_t n, hipStream_t s) {
   if (aligned16(in) && aligned16(out) && n % 4 == 0) {
-    unary_vec<OP><<<grid_for(n / 4), kBlock, 0, s>>>(
-        reinterpret_cast<const float4 *>(in), reinterpret_cast<float4 *>(out), n / 4);
+    if (n * 4 >= kStreamBytes)
+      unary_vec<OP, true><<<grid_for(n / 4), kBlock, 0, s>>>(
+          reinterpret_cast<const float4 *>(in), reinterpret_cast<float4 *>(out), n / 4);
+    else
+      unary_vec<OP, false><<<grid_for(n / 4), kBlock, 0, s>>>(
+          reinterpret_cast<const float4 *>(in), reinterpret_cast<float4 *>(out), n / 4);
     SILGPU_LAUNCH_CHECK("unary_vec");
   } else {
     unary_scalar<OP><<<grid_for(n), kBlock, 0, s>>>(in, out, n);
@@ -238,14 +247,15 @@ __global__ __launch_bounds__(kBlock) void bias_sigmoid_k(float *__restrict__ dat
     data[i] = sigmoidf_dev(data[i] + bias[i % cols]);
 }
 
+template <bool NT>
 __global__ __launch_bounds__(kBlock) void affine_vec(const float4 *__restrict__ in,
                                                      float4 *__restrict__ out, int64_t n4,
                                                      float scale, float offset) {
   int64_t stride = int64_t(gridDim.x) * kBlock;
   for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n4; i += stride) {
-    float4 v = in[i];
-    out[i] = make_float4(fmaf(v.x, scale, offset), fmaf(v.y, scale, offset),
-                         fmaf(v.z, scale, offset), fmaf(v.w, scale, offset));
+    float4 v = ld4<NT>(in + i);
+    st4<NT>(out + i, make_float4(fmaf(v.x, scale, offset), fmaf(v.y, scale, offset),
+                                 fmaf(v.z, scale, offset), fmaf(v.w, scale, offset)));
   }
 }
 
@@ -469,6 +479,7 @@ struct chain_launch {
 
 constexpr int kChainVec = 1;  // float4s per thread per grid-stride step
 
+template <bool NT>
 __global__ __launch_bounds__(kBlock) void affine_chain_k(chain_launch L,
                                                          float4 *__restrict__ out,
                                                          int64_t n4) {
@@ -480,7 +491,7 @@ __global__ __launch_bounds__(kBlock) void affine_chain_k(chain_launch L,
 #pragma unroll
     for (int u = 0; u < kChainVec; ++u) {
       int64_t i = base + int64_t(u) * kBlock;
-      v[u] = i < n4 ? in[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      v[u] = i < n4 ? ld4<NT>(in + i) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     for (int s = 0; s < L.n_steps; ++s) {
       float a = L.scale[s], b = L.offset[s];
@@ -495,7 +506,7 @@ __global__ __launch_bounds__(kBlock) void affine_chain_k(chain_launch L,
 #pragma unroll
     for (int u = 0; u < kChainVec; ++u) {
       int64_t i = base + int64_t(u) * kBlock;
-      if (i < n4) out[i] = v[u];
+      if (i < n4) st4<NT>(out + i, v[u]);
     }
   }
 }
@@ -626,9 +637,12 @@ int silgpu_affine_f32(const float *d_in, float *d_out, int64_t n, float scale,
   SILGPU_REQUIRE(d_in && d_out, "silgpu_affine_f32: null pointer");
   SILGPU_CTX(c);
   if (aligned16(d_in) && aligned16(d_out) && n % 4 == 0) {
-    affine_vec<<<grid_for(n / 4), kBlock, 0, c->stream>>>(
-        reinterpret_cast<const float4 *>(d_in), reinterpret_cast<float4 *>(d_out), n / 4,
-        scale, offset);
+    const float4 *i4 = reinterpret_cast<const float4 *>(d_in);
+    float4 *o4 = reinterpret_cast<float4 *>(d_out);
+    if (n * 4 >= kStreamBytes)
+      affine_vec<true><<<grid_for(n / 4), kBlock, 0, c->stream>>>(i4, o4, n / 4, scale, offset);
+    else
+      affine_vec<false><<<grid_for(n / 4), kBlock, 0, c->stream>>>(i4, o4, n / 4, scale, offset);
     SILGPU_LAUNCH_CHECK("affine_vec");
   } else {
     affine_scalar<<<grid_for(n), kBlock, 0, c->stream>>>(d_in, d_out, n, scale, offset);
@@ -709,8 +723,12 @@ int silgpu_program_f32(const silgpu_program *prog, float *d_out) {
       C.offset[s] = p.instrs[s + 1].imm2;
     }
     int64_t n4 = n / 4;
-    affine_chain_k<<<grid_for(n4, int64_t(kBlock) * kChainVec), kBlock, 0, c->stream>>>(
-        C, reinterpret_cast<float4 *>(d_out), n4);
+    if (n * 4 >= kStreamBytes)
+      affine_chain_k<true><<<grid_for(n4, int64_t(kBlock) * kChainVec), kBlock, 0, c->stream>>>(
+          C, reinterpret_cast<float4 *>(d_out), n4);
+    else
+      affine_chain_k<false><<<grid_for(n4, int64_t(kBlock) * kChainVec), kBlock, 0, c->stream>>>(
+          C, reinterpret_cast<float4 *>(d_out), n4);
     SILGPU_LAUNCH_CHECK("affine_chain_k");
     return SILGPU_OK;
   }

@@ -108,4 +108,38 @@ __device__ __forceinline__ float wave_min(float v) {
 
 __device__ __forceinline__ float sigmoidf_dev(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// 16-byte loads and stores; NT: non-temporal (streaming) accesses, for data
+// touched once and too large to be served from the caches by a consumer.
+// A copy on MI355X reaches 6.5 TB/s with both non-temporal against 5.95 TB/s
+// with neither.
+template <bool NT>
+__device__ __forceinline__ float4 ld4(const float4 *p) {
+  if constexpr (NT) {
+    float4 v;
+    v.x = __builtin_nontemporal_load(&p->x);
+    v.y = __builtin_nontemporal_load(&p->y);
+    v.z = __builtin_nontemporal_load(&p->z);
+    v.w = __builtin_nontemporal_load(&p->w);
+    return v;
+  } else {
+    return *p;
+  }
+}
+template <bool NT>
+__device__ __forceinline__ void st4(float4 *p, float4 v) {
+  if constexpr (NT) {
+    __builtin_nontemporal_store(v.x, &p->x);
+    __builtin_nontemporal_store(v.y, &p->y);
+    __builtin_nontemporal_store(v.z, &p->z);
+    __builtin_nontemporal_store(v.w, &p->w);
+  } else {
+    *p = v;
+  }
+}
+
+// Streaming kernels switch to non-temporal accesses from this many bytes per
+// operand (half the 256 MiB Infinity Cache: smaller results are likely to
+// be read again from the cache by the next kernel of a graph).
+constexpr int64_t kStreamBytes = int64_t(128) << 20;
+
 }  // namespace silgpu

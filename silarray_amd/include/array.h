@@ -1828,6 +1828,50 @@ inline void eval_batched(node *n) {
   n->strides = cs;
 }
 
+// Folds the leading `L` axes of `shape` into at most two groups that every
+// operand strides uniformly (stride[d] == stride[d+1] * shape[d+1]): the
+// inner group [inner, L) and the outer [0, inner).  False when the axes
+// need more groups or the batch exceeds the grid.
+inline bool fold_two_groups(const shape_type &shape, size_t L,
+                            const std::vector<const strides_type *> &ops, int64_t &bo,
+                            int64_t &bi, std::vector<std::pair<int64_t, int64_t>> &st) {
+  bo = bi = 1;
+  st.assign(ops.size(), {0, 0});
+  if (L == 0) return true;
+  auto uniform = [&](size_t d) {
+    for (const strides_type *s : ops)
+      if ((*s)[d] != (*s)[d + 1] * shape[d + 1]) return false;
+    return true;
+  };
+  size_t inner = L - 1;
+  bi = int64_t(shape[L - 1]);
+  while (inner > 0 && uniform(inner - 1)) bi *= int64_t(shape[--inner]);
+  if (inner > 0) {
+    size_t outer = inner - 1;
+    bo = int64_t(shape[outer]);
+    while (outer > 0 && uniform(outer - 1)) bo *= int64_t(shape[--outer]);
+    if (outer > 0) return false;
+  }
+  if (bo * bi > 65535) return false;
+  for (size_t i = 0; i < ops.size(); i++)
+    st[i] = {inner > 0 ? int64_t((*ops[i])[inner - 1]) : 0, int64_t((*ops[i])[L - 1])};
+  return true;
+}
+
+// A fused attention launch: n = batched_dot(softmax(q k^T * scale), v).
+struct attention_plan {
+  node *q = nullptr, *kt = nullptr, *v = nullptr;
+  float scale = 1.0f;
+  silgpu_attn_desc desc{};  // extents, leading dimensions and batch strides
+};
+
+inline void eval_attention(node *n, const attention_plan &p) {
+  auto out = new_output(n->shape);
+  gpu::attention(p.desc, p.q->data, p.kt->data, p.v->data, out);
+  finish(n, std::move(out));
+  if (!n->out_strides.empty()) n->strides = n->out_strides;
+}
+
 inline void eval_node_nonfused(node *n) {
   switch (n->operation) {
     case op::dot:
@@ -2063,12 +2107,96 @@ inline void evaluate(const std::vector<node *> &roots) {
     relayout[v] = p;
     relayout[n] = p;
   }
+  //  batched_dot(view?(softmax(view?(S))), v) with S = batched_dot(q, k^T)
+  //  (its scalar scale folded above) and the scores used by nothing else:
+  //  one fused attention launch, the scores never stored
+  //  (silgpu_attention_f32).  Needs unit stride along the head dim of q,
+  //  k and v, a head dim of 16, 32, 64 or 128, and leading axes that fold
+  //  into two uniformly strided batch groups.
+  std::unordered_map<node *, attention_plan> attention;
+  std::unordered_set<node *> attn_inner;  // nodes a fused attention computes
+  auto plain_view = [](node *x) {
+    return x->operation == op::view && x->view_off == 0 &&
+           x->strides == contiguous_strides(x->shape);
+  };
+  for (node *n : order) {
+    if (n->operation != op::batched_dot || n->use_scale || n->residual) continue;
+    std::vector<node *> inner;
+    node *prev = n, *cur = n->inputs[0].get();
+    auto step = [&](node *next) {
+      inner.push_back(cur);
+      prev = cur;
+      cur = next;
+    };
+    if (plain_view(cur)) {
+      if (!single_use(cur, prev)) continue;
+      step(cur->inputs[0].get());
+    }
+    if (cur->operation != op::softmax || cur->shape.size() != 2 || !single_use(cur, prev))
+      continue;
+    step(cur->inputs[0].get());
+    if (plain_view(cur)) {
+      if (!single_use(cur, prev)) continue;
+      step(cur->inputs[0].get());
+    }
+    node *s1 = cur;
+    if (auto it = alias.find(cur); it != alias.end()) {
+      if (!single_use(cur, prev)) continue;
+      s1 = it->second;
+      step(s1);
+    }
+    if (s1->operation != op::batched_dot || s1->residual || !single_use(s1, prev)) continue;
+    if (s1->use_scale && s1->scale_offset != 0.0f) continue;
+    inner.push_back(s1);
+    const size_t nd = n->shape.size();
+    if (nd < 2 || s1->shape.size() != nd || inner.front()->shape != s1->shape) continue;
+    node *q = s1->inputs[0].get(), *kt = s1->inputs[1].get(), *v = n->inputs[1].get();
+    const size_t Sq = s1->shape[nd - 2], Sk = s1->shape[nd - 1], D = q->shape[nd - 1];
+    if (n->shape[nd - 1] != D || (D != 16 && D != 32 && D != 64 && D != 128)) continue;
+    if (q->strides[nd - 1] != 1 || kt->strides[nd - 2] != 1 || v->strides[nd - 1] != 1)
+      continue;
+    const strides_type cs =
+        n->out_strides.empty() ? contiguous_strides(n->shape) : n->out_strides;
+    const int64_t ldq = Sq > 1 ? int64_t(q->strides[nd - 2]) : int64_t(D);
+    const int64_t ldk = Sk > 1 ? int64_t(kt->strides[nd - 1]) : int64_t(D);
+    const int64_t ldv = Sk > 1 ? int64_t(v->strides[nd - 2]) : int64_t(D);
+    const int64_t ldo = Sq > 1 ? int64_t(cs[nd - 2]) : int64_t(D);
+    if (ldq < int64_t(D) || ldk < int64_t(D) || ldv < int64_t(D) || ldo < int64_t(D)) continue;
+    attention_plan ap;
+    std::vector<std::pair<int64_t, int64_t>> st;
+    if (!fold_two_groups(n->shape, nd - 2, {&q->strides, &kt->strides, &v->strides, &cs},
+                         ap.desc.batch_outer, ap.desc.batch_inner, st))
+      continue;
+    ap.q = q;
+    ap.kt = kt;
+    ap.v = v;
+    ap.scale = s1->use_scale ? s1->scale : 1.0f;
+    ap.desc.Sq = int64_t(Sq);
+    ap.desc.Sk = int64_t(Sk);
+    ap.desc.D = int64_t(D);
+    ap.desc.scale = ap.scale;
+    ap.desc.ldq = ldq;
+    ap.desc.ldk = ldk;
+    ap.desc.ldv = ldv;
+    ap.desc.ldo = ldo;
+    ap.desc.stride_q_outer = st[0].first;
+    ap.desc.stride_q_inner = st[0].second;
+    ap.desc.stride_k_outer = st[1].first;
+    ap.desc.stride_k_inner = st[1].second;
+    ap.desc.stride_v_outer = st[2].first;
+    ap.desc.stride_v_inner = st[2].second;
+    ap.desc.stride_o_outer = st[3].first;
+    ap.desc.stride_o_inner = st[3].second;
+    attention[n] = ap;
+    for (node *x : inner) attn_inner.insert(x);
+  }
   // A node is computed inside its consumer's program when it is elementwise,
   // has exactly one consumer, that consumer is elementwise, it is not a root
   // and no array outside the graph holds it.
   auto fusable = [&](node *c) {
     if (c->evaluated || root_set.count(c) || !is_elementwise(c->operation)) return false;
-    if (materialize.count(c) || alias.count(c) || relayout.count(c)) return false;
+    if (materialize.count(c) || alias.count(c) || relayout.count(c) || attn_inner.count(c))
+      return false;
     auto it = consumers.find(c);
     if (it == consumers.end() || it->second != 1) return false;
     if (!is_elementwise(parent[c]->operation)) return false;
@@ -2080,6 +2208,11 @@ inline void evaluate(const std::vector<node *> &roots) {
   };
   for (node *n : order) {
     if (n->evaluated) continue;
+    if (attn_inner.count(n)) continue;  // computed inside a fused attention launch
+    if (auto it = attention.find(n); it != attention.end()) {
+      eval_attention(n, it->second);
+      continue;
+    }
     if (auto it = alias.find(n); it != alias.end()) {
       node *c = it->second;
       if (!c->evaluated) throw std::runtime_error("array: fused product not evaluated.");

@@ -225,6 +225,17 @@ class gpu {
     launched_(silgpu_gemm(&d), "gemm");
   }
 
+  // Fused attention (the lowering target of sil::eval for
+  // batched_dot(softmax(batched_dot(q, k^T) * s), v)).
+  static void attention(silgpu_attn_desc d, const storage &Q, const storage &K,
+                        const storage &V, storage &O) {
+    d.Q = Q.dev_in<float>();
+    d.K = K.dev_in<float>();
+    d.V = V.dev_in<float>();
+    d.O = O.dev_out<float>();
+    launched_(silgpu_attention_f32(&d), "attention");
+  }
+
   // Fused elementwise program (the lowering target of sil::eval).
   static void program(const silgpu_program &p, storage &OUT) {
     launched_(silgpu_program_f32(&p, OUT.dev_out<float>()), "program");

@@ -562,6 +562,32 @@ TEST_CASE("head merge: the product writes the permuted layout, bit-identical") {
   CHECK(twice);
 }
 
+TEST_CASE("attention graph runs as one fused launch, matching the unfused graph") {
+  // softmax(q k^T * scale) v over head views of a qkv array, the result
+  // head-merged: evaluated fused (scores used by nothing else) and unfused
+  // (scores requested too), then compared within fp32 rounding.
+  const size_t B = 2, S = 77, H = 3, dh = 32, D = H * dh;
+  auto qkv = random({B * S, 3 * D});
+  auto heads = qkv.view({B, S, 3, H, dh}).permute({2, 0, 3, 1, 4});
+  auto q = heads.select(0, 0), k = heads.select(0, 1), v = heads.select(0, 2);
+  const float scale = 1.0f / std::sqrt(float(dh));
+  auto scores_of = [&] { return q.batched_dot(k.permute({0, 1, 3, 2})) * scale; };
+  auto attend = [&](const array<float> &scores) {
+    auto attn = scores.view({B * H * S, S}).softmax().view({B, H, S, S});
+    return attn.batched_dot(v).permute({0, 2, 1, 3}).view({B * S, D});
+  };
+  auto fused = attend(scores_of());
+  eval(fused);
+  auto scores = scores_of();
+  auto plain = attend(scores);
+  eval(scores, plain);  // the scores are a root: nothing fuses across them
+  CHECK(fused.shape() == (shape_type{B * S, D}) && plain.shape() == fused.shape());
+  const float *a = std::as_const(fused).buffer_data(), *b = std::as_const(plain).buffer_data();
+  float worst = 0.0f;
+  for (size_t i = 0; i < B * S * D; i++) worst = std::max(worst, std::abs(a[i] - b[i]));
+  CHECK(worst <= 1e-5f);  // v in [0, 1): outputs are convex combinations of v rows
+}
+
 HOST_CASE("view, permute and select on evaluated arrays") {
   auto m = array<int>({2, 3, 4}, iota_n(24));
   auto p = m.permute({2, 0, 1});

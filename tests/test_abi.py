@@ -80,6 +80,24 @@ def test_validation_errors_without_device(lib):
     assert f("silgpu_softmax_rows_f32")(None, None, 0, 8) == 0
 
 
+def test_attention_validation(lib):
+    d = lib.AttnDesc()
+    d.Sq, d.Sk, d.D, d.batch_outer, d.batch_inner, d.scale = 8, 8, 48, 1, 1, 1.0
+    d.Q = d.K = d.V = d.O = 16
+    d.ldq = d.ldk = d.ldv = d.ldo = 64
+    rc = lib.raw("silgpu_attention_f32")(C.byref(d))
+    assert rc == lib.ERR_INVALID and "head dim" in lib.last_error()
+    d.D, d.ldq = 64, 60
+    rc = lib.raw("silgpu_attention_f32")(C.byref(d))
+    assert rc == lib.ERR_INVALID and "row stride" in lib.last_error()
+    d.ldq = 64
+    d.Sq = -1
+    rc = lib.raw("silgpu_attention_f32")(C.byref(d))
+    assert rc == lib.ERR_INVALID and "negative" in lib.last_error()
+    d.Sq = 0  # empty work is a no-op success
+    assert lib.raw("silgpu_attention_f32")(C.byref(d)) == 0
+
+
 def test_program_validation(lib):
     p = lib.make_program((4,), [(16, (1,))], [(lib.PI_LOAD, 0, 3, 0, 0.0, 0.0)])
     rc = lib.raw("silgpu_program_f32")(C.byref(p), C.c_void_p(16))

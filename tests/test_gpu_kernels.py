@@ -730,3 +730,73 @@ def test_sgemm_lds_direct_batched(native, oracle, ta, tb, tile, K, splits):
         ref = np.maximum(C64 + bias, 0)
         ok, nw, el = gemm_tolerance_ok(Cg[z], ref, Cabs + np.abs(bias), K)
         assert ok, (z, nw, el)
+
+
+# ---- fused attention ----------------------------------------------------------------
+
+def _attention_f64(Q, K, V, scale):
+    """softmax(scale * Q K^T) V per leading index, in float64 (the unfused
+    reference graph: product, scalar scale, row softmax, product)."""
+    S = np.einsum("...qd,...kd->...qk", Q.astype(np.float64), K.astype(np.float64)) * scale
+    S -= S.max(axis=-1, keepdims=True)
+    P = np.exp(S)
+    P /= P.sum(axis=-1, keepdims=True)
+    return P @ V.astype(np.float64)
+
+
+# B, H, Sq, Sk, D, layout ("merged": [B, S, H, D] buffers as attention heads
+# split out of a [B*S, H*D] array; "heads": contiguous [B, H, S, D])
+ATTN_CASES = [(1, 1, 64, 64, 64, "heads"), (2, 3, 37, 100, 64, "merged"),
+              (1, 2, 130, 1, 32, "heads"), (1, 1, 5, 200, 16, "merged"),
+              (2, 2, 64, 77, 128, "merged"), (4, 12, 512, 512, 64, "merged"),
+              (3, 1, 200, 64, 32, "heads"), (2, 2, 33, 70, 32, "unaligned")]
+
+
+@pytest.mark.parametrize("B,H,Sq,Sk,D,layout", ATTN_CASES)
+def test_attention_fused(native, B, H, Sq, Sk, D, layout):
+    """silgpu_attention_f32 against float64 on seeded N(0, 1) inputs: every
+    output is a convex combination of V rows, so the error is measured
+    against max|V|; tolerance 2e-5 * sqrt(max(D, Sk))."""
+    announce(f"attention B={B} H={H} Sq={Sq} Sk={Sk} D={D} {layout}")
+    g = rng(5100 + B * H + Sq + Sk + D)
+    scale = float(np.float32(1.0 / np.sqrt(D)))
+
+    def make(S):
+        if layout == "unaligned":  # rows of D + 1 floats, buffer offset by one float
+            buf = g.normal(0, 1, (B, H, S, D + 1)).astype(np.float32)
+            return buf, buf[..., :D], D + 1, (H * S * (D + 1), S * (D + 1))
+        if layout == "merged":
+            buf = g.normal(0, 1, (B, S, H, D)).astype(np.float32)
+            view = buf.transpose(0, 2, 1, 3)  # [B, H, S, D]
+            return buf, view, H * D, (S * H * D, D)
+        buf = g.normal(0, 1, (B, H, S, D)).astype(np.float32)
+        return buf, buf, D, (H * S * D, S * D)
+
+    qb, Qv, ldq, sq = make(Sq)
+    kb, Kv, ldk, sk = make(Sk)
+    vb, Vv, ldv, sv = make(Sk)
+    ob = np.full(qb.shape, np.nan, np.float32)
+    dQ, dK, dV, dO = up(native, qb), up(native, kb), up(native, vb), up(native, ob)
+    off = (1, 1, 1, 0) if layout == "unaligned" else (0, 0, 0, 0)
+    if off[0]:  # Q, K, V start one float into their buffers (rows D + 1 wide)
+        qb, kb, vb = (np.concatenate([[0.0], x.ravel()]).astype(np.float32) for x in (qb, kb, vb))
+        dQ, dK, dV = up(native, qb), up(native, kb), up(native, vb)
+    native.attention(Sq, Sk, D, scale, dQ, ldq, dK, ldk, dV, ldv, dO, ldq, B, H, sq, sk, sv, sq,
+                     offsets=off)
+    out = down(native, dO, ob.shape)
+    Ov = out.transpose(0, 2, 1, 3) if layout == "merged" else out
+    if layout == "unaligned":
+        Ov = Ov[..., :D]
+    ref = _attention_f64(Qv, Kv, Vv, scale)
+    err = np.abs(Ov.astype(np.float64) - ref).max()
+    tol = 2e-5 * np.sqrt(max(D, Sk)) * np.abs(Vv).max()
+    assert np.isfinite(Ov).all() and err <= tol, (err, tol)
+
+
+def test_attention_no_keys_gives_zero(native):
+    announce("attention Sk=0")
+    ob = np.full((2, 16, 32), np.nan, np.float32)
+    dO = up(native, ob)
+    native.attention(16, 0, 32, 1.0, None, 32, None, 32, None, 32, dO, 32, 1, 2, (0, 0),
+                     (0, 0), (0, 0), (0, 16 * 32))
+    assert np.all(down(native, dO, ob.shape) == 0)
