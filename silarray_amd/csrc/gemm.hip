@@ -557,22 +557,23 @@ __global__ __launch_bounds__(kSkWaves *kWave) void sgemm_skinny_k(gemm_args p) {
   }
 }
 
-// ---- SGEMM with LDS-direct operand loads (BT x BT x BK tiles, BT 256 or 128)
+// ---- SGEMM with LDS-direct operand loads (BM x BN x BK tiles: 256 x 256,
+// 128 x 128, 128 x 64)
 //
-// Full tiles only (M, N multiples of BT, K range a multiple of BK, 16-byte
-// aligned operands): every lane's 16-byte global_load_lds_dwordx4 stays in
-// bounds, so no lane needs masking.  The load engine writes each wave's 64 x
-// 16 bytes to one contiguous 1 KB LDS window (lane L at 16 L), with no
-// staging registers and no ds_write; the layout is chosen through which
-// global chunk each lane fetches.  An operand tile (BT x BK) takes
-// BT * BK / 256 windows either way:
+// Full tiles only (M, N multiples of BM, BN, K range a multiple of BK,
+// 16-byte aligned operands): every lane's 16-byte global_load_lds_dwordx4
+// stays in bounds, so no lane needs masking.  The load engine writes each
+// wave's 64 x 16 bytes to one contiguous 1 KB LDS window (lane L at 16 L),
+// with no staging registers and no ds_write; the layout is chosen through
+// which global chunk each lane fetches.  An operand tile of extent X (BM for
+// A, BN for B) by BK takes X * BK / 256 windows either way:
 //   - contiguous in K (A, or B transposed): a window holds 16 rows x 16 k,
-//     window kh * BT/16 + rg holding rows 16 rg.. and k 16 kh..; the 16-byte
+//     window kh * X/16 + rg holding rows 16 rg.. and k 16 kh..; the 16-byte
 //     chunk of (row rr, k quad kq) sits at position rr*4 + (kq ^ ((rr/2) & 3));
-//   - contiguous in M or N (A transposed, or B), BT = 256: one k row per
-//     window, pitch 260 floats;
-//   - contiguous in M or N, BT = 128: two k rows per window (lanes 0-31 the
-//     even row, 32-63 the odd row), pitch 264.
+//   - contiguous in M or N (A transposed, or B): X = 256 one k row per
+//     window, pitch 260 floats; X = 128 two k rows per window (lanes 0-31
+//     the even row, 32-63 the odd one), pitch 264; X = 64 four k rows per
+//     window (lanes 16p .. 16p+15 row p), pitch 272.
 // MFMA step j of a 16-deep k block puts k = 4g + j in the k slot g = lane/16
 // of both operands (any assignment of k to slots sums the same products), so
 // a K-contiguous operand is read with one ds_read_b128 per 16-row block and
@@ -582,32 +583,44 @@ __global__ __launch_bounds__(kSkWaves *kWave) void sgemm_skinny_k(gemm_args p) {
 // banks and ds_read_b128 16 lanes per pass (equal lane bit 5 and equal
 // parity of lane bits 2-4) over 64 banks, as measured with the bank-conflict
 // counter; the swizzle and pitches make every read conflict-free under that
-// model (tests/test_gemm_layout.py).  BT = 256: 8 waves (2 x 4) of 128 x 64;
-// BT = 128: 4 waves (2 x 2) of 64 x 64.  The next K tile's loads are issued
-// before the current tile is multiplied, and one s_waitcnt + barrier ends
-// each tile; BK = 32 halves the barriers per flop (two 256 x 32 stages take
-// 130 KB of the 160 KB LDS).
+// model (tests/test_gemm_layout.py).  256 x 256: 8 waves (2 x 4) of 128 x 64;
+// 128 x 128: 4 waves (2 x 2) of 64 x 64; 128 x 64: 4 waves of 64 x 32.  The
+// next K tile's loads are issued before the current tile is multiplied, and
+// one s_waitcnt + barrier ends each tile; BK = 32 halves the barriers per
+// flop (two 256 x 32 stages take 130 KB of the 160 KB LDS).
 constexpr int kDtlBK = 16;  // K granularity of the path (BK = 16 or 32)
 
-// NW waves per workgroup in a 2 x NW/2 grid: BT = 256 with 8 waves (128 x 64
-// each, two waves per SIMD) or 4 waves (128 x 128, one wave per SIMD with 256
-// accumulators per lane); BT = 128 with 4 waves of 64 x 64.
-template <int BT, int BK, int NW = BT == 256 ? 8 : 4, int NS = 2>
+// Pitch (floats) of an M/N-contiguous window for a tile extent X: one k row
+// per window for 256, two for 128, four for 64 (the rows of one window at
+// 0, X, 2X, ..; consecutive windows 16 banks apart, so a ds_read_b32 half-wave
+// over k rows 4 apart is conflict-free).
+template <int X>
+constexpr int dtl_pitch() {
+  return X == 256 ? 260 : X == 128 ? 264 : 272;
+}
+
+// BM x BN tiles, NW waves in a 2 x NW/2 grid: 256 x 256 with 8 waves (128 x
+// 64 each, two waves per SIMD) or 4 waves (128 x 128, one wave per SIMD with
+// 256 accumulators per lane); 128 x 128 with 4 waves of 64 x 64; 128 x 64
+// with 4 waves of 64 x 32.
+template <int BM, int BN, int BK, int NW = (BM == 256 ? 8 : 4), int NS = 2>
 struct dtl_cfg {
   static constexpr int WM = 2, WN = NW / 2;
   static constexpr int kThreads = WM * WN * kWave;
-  static constexpr int TM = BT / WM / 16, TN = BT / WN / 16;  // 16x16 blocks per wave
-  static constexpr int kWin = BT * BK / 256;                  // windows per operand tile
-  static constexpr int kPitch = BT == 256 ? 260 : 264;        // M/N-contiguous window pitch
-  static constexpr int kOperand = kWin * kPitch;              // floats (>= the K-contiguous 256)
-  static constexpr int kStage = 2 * kOperand;
+  static constexpr int TM = BM / WM / 16, TN = BN / WN / 16;  // 16x16 blocks per wave
+  static constexpr int kWinA = BM * BK / 256, kWinB = BN * BK / 256;  // windows per operand
+  // floats per operand tile (>= the K-contiguous 256 per window)
+  static constexpr int kOperandA = kWinA * dtl_pitch<BM>();
+  static constexpr int kOperandB = kWinB * dtl_pitch<BN>();
+  static constexpr int kStage = kOperandA + kOperandB;
   static constexpr int kLdsBytes = NS * kStage * 4;  // static, NS arrays of kStage floats
   // Waves per SIMD the register allocation aims at: one 8-wave workgroup per
-  // CU (LDS allows no second) for BT = 256, three 4-wave workgroups for 128.
-  // Without it the compiler squeezes the 256 tile toward three waves and
-  // serialises the first fragment reads of every K tile.
-  static constexpr int kWavesPerEU = BT == 256 ? NW / 4 : 3;
-  static_assert(BK % kDtlBK == 0 && kWin % (WM * WN) == 0, "windows per wave");
+  // CU (LDS allows no second) for 256 x 256, three 4-wave workgroups for the
+  // smaller tiles.  Without it the compiler squeezes the 256 tile toward
+  // three waves and serialises the first fragment reads of every K tile.
+  static constexpr int kWavesPerEU = (BM == 256 && BN == 256) ? NW / 4 : 3;
+  static_assert(BK % kDtlBK == 0 && kWinA % (WM * WN) == 0 && kWinB % (WM * WN) == 0,
+                "windows per wave");
   static_assert(kLdsBytes <= 160 * 1024, "LDS");
 };
 
@@ -616,36 +629,40 @@ __device__ __forceinline__ void dtl16(const float *src, float *lds_dst) {
                                    (__attribute__((address_space(3))) void *)lds_dst, 16, 0, 0);
 }
 
-// Source of lane `lane` for window w of an operand tile starting at x0
-// (rows x0.. of a [rows][K] operand when KCONTIG, else columns x0.. of a
-// [K][cols] operand; k relative to the tile).
-template <bool KCONTIG, int BT>
+// Source of lane `lane` for window w of an operand tile of extent X starting
+// at x0 (rows x0.. of a [rows][K] operand when KCONTIG, else columns x0.. of
+// a [K][cols] operand; k relative to the tile).
+template <bool KCONTIG, int X>
 __device__ __forceinline__ const float *dtl_src(const float *base, int64_t ld, int x0, int w,
                                                 int lane) {
   if constexpr (KCONTIG) {
     const int rr = lane / 4, kq = (lane % 4) ^ ((rr / 2) & 3);
-    const int rg = w % (BT / 16), kh = w / (BT / 16);
+    const int rg = w % (X / 16), kh = w / (X / 16);
     return base + int64_t(x0 + 16 * rg + rr) * ld + 16 * kh + 4 * kq;
-  } else if constexpr (BT == 256) {
+  } else if constexpr (X == 256) {
     return base + int64_t(w) * ld + x0 + 4 * lane;
-  } else {
+  } else if constexpr (X == 128) {
     return base + int64_t(2 * w + lane / 32) * ld + x0 + 4 * (lane % 32);
+  } else {
+    return base + int64_t(4 * w + lane / 16) * ld + x0 + 4 * (lane % 16);
   }
 }
-template <bool KCONTIG, int BT>
+template <bool KCONTIG, int X>
 __device__ __forceinline__ int dtl_window(int w) {
-  return KCONTIG ? w * 256 : w * dtl_cfg<BT, kDtlBK>::kPitch;
+  return KCONTIG ? w * 256 : w * dtl_pitch<X>();
 }
-// LDS offset (floats) of element (x, k) of an operand tile.
-template <bool KCONTIG, int BT>
+// LDS offset (floats) of element (x, k) of an operand tile of extent X.
+template <bool KCONTIG, int X>
 __device__ __forceinline__ int dtl_elem(int x, int k) {
   if constexpr (KCONTIG) {
-    return ((k / 16) * (BT / 16) + x / 16) * 256 +
+    return ((k / 16) * (X / 16) + x / 16) * 256 +
            ((x % 16) * 4 + (((k % 16) / 4) ^ (((x % 16) / 2) & 3))) * 4 + (k % 4);
-  } else if constexpr (BT == 256) {
-    return k * dtl_cfg<BT, kDtlBK>::kPitch + x;
+  } else if constexpr (X == 256) {
+    return k * dtl_pitch<X>() + x;
+  } else if constexpr (X == 128) {
+    return (k / 2) * dtl_pitch<X>() + 128 * (k % 2) + x;
   } else {
-    return (k / 2) * dtl_cfg<BT, kDtlBK>::kPitch + 128 * (k % 2) + x;
+    return (k / 4) * dtl_pitch<X>() + 64 * (k % 4) + x;
   }
 }
 
@@ -656,14 +673,15 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
 }
 
-template <int BT, int BK, int NWV, int NS, bool TA, bool TB>
-__global__ __launch_bounds__((dtl_cfg<BT, BK, NWV, NS>::kThreads))
-__attribute__((amdgpu_waves_per_eu(dtl_cfg<BT, BK, NWV, NS>::kWavesPerEU,
-                                   dtl_cfg<BT, BK, NWV, NS>::kWavesPerEU))) void sgemm_dtl_k(gemm_args p) {
-  using D = dtl_cfg<BT, BK, NWV, NS>;
+template <int BM, int BN, int BK, int NWV, int NS, bool TA, bool TB>
+__global__ __launch_bounds__((dtl_cfg<BM, BN, BK, NWV, NS>::kThreads))
+__attribute__((amdgpu_waves_per_eu(dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU,
+                                   dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU))) void sgemm_dtl_k(gemm_args p) {
+  using D = dtl_cfg<BM, BN, BK, NWV, NS>;
   static_assert(NS == 2 || NS == 4, "stages");
   using F = mfma<16>;
-  constexpr int TM = D::TM, TN = D::TN, NW = D::WM * D::WN, WPW = D::kWin / NW;
+  constexpr int TM = D::TM, TN = D::TN, NW = D::WM * D::WN;
+  constexpr int WPA = D::kWinA / NW, WPB = D::kWinB / NW;  // windows per wave
   constexpr bool AK = !TA, BKc = TB;  // operand contiguous in K
   // NS stages as NS LDS objects: alias analysis then sees that the loads
   // into one stage cannot touch the fragment reads from another, and the
@@ -677,7 +695,7 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BT, BK, NWV, NS>::kWavesPerEU,
   const int wm = wave / D::WN, wn = wave % D::WN;
   int tm, tn;
   tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-  const int m0 = tm * BT, n0 = tn * BT;
+  const int m0 = tm * BM, n0 = tn * BN;
   const int64_t zo = blockIdx.z / p.binner, zi = blockIdx.z % p.binner;
   const float *__restrict__ A = p.A + zo * p.sA2 + zi * p.sA;
   const float *__restrict__ B = p.B + zo * p.sB2 + zi * p.sB;
@@ -686,24 +704,24 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BT, BK, NWV, NS>::kWavesPerEU,
   const int kbeg = blockIdx.y * p.klen;
   const int kend = min(p.K, kbeg + p.klen);
   const int KT = kend > kbeg ? (kend - kbeg) / BK : 0;  // K % BK == 0 on this path
-  // This wave loads windows wave + q*NW, q < WPW, of each operand.
-  const float *a_src[WPW], *b_src[WPW];
+  // This wave loads windows wave + q*NW (q < WPA, WPB) of each operand.
+  const float *a_src[WPA], *b_src[WPB];
 #pragma unroll
-  for (int q = 0; q < WPW; ++q) {
-    a_src[q] = dtl_src<AK, BT>(A, p.lda, m0, wave + q * NW, lane);
-    b_src[q] = dtl_src<BKc, BT>(B, p.ldb, n0, wave + q * NW, lane);
-  }
+  for (int q = 0; q < WPA; ++q) a_src[q] = dtl_src<AK, BM>(A, p.lda, m0, wave + q * NW, lane);
+#pragma unroll
+  for (int q = 0; q < WPB; ++q) b_src[q] = dtl_src<BKc, BN>(B, p.ldb, n0, wave + q * NW, lane);
   // Advance of one K tile for each operand.
   const int64_t a_step = AK ? BK : int64_t(BK) * p.lda;
   const int64_t b_step = BKc ? BK : int64_t(BK) * p.ldb;
-  constexpr int kBOff = D::kOperand;
+  constexpr int kBOff = D::kOperandA;
   auto issue = [&](int kt, float *S) {
     const int64_t k = int64_t(kbeg / BK + kt);
 #pragma unroll
-    for (int q = 0; q < WPW; ++q) {
-      dtl16(a_src[q] + k * a_step, S + dtl_window<AK, BT>(wave + q * NW));
-      dtl16(b_src[q] + k * b_step, S + kBOff + dtl_window<BKc, BT>(wave + q * NW));
-    }
+    for (int q = 0; q < WPA; ++q)
+      dtl16(a_src[q] + k * a_step, S + dtl_window<AK, BM>(wave + q * NW));
+#pragma unroll
+    for (int q = 0; q < WPB; ++q)
+      dtl16(b_src[q] + k * b_step, S + kBOff + dtl_window<BKc, BN>(wave + q * NW));
   };
   typename F::acc_t acc[TM][TN];
 #pragma unroll
@@ -732,23 +750,23 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BT, BK, NWV, NS>::kWavesPerEU,
     if constexpr (AK) {
 #pragma unroll
       for (int i = 0; i < TM; ++i)
-        read4(a4[kh & 1][i], Sa + dtl_elem<true, BT>(xa + 16 * i, 16 * kh + 4 * kg));
+        read4(a4[kh & 1][i], Sa + dtl_elem<true, BM>(xa + 16 * i, 16 * kh + 4 * kg));
     }
     if constexpr (BKc) {
 #pragma unroll
       for (int j = 0; j < TN; ++j)
-        read4(b4[kh & 1][j], Sb + dtl_elem<true, BT>(xb + 16 * j, 16 * kh + 4 * kg));
+        read4(b4[kh & 1][j], Sb + dtl_elem<true, BN>(xb + 16 * j, 16 * kh + 4 * kg));
     }
   };
   auto read_step = [&](const float *Sa, const float *Sb, int st) {
     const int k = 16 * (st / 4) + 4 * kg + st % 4;
     if constexpr (!AK) {
 #pragma unroll
-      for (int i = 0; i < TM; ++i) a1[st & 1][i] = Sa[dtl_elem<false, BT>(xa + 16 * i, k)];
+      for (int i = 0; i < TM; ++i) a1[st & 1][i] = Sa[dtl_elem<false, BM>(xa + 16 * i, k)];
     }
     if constexpr (!BKc) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j) b1[st & 1][j] = Sb[dtl_elem<false, BT>(xb + 16 * j, k)];
+      for (int j = 0; j < TN; ++j) b1[st & 1][j] = Sb[dtl_elem<false, BN>(xb + 16 * j, k)];
     }
   };
   auto fa = [&](int st, int i) -> float {
@@ -762,7 +780,7 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BT, BK, NWV, NS>::kWavesPerEU,
   // Waits until this wave's loads of tile `next` have landed, leaving the
   // loads of the tiles after it (at most NS - 2, kDma instructions each) in
   // flight, then the barrier makes every wave's loads visible.
-  constexpr int kDma = 2 * WPW;
+  constexpr int kDma = WPA + WPB;
   auto land = [&](int next) {
     if constexpr (NS == 2) {
       wait_vm_lgkm0<0>();
@@ -1120,13 +1138,13 @@ int launch_cfg(const gemm_args &a, int64_t batch, int splits, hipStream_t s) {
   return splits;  // >= 1: the number of K splits actually launched
 }
 
-template <int BT, int BK, int NWV, int NS, bool TA, bool TB>
+template <int BM, int BN, int BK, int NWV, int NS, bool TA, bool TB>
 int launch_dtl(const gemm_args &a, int64_t batch, int splits, hipStream_t s) {
-  using D = dtl_cfg<BT, BK, NWV, NS>;
-  auto kern = sgemm_dtl_k<BT, BK, NWV, NS, TA, TB>;
+  using D = dtl_cfg<BM, BN, BK, NWV, NS>;
+  auto kern = sgemm_dtl_k<BM, BN, BK, NWV, NS, TA, TB>;
   gemm_args g = a;
-  g.tiles_m = static_cast<int>(a.M / BT);
-  g.tiles_n = static_cast<int>(a.N / BT);
+  g.tiles_m = static_cast<int>(a.M / BM);
+  g.tiles_n = static_cast<int>(a.N / BN);
   g.klen = static_cast<int>(cdiv(cdiv(a.K, splits), BK) * BK);
   if (g.klen < BK) g.klen = BK;
   splits = static_cast<int>(a.K > 0 ? cdiv(a.K, g.klen) : 1);
@@ -1142,14 +1160,19 @@ int launch_tb(const gemm_args &a, int64_t batch, int splits, bool vec, hipStream
   // Every split's K range is a multiple of BK except possibly the last, and
   // that one is too when K is.
   const bool edge = (a.M % BM) || (a.N % BN) || (a.K % BK);
-  // Full square tiles of 16-byte aligned operands: LDS-direct loads.
-  if constexpr (BM == BN && (BM == 256 || BM == 128)) {
+  // Full tiles of 16-byte aligned operands: LDS-direct loads.
+  if constexpr ((BM == 256 && BN == 256) || (BM == 128 && BN == 128) ||
+                (BM == 128 && BN == 64)) {
     if (vec && a.M % BM == 0 && a.N % BN == 0 && a.K % kDtlBK == 0) {
       if constexpr (BM == 256) {
-        if (a.K % 32 == 0) return launch_dtl<BM, 32, 8, 2, TA, TB>(a, batch, splits, s);
-        return launch_dtl<BM, kDtlBK, 8, 4, TA, TB>(a, batch, splits, s);
-      } else
-        return launch_dtl<BM, kDtlBK, 4, 2, TA, TB>(a, batch, splits, s);
+        if (a.K % 32 == 0) return launch_dtl<BM, BN, 32, 8, 2, TA, TB>(a, batch, splits, s);
+        return launch_dtl<BM, BN, kDtlBK, 8, 4, TA, TB>(a, batch, splits, s);
+      } else if constexpr (BN == 128) {
+        return launch_dtl<BM, BN, kDtlBK, 4, 2, TA, TB>(a, batch, splits, s);
+      } else {
+        if (a.K % 32 == 0) return launch_dtl<BM, BN, 32, 4, 2, TA, TB>(a, batch, splits, s);
+        return launch_dtl<BM, BN, kDtlBK, 4, 2, TA, TB>(a, batch, splits, s);
+      }
     }
   }
   if (vec) {
@@ -1278,7 +1301,7 @@ plan small_m_tiles(int64_t M, int64_t N, int64_t K, int64_t batch) {
   return p;
 }
 
-plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch) {
+plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dtl_ok) {
   auto tiles = [&](int bm, int bn) { return cdiv(M, bm) * cdiv(N, bn) * batch; };
   // M <= 32: the small-M kernel (splits chosen at launch), or where it does
   // not apply (batched, A transposed) the 32x128 tile.
@@ -1301,10 +1324,14 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch) {
     int tile, bm, bn, bk, waves, occupancy;
     double eff;
   };
-  static const cand cands[] = {{TILE_256x256, 256, 256, 16, 8, 1, 0.87},
-                               {TILE_128x128, 128, 128, 16, 4, 3, 0.84},
-                               {TILE_128x64, 128, 64, 16, 4, 5, 0.75},
-                               {TILE_64x64, 64, 64, 16, 4, 8, 0.64}};
+  // The 128x64 tile runs the LDS-direct kernel when the operands allow it
+  // (fitted 0.82 of peak at three workgroups per CU on the 2048-row
+  // transformer and square shapes), the register-staged one otherwise.
+  const bool dtl64 = dtl_ok && M % 128 == 0 && N % 64 == 0;
+  const cand cands[] = {{TILE_256x256, 256, 256, 16, 8, 1, 0.87},
+                        {TILE_128x128, 128, 128, 16, 4, 3, 0.84},
+                        {TILE_128x64, 128, 64, 16, 4, dtl64 ? 3 : 5, dtl64 ? 0.82 : 0.75},
+                        {TILE_64x64, 64, 64, 16, 4, 8, 0.64}};
   constexpr double kK0 = 64.0, kSingleWave = 0.76, kReduceBw = 2.0e13, kLaunch = 4.0e-6;
   const double rate_cu = 157.3e12 / 256.0;
   plan best{TILE_128x128, 1};
@@ -1618,7 +1645,8 @@ int gemm_impl(const silgpu_gemm_desc &d, const plan *forced) {
                    (ta ? M % 4 == 0 : K % 4 == 0) && (tb ? K % 4 == 0 : N % 4 == 0) &&
                    (batch == 1 || (d.stride_a_inner % 4 == 0 && d.stride_b_inner % 4 == 0 &&
                                    d.stride_a_outer % 4 == 0 && d.stride_b_outer % 4 == 0));
-  return run_sgemm(a, batch, forced ? *forced : choose_plan(M, N, K, batch), ta, tb, vec, c);
+  return run_sgemm(a, batch, forced ? *forced : choose_plan(M, N, K, batch, vec && K % 16 == 0),
+                   ta, tb, vec, c);
 }
 
 silgpu_gemm_desc plain_desc(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,

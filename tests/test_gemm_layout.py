@@ -1,5 +1,5 @@
 """Host-side checks of the LDS-direct SGEMM layouts (silarray_amd/csrc/gemm.hip,
-sgemm_dtl_k, tiles of 256 and 128, K tiles of 16 and 32).
+sgemm_dtl_k, operand extents 256, 128 and 64, K tiles of 16 and 32).
 
 The index functions below restate dtl_src / dtl_window / dtl_elem / dtl_frag4,
 and the tests check the properties the kernel relies on: every element of a
@@ -27,8 +27,8 @@ No GPU."""
 
 import pytest
 
-PITCH = {256: 260, 128: 264}  # M/N-contiguous window pitch per tile width (floats)
-SHAPES = [(256, 16), (256, 32), (128, 16), (128, 32)]  # (tile, BK)
+PITCH = {256: 260, 128: 264, 64: 272}  # M/N-contiguous window pitch per tile extent (floats)
+SHAPES = [(256, 16), (256, 32), (128, 16), (128, 32), (64, 16), (64, 32)]  # (extent, BK)
 
 
 def windows(tile, bk):
@@ -48,8 +48,11 @@ def lane_chunks(kcontig, tile, w, lane):
         return [(16 * rg + rr, 16 * kh + 4 * kq + e) for e in range(4)]
     if tile == 256:
         return [(4 * lane + e, w) for e in range(4)]
-    p, c = lane // 32, lane % 32
-    return [(4 * c + e, 2 * w + p) for e in range(4)]
+    if tile == 128:
+        p, c = lane // 32, lane % 32
+        return [(4 * c + e, 2 * w + p) for e in range(4)]
+    p, c = lane // 16, lane % 16
+    return [(4 * c + e, 4 * w + p) for e in range(4)]
 
 
 def window_base(kcontig, tile, w):
@@ -63,7 +66,9 @@ def elem(kcontig, tile, x, k):
                 (4 * r + (((k % 16) // 4) ^ swz(r))) * 4 + k % 4)
     if tile == 256:
         return k * PITCH[256] + x
-    return (k // 2) * PITCH[128] + 128 * (k % 2) + x
+    if tile == 128:
+        return (k // 2) * PITCH[128] + 128 * (k % 2) + x
+    return (k // 4) * PITCH[64] + 64 * (k % 4) + x
 
 
 def operand_floats(tile, bk):

@@ -700,15 +700,15 @@ def test_gemm_desc_validation(native):
 
 
 @pytest.mark.parametrize("K,splits", [(80, 1), (96, 1), (96, 3), (80, 3)])
-@pytest.mark.parametrize("tile", [5, 1])
+@pytest.mark.parametrize("tile", [5, 1, 4])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_sgemm_lds_direct_batched(native, oracle, ta, tb, tile, K, splits):
-    """Full 256 x 256 (tile 5) and 128 x 128 (tile 1) tiles take the
-    LDS-direct kernel: batched, strided (padded leading dimensions), every
-    transpose, bias + relu epilogue.  The 256 tile runs K tiles of 32 when
-    K % 32 == 0 (K = 96) and of 16 otherwise (K = 80); splits = 3 adds the
-    split-K partial pass (K ranges 32 + 32 + 32 and 32 + 32 + 16; split K
-    runs unbatched)."""
+    """Full 256 x 256 (tile 5), 128 x 128 (tile 1) and 128 x 64 (tile 4)
+    tiles take the LDS-direct kernel: batched, strided (padded leading
+    dimensions), every transpose, bias + relu epilogue.  The 256 and 128 x 64
+    tiles run K tiles of 32 when K % 32 == 0 (K = 96) and of 16 otherwise
+    (K = 80); splits = 3 adds the split-K partial pass (K ranges 32 + 32 + 32
+    and 32 + 32 + 16; split K runs unbatched)."""
     announce(f"sgemm lds-direct batched tile={tile} ta={ta} tb={tb} K={K} splits={splits}")
     M, N, batch = 256, 512, (3 if splits == 1 else 1)
     g = rng(2300 + 2 * ta + tb)
