@@ -16,22 +16,24 @@
 // all resident) and each wavefront's running softmax covers half the keys;
 // the two halves of a row group are merged through LDS at the end
 // (m = max(m0, m1), l and O rescaled by exp(m_h - m)).  The block's K
-// (row-major, pitch D + 4) and V (transposed, Vt[d][key], pitch 68) are
+// (row-major, pitch D + 8) and V (transposed, Vt[d][key], pitch 72) are
 // staged in LDS; the next block's loads are issued before the current block
-// is multiplied.  Per block and wavefront:
-//   S (16 x 32) = Q_w K^T on v_mfma_f32_16x16x4f32, the head dim in groups
-//     of 16 whose k values go to the lane's k slot q as 16 g + 4 q + j at
-//     step j (any assignment of k to slots adds the same products), so Q
-//     sits in registers as float4 per group and K is read with one
-//     ds_read_b128 per 16-key block and group;
-//   online softmax: s = acc * scale (the unfused product's rounding),
-//     masked keys -inf, row max and sum over the 16 lanes that share a row
-//     (DPP row reductions), exponentials on v_exp_f32, running max m and
-//     sum l, O rescaled by exp(m - m');
-//   P goes to the wavefront's LDS rows, is read back in the A-operand
-//     layout and O (16 x D) += P V on MFMA, V read as ds_read_b128 from Vt.
+// is multiplied.  Both products are computed transposed on
+// v_mfma_f32_16x16x4f32, so that each lane owns one query row:
+//   S^T (32 keys x 16 rows) = K Q^T: the head dim in groups of 16 whose k
+//     values go to the lane's k slot q as 16 g + 4 q + j at step j (any
+//     assignment of k to slots adds the same products), so Q^T sits in
+//     registers as a float4 per group and K is read with one ds_read_b128
+//     per 16-key block and group; lane (c, q) then holds scores of row c at
+//     keys 16 jb + 4 q + r;
+//   online softmax per lane: row max and sum over its 8 registers and the
+//     lanes c + 16, c + 32, c + 48, running max m and sum l, O rescaled by
+//     one factor per lane;
+//   O^T (D x 16 rows) += V^T P^T: the exponentiated scores are already the
+//     B operand (key 16 jb + 4 q + j of row c at step j), so P never leaves
+//     registers; V^T is one ds_read_b128 from Vt per block and key group.
 // O is divided by l at the end and stored through the output strides (the
-// head-merged [B*S, H*D] layout included).
+// head-merged [B*S, H*D] layout included) as a float4 per lane and block.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -48,21 +50,23 @@ constexpr int kAttnThreads = kAttnWaves * kWave;
 constexpr int kBQ = 32;       // query rows per workgroup (two row groups of 16)
 constexpr int kBKey = 64;     // keys per block (two halves of 32)
 constexpr int kHalf = kBKey / 2;
-constexpr int kPadA = 4;      // LDS row padding (floats), keeps rows 16-byte aligned
+// LDS row pitches.  K and Vt are read with ds_read_b128 by lanes (c, q) at
+// row c, float 4 q: with the pitch a multiple of 8 floats but not of 16
+// ((pitch / 4) % 4 == 2), the 16 lanes of each b128 pass hit distinct
+// 16-byte bank groups.
+constexpr int kPadKV = 8;
 
 template <int D>
 struct attn_cfg {
   static_assert(D % 16 == 0 && D >= 16 && D <= 128, "head dim");
   static constexpr int kG = D / 16;                  // 16-deep groups of D = 16-column blocks of O
-  static constexpr int kKPitch = D + kPadA;          // Ks[key][d]
-  static constexpr int kVPitch = kBKey + kPadA;      // Vt[d][key]
-  static constexpr int kPPitch = kHalf + kPadA;      // Ps[row][key]
+  static constexpr int kKPitch = D + kPadKV;         // Ks[key][d]
+  static constexpr int kVPitch = kBKey + kPadKV;     // Vt[d][key]
   static constexpr int kKs = kBKey * kKPitch;
   static constexpr int kVt = D * kVPitch;
-  static constexpr int kPs = kAttnWaves * 16 * kPPitch;
-  static constexpr int kLdsBytes = (kKs + kVt + kPs) * 4;
-  // Merge of the key halves: per lane, O (D/4 floats), m and l (4 each).
-  static constexpr int kXfer = (D / 4 + 8) * kWave * 2;  // two row groups
+  static constexpr int kLdsBytes = (kKs + kVt) * 4;
+  // Merge of the key halves: per lane, O (D/4 floats), m and l.
+  static constexpr int kXfer = (D / 4 + 2) * kWave * 2;  // two row groups
   static_assert(kXfer <= kKs + kVt, "merge area");
   static constexpr int kLoads = kBKey * (D / 4) / kAttnThreads;  // float4 per thread per operand
   static_assert(kLoads * kAttnThreads * 4 == kBKey * D, "block load split");
@@ -121,7 +125,7 @@ template <int D>
 __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
   using C = attn_cfg<D>;
   extern __shared__ __attribute__((aligned(16))) float lds[];
-  float *Ks = lds, *Vt = lds + C::kKs, *Ps = lds + C::kKs + C::kVt;
+  float *Ks = lds, *Vt = lds + C::kKs;
   const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
   const int c = lane % 16, q = lane / 16;
   const int64_t zo = blockIdx.y / a.binner, zi = blockIdx.y % a.binner;
@@ -129,15 +133,16 @@ __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
   const float *__restrict__ K = a.K + zo * a.sk_o + zi * a.sk_i;
   const float *__restrict__ V = a.V + zo * a.sv_o + zi * a.sv_i;
   float *__restrict__ O = a.O + zo * a.so_o + zi * a.so_i;
-  const int rg = wave % 2, kh = wave / 2;            // row group, key half
-  const int row0 = blockIdx.x * kBQ + rg * 16;        // this wavefront's first query row
+  const int rg = wave % 2, kh = wave / 2;        // row group, key half
+  const int row0 = blockIdx.x * kBQ + rg * 16;    // this wavefront's first query row
+  const int row = row0 + c;                       // the query row of this lane
   const int Sq = a.Sq, Sk = a.Sk;
 
-  // Q fragments: lane (c, q) holds Q[row0 + c][16 g + 4 q .. + 3] for each
-  // group g (rows past Sq read row Sq - 1 and are never stored).
+  // Q fragments: lane (c, q) holds Q[row][16 g + 4 q .. + 3] for each group
+  // g (rows past Sq read row Sq - 1 and are never stored).
   float4 qf[C::kG];
   if (Sk > 0) {  // with no keys Q is not read (and may be null): O is 0
-    const float *qr = Q + int64_t(min(row0 + c, Sq - 1)) * a.ldq + 4 * q;
+    const float *qr = Q + int64_t(min(row, Sq - 1)) * a.ldq + 4 * q;
 #pragma unroll
     for (int g = 0; g < C::kG; ++g) qf[g] = ld4u(qr + 16 * g, a.vec);
   }
@@ -145,16 +150,31 @@ __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
   // Staging registers of one key block: thread t loads float4 f = t + 256 u
   // of K as (key f / (D/4), d4 f % (D/4)) and of V as (key f % 64,
   // d4 f / 64), so the transposed LDS writes of V are conflict-free.
+  // Per-thread source pointers at key 0, advanced by whole blocks.
   float4 kst[C::kLoads], vst[C::kLoads];
-  auto load_block = [&](int key0) {
+  const float *kp[C::kLoads], *vp[C::kLoads];
 #pragma unroll
-    for (int u = 0; u < C::kLoads; ++u) {
-      const int f = t + kAttnThreads * u;
-      const int kk = f / (D / 4), kd = f % (D / 4);
-      const int vk = f % kBKey, vd = f / kBKey;
-      const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-      kst[u] = key0 + kk < Sk ? ld4u(K + int64_t(key0 + kk) * a.ldk + 4 * kd, a.vec) : z;
-      vst[u] = key0 + vk < Sk ? ld4u(V + int64_t(key0 + vk) * a.ldv + 4 * vd, a.vec) : z;
+  for (int u = 0; u < C::kLoads; ++u) {
+    const int f = t + kAttnThreads * u;
+    kp[u] = K + int64_t(f / (D / 4)) * a.ldk + 4 * (f % (D / 4));
+    vp[u] = V + int64_t(f % kBKey) * a.ldv + 4 * (f / kBKey);
+  }
+  auto load_block = [&](int key0) {
+    const int64_t ko = int64_t(key0) * a.ldk, vo = int64_t(key0) * a.ldv;
+    if (key0 + kBKey <= Sk) {  // a full block: no masks
+#pragma unroll
+      for (int u = 0; u < C::kLoads; ++u) {
+        kst[u] = ld4u(kp[u] + ko, a.vec);
+        vst[u] = ld4u(vp[u] + vo, a.vec);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < C::kLoads; ++u) {
+        const int f = t + kAttnThreads * u;
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        kst[u] = key0 + f / (D / 4) < Sk ? ld4u(kp[u] + ko, a.vec) : z;
+        vst[u] = key0 + f % kBKey < Sk ? ld4u(vp[u] + vo, a.vec) : z;
+      }
     }
   };
   auto store_block = [&]() {
@@ -171,126 +191,126 @@ __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
     }
   };
 
+  // O^T accumulators: register r of block jd in lane (c, q) is
+  // O[row][16 jd + 4 q + r].  Running max m and sum l of this lane's row.
   floatx4 acc_o[C::kG];
 #pragma unroll
   for (int j = 0; j < C::kG; ++j) acc_o[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m[4], l[4];  // running max and sum of rows 4 q + i
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m[i] = -INFINITY;
-    l[i] = 0.0f;
-  }
-  float *Pw = Ps + wave * 16 * C::kPPitch;  // this wavefront's 16 rows of P
+  float m = -INFINITY, l = 0.0f;
 
   const int nblocks = (Sk + kBKey - 1) / kBKey;
   if (nblocks > 0) load_block(0);
   for (int kb = 0; kb < nblocks; ++kb) {
     const int key0 = kb * kBKey;
+    const bool full = key0 + kBKey <= Sk;
     __syncthreads();  // every wavefront is done reading the previous block
     store_block();
     __syncthreads();
     if (kb + 1 < nblocks) load_block(key0 + kBKey);  // lands while this block is multiplied
 
-    // S = Q_w K^T over this wavefront's half: two 16-key blocks.
-    const int kbase = kHalf * kh;  // first key of the half within the block
-    floatx4 s[2];
+    // S^T = K_half Q_w^T, two 16-key blocks: register r of block jb in lane
+    // (c, q) is S[row][key0 + kbase + 16 jb + 4 q + r].  The A operand is K
+    // (one ds_read_b128 per block and group), the B operand Q^T (qf).
+    const int kbase = kHalf * kh;
+    floatx4 st[2];
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) s[jb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int jb = 0; jb < 2; ++jb) st[jb] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int g = 0; g < C::kG; ++g)
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb) {
         const float4 kv = *reinterpret_cast<const float4 *>(
             Ks + (kbase + 16 * jb + c) * C::kKPitch + 16 * g + 4 * q);
-        s[jb] = mma4(s[jb], qf[g], kv);
+        st[jb] = mma4(st[jb], kv, qf[g]);
       }
 
-    // Online softmax over the half.  Register i of block jb in lane (c, q)
-    // is row 4 q + i, key key0 + kbase + 16 jb + c.
-    float alpha[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float rm = -INFINITY;
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        float v = s[jb][i] * a.scale;
-        if (key0 + kbase + 16 * jb + c >= Sk) v = -INFINITY;
-        s[jb][i] = v;
-        rm = fmaxf(rm, v);
-      }
-      rm = row16_max(rm);
-      const float mn = fmaxf(m[i], rm);
-      const bool none = mn == -INFINITY;  // no finite score in this row yet
-      alpha[i] = none ? 1.0f : exp_fast(m[i] - mn);
-      float rs = 0.0f;
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        const float p = none ? 0.0f : exp_fast(s[jb][i] - mn);
-        s[jb][i] = p;
-        rs += p;
-      }
-      rs = row16_sum(rs);
-      l[i] = l[i] * alpha[i] + rs;
-      m[i] = mn;
-    }
-#pragma unroll
-    for (int jd = 0; jd < C::kG; ++jd)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc_o[jd][i] *= alpha[i];
-
-    // P to this wavefront's LDS rows, then back in the A-operand layout
-    // (LDS accesses of one wavefront complete in order).
+    // Online softmax of this lane's row over the half: the row's 32 keys are
+    // the 8 registers here and in lanes c + 16, c + 32, c + 48.  Scores are
+    // acc * scale (the unfused product's rounding); e^(s - m) is taken as
+    // 2^((s - m) log2 e) on v_exp_f32 (relative error about |s - m| 2^-24).
+    float v[2][4];
+    float rm = -INFINITY;
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) Pw[(4 * q + i) * C::kPPitch + 16 * jb + c] = s[jb][i];
-
-    // O += P V over the half's two 16-key groups.
+      for (int r = 0; r < 4; ++r) {
+        float x = st[jb][r] * a.scale;
+        if (!full && key0 + kbase + 16 * jb + 4 * q + r >= Sk) x = -INFINITY;
+        v[jb][r] = x;
+        rm = fmaxf(rm, x);
+      }
+    rm = fmaxf(rm, __shfl_xor(rm, 16, kWave));
+    rm = fmaxf(rm, __shfl_xor(rm, 32, kWave));
+    const float mn = fmaxf(m, rm);
+    const bool none = mn == -INFINITY;  // no finite score in this row yet
+    const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f((m - mn) * 1.4426950408889634f);
+    float4 p[2];
+    float rs = 0.0f;
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const float4 pa = *reinterpret_cast<const float4 *>(Pw + c * C::kPPitch + 16 * g + 4 * q);
+    for (int jb = 0; jb < 2; ++jb) {
+      float e[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        e[r] = none ? 0.0f : __builtin_amdgcn_exp2f((v[jb][r] - mn) * 1.4426950408889634f);
+        rs += e[r];
+      }
+      p[jb] = make_float4(e[0], e[1], e[2], e[3]);
+    }
+    rs += __shfl_xor(rs, 16, kWave);
+    rs += __shfl_xor(rs, 32, kWave);
+    l = l * alpha + rs;
+    m = mn;
+#pragma unroll
+    for (int jd = 0; jd < C::kG; ++jd) acc_o[jd] *= alpha;
+
+    // O^T += V^T P^T: A operand V^T (ds_read_b128 from Vt), B operand P^T,
+    // which is p: register r of key block jb is key 16 jb + 4 q + r of this
+    // lane's row, the operand layout the MFMA asks for.
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
       for (int jd = 0; jd < C::kG; ++jd) {
         const float4 vb = *reinterpret_cast<const float4 *>(
-            Vt + (16 * jd + c) * C::kVPitch + kbase + 16 * g + 4 * q);
-        acc_o[jd] = mma4(acc_o[jd], pa, vb);
+            Vt + (16 * jd + c) * C::kVPitch + kbase + 16 * jb + 4 * q);
+        acc_o[jd] = mma4(acc_o[jd], vb, p[jb]);
       }
-    }
   }
 
   // Merge the key halves: the second half's wavefronts park (O, m, l) in
   // LDS (over the K/V stage), the first half's combine and store.  Lane
   // layouts of the two partners are identical.
   __syncthreads();  // every wavefront is done with the last K/V block
-  float *X = lds + rg * (D / 4 + 8) * kWave;  // this row group's merge slots
+  float *X = lds + rg * (D / 4 + 2) * kWave;  // this row group's merge slots
   if (kh == 1) {
 #pragma unroll
     for (int jd = 0; jd < C::kG; ++jd)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) X[(4 * jd + i) * kWave + lane] = acc_o[jd][i];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      X[(D / 4 + i) * kWave + lane] = m[i];
-      X[(D / 4 + 4 + i) * kWave + lane] = l[i];
-    }
+      for (int r = 0; r < 4; ++r) X[(4 * jd + r) * kWave + lane] = acc_o[jd][r];
+    X[(D / 4) * kWave + lane] = m;
+    X[(D / 4 + 1) * kWave + lane] = l;
   }
   __syncthreads();
-  if (kh == 1) return;
-  // O / l, register i of block jd in lane (c, q) = O[row0 + 4 q + i][16 jd + c].
+  if (kh == 1 || row >= Sq) return;
+  const float m1 = X[(D / 4) * kWave + lane], l1 = X[(D / 4 + 1) * kWave + lane];
+  const float mm = fmaxf(m, m1);
+  const float e0 = mm == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m - mm) * 1.4426950408889634f);
+  const float e1 = mm == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m1 - mm) * 1.4426950408889634f);
+  const float lt = l * e0 + l1 * e1;
+  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  float *orow = O + int64_t(row) * a.ldo + 4 * q;
+  const bool vst4 = (a.ldo & 3) == 0 && aligned16_dev(O);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float m1 = X[(D / 4 + i) * kWave + lane], l1 = X[(D / 4 + 4 + i) * kWave + lane];
-    const float mm = fmaxf(m[i], m1);
-    const float e0 = mm == -INFINITY ? 0.0f : expf(m[i] - mm);
-    const float e1 = mm == -INFINITY ? 0.0f : expf(m1 - mm);
-    const float lt = l[i] * e0 + l1 * e1;
-    const int row = row0 + 4 * q + i;
-    if (row >= Sq) continue;
-    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-    float *orow = O + int64_t(row) * a.ldo;
+  for (int jd = 0; jd < C::kG; ++jd) {
+    float o[4];
 #pragma unroll
-    for (int jd = 0; jd < C::kG; ++jd)
-      orow[16 * jd + c] = (acc_o[jd][i] * e0 + X[(4 * jd + i) * kWave + lane] * e1) * inv;
+    for (int r = 0; r < 4; ++r)
+      o[r] = (acc_o[jd][r] * e0 + X[(4 * jd + r) * kWave + lane] * e1) * inv;
+    if (vst4) {
+      *reinterpret_cast<float4 *>(orow + 16 * jd) = make_float4(o[0], o[1], o[2], o[3]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) orow[16 * jd + r] = o[r];
+    }
   }
 }
 
