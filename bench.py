@@ -11,11 +11,12 @@ steps with a device synchronisation on both sides.
 
 The other rows of the workload (GEMV, small-batch SGEMM, linear_sigmoid, row
 softmax / layer_norm / sum(axis=1), full sum/min/max/argmax, the 20-op affine
-chain, the 2048^3 and 4096^3 SGEMMs) are reported under "secondary" with
-their own roofline fractions, together with whole sil::eval graphs run
-through the C++ front end (the encoder block, the reference's transformer
-and MLP benchmarks, the affine chain at the API level).  Bandwidth rows rotate >= 1 GiB of buffers so
-the 256 MiB Infinity Cache cannot serve repeated reads.
+chain, the 2048^3 and 4096^3 SGEMMs, the reference's three conv2d layers)
+are reported under "secondary" with their own roofline fractions, together
+with whole sil::eval graphs run through the C++ front end (the encoder
+block, the reference's transformer and MLP benchmarks, the affine chain at
+the API level).  Bandwidth rows rotate >= 1 GiB of buffers so the 256 MiB
+Infinity Cache cannot serve repeated reads.
 
 cpu_baseline: cblas_sgemm from OpenBLAS (the x86 stand-in for the
 reference's Accelerate call, include/cpu.h:239-264) on the headline 8192^3
@@ -184,6 +185,29 @@ def bench_linear_sigmoid(nat, g, reps=50):
     ms = t.ms_per_launch(lambda i: nat.sgemm(0, 0, M, N, K, X, K, 0, W, N, 0, Y, N, 0, 1, b, N,
                                              nat.EPI_BIAS_SIGMOID), reps)
     return {"tflops": 2.0 * M * N * K / (ms / 1e3) / 1e12, "us": ms * 1e3}
+
+
+# The reference's conv2d benchmark layers (bench/micro/bench_nn_ops.cpp:193-195)
+# with its published sil-gpu times on the M1 Pro (bench/README.md:131-133).
+CONV_LAYERS = [("imagenet_first", 1, 224, 224, 3, 3, 32, 0.564),
+               ("resnet_mid", 16, 56, 56, 64, 3, 128, 2.89),
+               ("resnet_deep", 16, 28, 28, 128, 3, 256, 2.93)]
+
+
+def bench_conv2d(nat, g, reps=50):
+    """Implicit-GEMM conv2d (stride 1, same padding) on the reference's
+    layers; flops = 2 N H W C_out K K C_in."""
+    out = {}
+    for name, N, H, W, Ci, K, Co, ref_ms in CONV_LAYERS:
+        x = nat.DeviceBuffer.from_array(uniform(g, (N, H, W, Ci)))
+        w = nat.DeviceBuffer.from_array(uniform(g, (Co, K, K, Ci)))
+        y = nat.DeviceBuffer(N * H * W * Co * 4)
+        t = Timer(nat)
+        ms = t.ms_per_launch(lambda i: nat.conv2d(x, w, y, N, H, W, Ci, K, Co), reps)
+        flops = 2.0 * N * H * W * Co * K * K * Ci
+        out[f"conv2d_{name}_{N}x{Ci}x{H}x{W}_k{K}_co{Co}"] = {
+            "tflops": flops / (ms / 1e3) / 1e12, "us": ms * 1e3, "ref_ms": ref_ms}
+    return out
 
 
 def bench_rowops(nat, g, reps=20):
@@ -365,6 +389,12 @@ def main():
         secondary["linear_sigmoid_256x4096x4096"] = {
             "value": round(r["tflops"], 2), "unit": "TFLOP/s", "us": round(r["us"], 1),
             "roofline": roofline("mfma", r["tflops"], load_traffic("linear_sigmoid_256x4096x4096"))}
+    if want("conv2d"):
+        for k, v in bench_conv2d(nat, g).items():
+            log(f"{k} {v}")
+            secondary[k] = {"value": round(v["tflops"], 2), "unit": "TFLOP/s",
+                            "us": round(v["us"], 1), "reference_m1pro_ms": v["ref_ms"],
+                            "roofline": roofline("mfma", v["tflops"])}
     if want("rowops"):
         r = bench_rowops(nat, g)
         log(f"rowops {r}")

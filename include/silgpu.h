@@ -335,6 +335,18 @@ typedef struct silgpu_attn_desc {
 
 int silgpu_attention_f32(const silgpu_attn_desc *desc);
 
+/* 2-D convolution, stride 1, zero padding K/2 on every side (output H x W):
+ *   out[n][oh][ow][co] = sum_{kh, kw < K, ci < C_in}
+ *       in[n][oh + kh - K/2][ow + kw - K/2][ci] * w[co][kh][kw][ci]
+ * with NHWC input [N][H][W][C_in], OHWI weight [C_out][K][K][C_in] and NHWC
+ * output [N][H][W][C_out], all contiguous.  An implicit GEMM on the fp32
+ * matrix cores (M = N*H*W output pixels, N = C_out, K = K*K*C_in; no im2col
+ * buffer).  Replaces gpu::conv2d (include/gpu.h:815-833: conv2d_gemm,
+ * conv2d_gemm_smallch3, MPSGraph) as array::conv2d lowers to it
+ * (include/array.h:1508-1517, 2259-2273). */
+int silgpu_conv2d_f32(const float *d_in, const float *d_w, float *d_out, int64_t N, int64_t H,
+                      int64_t W, int64_t C_in, int64_t K, int64_t C_out);
+
 /* y[1 x N] = x[1 x K] * B[K x N] (B row-major, ldb >= N).  Replaces gpu::sgemv
  * (include/gpu.h:549-574).  silgpu_sgemm routes M == 1 here as well. */
 int silgpu_sgemv(const float *d_x, const float *d_B, int64_t ldb, float *d_y, int64_t N,

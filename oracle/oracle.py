@@ -240,3 +240,28 @@ def gemv_f32(x, B):
     y = np.empty(B.shape[1], np.float32)
     _lib.oracle_gemv_f32(_p(x), _p(B), B.shape[1], B.shape[0], _p(y))
     return y
+
+
+def conv2d_f64(x, w):
+    """2-D convolution in float64: NHWC x [N, H, W, C_in], OHWI w [C_out, K,
+    K, C_in], stride 1, zero padding K // 2, output [N, H, W, C_out] --
+    out[n, oh, ow, co] = sum over kh, kw, ci of x[n, oh + kh - K//2,
+    ow + kw - K//2, ci] * w[co, kh, kw, ci].  Follows the reference's
+    implicit-GEMM conv (include/gpu.h:1247-1257: pad = K / 2, H_out = H,
+    W_out = W; include/gpu_kernels.metal:1536-1545 and the (kh, kw, ci)
+    order of the K dimension), array::conv2d's shapes
+    (include/array.h:1508-1517, 2259-2273) and the OHWI weight the
+    reference's benchmark builds (bench/micro/bench_nn_ops.cpp:204-205)."""
+    x = np.asarray(x, np.float64)
+    w = np.asarray(w, np.float64)
+    N, H, W, Ci = x.shape
+    Co, K, K2, Ci2 = w.shape
+    assert K == K2 and Ci == Ci2
+    p = K // 2
+    xp = np.zeros((N, H + K - 1, W + K - 1, Ci))
+    xp[:, p:p + H, p:p + W, :] = x
+    out = np.zeros((N, H, W, Co))
+    for kh in range(K):
+        for kw in range(K):
+            out += xp[:, kh:kh + H, kw:kw + W, :] @ w[:, kh, kw, :].T
+    return out

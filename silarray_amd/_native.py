@@ -140,6 +140,7 @@ _SIGS = {
     "silgpu_gemm": (_i, [C.POINTER(GemmDesc)]),
     "silgpu_sgemv": (_i, [_vp, _vp, _i64, _vp, _i64, _i64]),
     "silgpu_attention_f32": (_i, [C.POINTER(AttnDesc)]),
+    "silgpu_conv2d_f32": (_i, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64]),
     "silgpu_event_create": (_i, [C.POINTER(_vp)]),
     "silgpu_event_destroy": (_i, [_vp]),
     "silgpu_event_record": (_i, [_vp]),
@@ -378,6 +379,11 @@ def attention(Sq, Sk, D, scale, Q, ldq, K, ldk, V, ldv, O, ldo, batch_outer=1, b
         setattr(d, f"stride_{name.lower()}_outer", st[0])
         setattr(d, f"stride_{name.lower()}_inner", st[1])
     call("silgpu_attention_f32", C.byref(d))
+
+
+def conv2d(x, w, out, N, H, W, C_in, K, C_out):
+    """silgpu_conv2d_f32: NHWC x, OHWI w, NHWC out; stride 1, padding K // 2."""
+    call("silgpu_conv2d_f32", vp(x), vp(w), vp(out), N, H, W, C_in, K, C_out)
 
 
 def sgemv(x, B, ldb, y, N, K):

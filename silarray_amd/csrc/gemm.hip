@@ -119,6 +119,11 @@ struct gemm_args {
   // ws[y][M][N] and splitk_sum_k applies the epilogue.
   int klen;
   float *ws;
+  // Implicit-GEMM convolution (sgemm_mfma_k<..., CONV>): A is the virtual
+  // im2col matrix of an NHWC input [batch][H][W][C_in], row m = output
+  // pixel (n, oh, ow), column k = (kh, kw, ci) with ci fastest, stride 1,
+  // zero padding `pad` on every side (output H x W).
+  int cv_h, cv_w, cv_cin, cv_k, cv_pad;
 };
 
 template <int BM, int BN, int BK, int WM, int WN, int MI>
@@ -200,7 +205,73 @@ __device__ __forceinline__ void store_groups(float *__restrict__ S, int t,
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int MI, bool TA, bool TB, bool VEC, bool EDGE>
+// The pixels of the A rows this thread loads (fixed over the K loop): base
+// of image n in the input, output row and column, or oh = -1 past M.
+template <int R, int Cc, int NT, int NG>
+__device__ __forceinline__ void conv_rows(const gemm_args &p, int row0, int t,
+                                          const float *(&img)[NG], int (&oh)[NG],
+                                          int (&ow)[NG]) {
+  constexpr int GPR = Cc / 4;
+  const int hw = p.cv_h * p.cv_w;
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    const int m = row0 + (t + i * NT) / GPR;
+    if (m < p.M) {
+      const int n = m / hw, rem = m - n * hw;
+      oh[i] = rem / p.cv_w;
+      ow[i] = rem - oh[i] * p.cv_w;
+      img[i] = p.A + int64_t(n) * hw * p.cv_cin;
+    } else {
+      oh[i] = -1;
+      ow[i] = 0;
+      img[i] = p.A;
+    }
+  }
+}
+
+// Gathers this thread's groups of the A tile [row0 .. row0 + R) x [k0 ..
+// k0 + Cc) from the input (4 k per group; zero outside the image, past M
+// and past K).  VEC: C_in % 4 == 0 and 16-byte aligned rows, so a group is
+// ci .. ci + 3 of one (kh, kw) and one float4 load.
+template <int R, int Cc, int NT, int NG, bool VEC>
+__device__ __forceinline__ void conv_gather(const gemm_args &p, int k0, int t,
+                                            const float *const (&img)[NG], const int (&oh)[NG],
+                                            const int (&ow)[NG], float (&g)[NG][4]) {
+  constexpr int GPR = Cc / 4;
+  const int cin = p.cv_cin, kk = p.cv_k, Kd = p.K;
+  auto elem = [&](int i, int k) -> float {
+    if (oh[i] < 0 || k >= Kd) return 0.0f;
+    const int khw = k / cin, ci = k - khw * cin;
+    const int kh = khw / kk, kw = khw - kh * kk;
+    const int ih = oh[i] + kh - p.cv_pad, iw = ow[i] + kw - p.cv_pad;
+    if (ih < 0 || ih >= p.cv_h || iw < 0 || iw >= p.cv_w) return 0.0f;
+    return img[i][(int64_t(ih) * p.cv_w + iw) * cin + ci];
+  };
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    const int k = k0 + ((t + i * NT) % GPR) * 4;
+    if constexpr (VEC) {
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (oh[i] >= 0 && k < Kd) {
+        const int khw = k / cin, ci = k - khw * cin;
+        const int kh = khw / kk, kw = khw - kh * kk;
+        const int ih = oh[i] + kh - p.cv_pad, iw = ow[i] + kw - p.cv_pad;
+        if (ih >= 0 && ih < p.cv_h && iw >= 0 && iw < p.cv_w)
+          v = *reinterpret_cast<const float4 *>(img[i] + (int64_t(ih) * p.cv_w + iw) * cin + ci);
+      }
+      g[i][0] = v.x;
+      g[i][1] = v.y;
+      g[i][2] = v.z;
+      g[i][3] = v.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) g[i][j] = elem(i, k + j);
+    }
+  }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int MI, bool TA, bool TB, bool VEC, bool EDGE,
+          bool CONV = false>
 __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
   using C = cfg<BM, BN, BK, WM, WN, MI>;
   using F = mfma<MI>;
@@ -232,10 +303,16 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
       for (int r = 0; r < F::R; ++r) acc[i][j][r] = 0.0f;
 
   float ga[C::NA][4], gb[C::NB][4];
+  // Convolution: the pixels of this thread's A rows, fixed over the K loop.
+  const float *cimg[CONV ? C::NA : 1];
+  int coh[CONV ? C::NA : 1], cow[CONV ? C::NA : 1];
+  if constexpr (CONV) conv_rows<BM, BK, NT, C::NA>(p, m0, t, cimg, coh, cow);
   // Global views: A non-trans is [M][K] (contiguous K), trans is [K][M].
   //               B non-trans is [K][N] (contiguous N), trans is [N][K].
   auto load_a = [&](int k0) {
-    if constexpr (!TA)
+    if constexpr (CONV)
+      conv_gather<BM, BK, NT, C::NA, VEC>(p, k0, t, cimg, coh, cow, ga);
+    else if constexpr (!TA)
       load_groups<BM, BK, NT, C::NA, VEC, EDGE>(A, p.lda, m0, k0, M, K, t, ga);
     else
       load_groups<BK, BM, NT, C::NA, VEC, EDGE>(A, p.lda, k0, m0, K, M, t, ga);
@@ -1481,6 +1558,31 @@ int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, boo
   return SILGPU_OK;
 }
 
+// Implicit-GEMM convolution on the register-staged MFMA kernel (CONV): the A
+// tile is gathered from the NHWC input, B is the OHWI weight read as a
+// [C_out][K*K*C_in] matrix (transposed B), C is the NHWC output.
+template <int BM, int BN, int WM, int WN, bool VEC>
+int launch_conv_cfg(const gemm_args &a, hipStream_t s) {
+  using C = cfg<BM, BN, 16, WM, WN, 16>;
+  auto kern = sgemm_mfma_k<BM, BN, 16, WM, WN, 16, false, true, VEC, true, true>;
+  static bool attr_done = false;
+  if (!attr_done) {
+    SILGPU_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         C::kLdsBytes));
+    attr_done = true;
+  }
+  gemm_args g = a;
+  g.tiles_m = static_cast<int>(cdiv(a.M, BM));
+  g.tiles_n = static_cast<int>(cdiv(a.N, BN));
+  g.klen = static_cast<int>(cdiv(a.K, 16) * 16);
+  if (g.klen < 16) g.klen = 16;
+  dim3 grid(static_cast<unsigned>(int64_t(g.tiles_m) * g.tiles_n), 1u, 1u);
+  kern<<<grid, C::kThreads, C::kLdsBytes, s>>>(g);
+  SILGPU_LAUNCH_CHECK("sgemm_mfma_k (conv2d)");
+  return SILGPU_OK;
+}
+
 int launch_gemv_n(const float *x, const float *Bm, int64_t ldb, float *y, int64_t N,
                   int64_t K, context *c) {
   const bool vec = N % 4 == 0 && ldb % 4 == 0 && aligned16(Bm);
@@ -1710,6 +1812,48 @@ int silgpu_sgemm_tuned(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K
 int silgpu_gemm(const silgpu_gemm_desc *desc) {
   SILGPU_REQUIRE(desc != nullptr, "silgpu_gemm: null descriptor");
   return gemm_impl(*desc, nullptr);
+}
+
+int silgpu_conv2d_f32(const float *d_in, const float *d_w, float *d_out, int64_t N, int64_t H,
+                      int64_t W, int64_t C_in, int64_t K, int64_t C_out) {
+  SILGPU_REQUIRE(N >= 0 && H >= 0 && W >= 0 && C_in >= 0 && C_out >= 0 && K >= 1,
+                 "silgpu_conv2d_f32: negative extent or kernel size < 1");
+  int64_t M = 0, Kd = 0;
+  SILGPU_REQUIRE(!__builtin_mul_overflow(N, H, &M) && !__builtin_mul_overflow(M, W, &M) &&
+                     !__builtin_mul_overflow(K, K, &Kd) &&
+                     !__builtin_mul_overflow(Kd, C_in, &Kd),
+                 "silgpu_conv2d_f32: extent product overflows int64");
+  if (M == 0 || C_out == 0) return SILGPU_OK;
+  SILGPU_REQUIRE(M <= INT32_MAX && Kd <= INT32_MAX && C_out <= INT32_MAX &&
+                     M * C_in <= INT64_MAX / 4,
+                 "silgpu_conv2d_f32: extent exceeds int32");
+  SILGPU_REQUIRE(d_out != nullptr, "silgpu_conv2d_f32: null output");
+  SILGPU_CTX(c);
+  if (Kd == 0) return silgpu_fill_u32(d_out, 0u, M * C_out);
+  SILGPU_REQUIRE(d_in && d_w, "silgpu_conv2d_f32: null pointer");
+  gemm_args a{};
+  a.A = d_in;
+  a.B = d_w;
+  a.C = d_out;
+  a.ldb = Kd;
+  a.ldc = C_out;
+  a.binner = 1;
+  a.M = static_cast<int>(M);
+  a.N = static_cast<int>(C_out);
+  a.K = static_cast<int>(Kd);
+  a.ep.bias_len = 1;
+  a.ep.epi = SILGPU_EPI_NONE;
+  a.cv_h = static_cast<int>(H);
+  a.cv_w = static_cast<int>(W);
+  a.cv_cin = static_cast<int>(C_in);
+  a.cv_k = static_cast<int>(K);
+  a.cv_pad = static_cast<int>(K / 2);
+  const bool vec = C_in % 4 == 0 && aligned16(d_in) && aligned16(d_w);
+  if (C_out <= 32)
+    return vec ? launch_conv_cfg<64, 64, 2, 2, true>(a, c->stream)
+               : launch_conv_cfg<64, 64, 2, 2, false>(a, c->stream);
+  return vec ? launch_conv_cfg<128, 64, 2, 2, true>(a, c->stream)
+             : launch_conv_cfg<128, 64, 2, 2, false>(a, c->stream);
 }
 
 }  // extern "C"

@@ -93,7 +93,7 @@ enum class op : uint8_t {
   sigmoid, relu, copy,               // unary elementwise (copy: identity)
   sigmoid_backward,                  // elementwise (x, dout)
   softmax, layer_norm,               // row ops
-  dot, batched_dot, linear, linear_sigmoid,
+  dot, batched_dot, linear, linear_sigmoid, conv2d,
   sum_axis,
   view,                              // zero-copy strided view of inputs[0]
 };
@@ -112,6 +112,7 @@ struct node {
   bool evaluated = false;
 
   float eps = 0.0f;   // layer_norm
+  size_t ksize = 0;   // conv2d kernel size
   size_t axis = 0;    // sum_axis
   size_t view_off = 0;  // view: element offset into inputs[0]'s contiguous result
   int epilogue = 0;     // linear: epilogue fused by the lowering (relu)
@@ -581,9 +582,9 @@ class array {
   array<float> relu() const;
   array<float> layer_norm(const array<float> &gamma, const array<float> &beta,
                           float eps = 1e-5f) const;
-  array<float> conv2d(const array<float> &, size_t) const {
-    throw std::runtime_error("array: conv2d is not part of this build.");
-  }
+  // NHWC input [N, H, W, C_in] with an OHWI weight [C_out, K, K, C_in]:
+  // [N, H, W, C_out], stride 1, zero padding K / 2 (include/array.h:1508-1517).
+  array<float> conv2d(const array<float> &weight, size_t kernel_size) const;
 
   //----------------------------------------------------------------------------
 
@@ -1162,6 +1163,23 @@ inline array<float> array<T>::relu() const {
     return from_node_(detail::node::make(detail::op::relu, {to_node_(*this)}, shape_));
   else
     return clone<float>().relu();
+}
+
+template <value_type T>
+inline array<float> array<T>::conv2d(const array<float> &weight, size_t kernel_size) const {
+  if (dimension() != 4 || weight.dimension() != 4)
+    throw std::runtime_error("array: conv2d requires a 4D NHWC input and a 4D OHWI weight.");
+  const auto &ws = weight.shape();
+  if (ws[1] != kernel_size || ws[2] != kernel_size || ws[3] != shape_[3] || kernel_size == 0)
+    throw std::runtime_error("array: conv2d weight shape does not match the input.");
+  if constexpr (std::is_same_v<T, float>) {
+    auto n = detail::node::make(detail::op::conv2d, {to_node_(*this), to_node_(weight)},
+                                shape_type{shape_[0], shape_[1], shape_[2], ws[0]});
+    n->ksize = kernel_size;
+    return from_node_(std::move(n));
+  } else {
+    return clone<float>().conv2d(weight, kernel_size);
+  }
 }
 
 template <value_type T>
@@ -1903,6 +1921,16 @@ inline void eval_node_nonfused(node *n) {
       auto out = new_output(n->shape);
       const size_t rows = n->shape.size() == 2 ? n->shape[0] : 1;
       gpu::softmax(a.storage_ref(), out, uint32_t(rows), uint32_t(n->shape.back()));
+      finish(n, std::move(out));
+      return;
+    }
+    case op::conv2d: {
+      auto x = contiguous(n->inputs[0].get());
+      auto w = contiguous(n->inputs[1].get());
+      const auto &xs = n->inputs[0]->shape;
+      auto out = new_output(n->shape);
+      gpu::conv2d(x.storage_ref(), w.storage_ref(), out, uint32_t(xs[0]), uint32_t(xs[1]),
+                  uint32_t(xs[2]), uint32_t(xs[3]), uint32_t(n->ksize), uint32_t(n->shape[3]));
       finish(n, std::move(out));
       return;
     }

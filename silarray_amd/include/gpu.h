@@ -241,10 +241,13 @@ class gpu {
     launched_(silgpu_program_f32(&p, OUT.dev_out<float>()), "program");
   }
 
-  // ---- not part of this build ---------------------------------------------
-  static void conv2d(const storage &, const storage &, storage &, size_t, size_t, size_t,
-                     size_t, size_t, size_t) {
-    throw std::runtime_error("gpu: conv2d is not part of this build");
+  // NHWC input, OHWI weight, NHWC output; stride 1, padding K / 2
+  // (include/gpu.h:815-833 of the reference).
+  static void conv2d(const storage &input, const storage &weight, storage &output, uint32_t N,
+                     uint32_t H, uint32_t W, uint32_t C_in, uint32_t K, uint32_t C_out) {
+    launched_(silgpu_conv2d_f32(input.dev_in<float>(), weight.dev_in<float>(),
+                                output.dev_out<float>(), N, H, W, C_in, K, C_out),
+              "conv2d");
   }
 
   static void launched_(int rc, const char *what) {

@@ -588,6 +588,31 @@ TEST_CASE("attention graph runs as one fused launch, matching the unfused graph"
   CHECK(worst <= 1e-5f);  // v in [0, 1): outputs are convex combinations of v rows
 }
 
+TEST_CASE("conv2d: same padding closed form and the 1x1 kernel as a product") {
+  // ones in and ones weights: C_in times the taps inside the image
+  auto x = ones<float>({1, 3, 3, 2});
+  auto w = ones<float>({1, 3, 3, 2});
+  auto y = x.conv2d(w, 3);
+  CHECK(y.shape() == (shape_type{1, 3, 3, 1}));
+  const float want[9] = {8, 12, 8, 12, 18, 12, 8, 12, 8};
+  bool ok = true;
+  for (size_t i = 0; i < 9; i++) ok = ok && y.at(i) == want[i];
+  CHECK(ok);
+  // a 1x1 kernel is the pixels times the weight's transpose
+  auto img = random({2, 5, 7, 12}) - 0.5f;
+  auto k1 = random({9, 1, 1, 12}) - 0.5f;
+  auto conv = img.conv2d(k1, 1);
+  auto prod = img.view({70, 12}).dot(k1.view({9, 12}).transpose());
+  eval(conv, prod);
+  CHECK(conv.shape() == (shape_type{2, 5, 7, 9}));
+  float worst = 0.0f;
+  for (size_t i = 0; i < 70 * 9; i++) worst = std::max(worst, std::abs(conv.at(i) - prod.at(i)));
+  CHECK(worst <= 1e-5f);
+  CHECK_THROWS_WITH(img.conv2d(k1, 3), "array: conv2d weight shape does not match the input.");
+  CHECK_THROWS_WITH(img.view({70, 12}).conv2d(k1, 1),
+                    "array: conv2d requires a 4D NHWC input and a 4D OHWI weight.");
+}
+
 HOST_CASE("view, permute and select on evaluated arrays") {
   auto m = array<int>({2, 3, 4}, iota_n(24));
   auto p = m.permute({2, 0, 1});

@@ -98,6 +98,18 @@ def test_attention_validation(lib):
     assert lib.raw("silgpu_attention_f32")(C.byref(d)) == 0
 
 
+def test_conv2d_validation(lib):
+    f = lib.raw("silgpu_conv2d_f32")
+    assert f(None, None, None, 1, 4, 4, 3, 0, 8) == lib.ERR_INVALID
+    assert "kernel size" in lib.last_error()
+    assert f(None, None, None, 1, -4, 4, 3, 3, 8) == lib.ERR_INVALID
+    assert f(None, None, None, 1 << 40, 1 << 40, 4, 3, 3, 8) == lib.ERR_INVALID
+    assert "overflows" in lib.last_error()
+    assert f(None, None, None, 1 << 20, 1 << 12, 1, 3, 3, 8) == lib.ERR_INVALID
+    assert "int32" in lib.last_error()
+    assert f(None, None, None, 0, 4, 4, 3, 3, 8) == 0  # no output pixels: no-op
+
+
 def test_program_validation(lib):
     p = lib.make_program((4,), [(16, (1,))], [(lib.PI_LOAD, 0, 3, 0, 0.0, 0.0)])
     rc = lib.raw("silgpu_program_f32")(C.byref(p), C.c_void_p(16))

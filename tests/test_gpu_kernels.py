@@ -800,3 +800,54 @@ def test_attention_no_keys_gives_zero(native):
     native.attention(16, 0, 32, 1.0, None, 32, None, 32, None, 32, dO, 32, 1, 2, (0, 0),
                      (0, 0), (0, 0), (0, 16 * 32))
     assert np.all(down(native, dO, ob.shape) == 0)
+
+
+# ---- conv2d (implicit GEMM) ---------------------------------------------------------
+
+# N, H, W, C_in, K, C_out: scalar gathers (C_in % 4 != 0), float4 gathers,
+# even and 1x1 kernels, ragged tiles on both GEMM axes, both tile shapes
+# (C_out <= 32 and above) and the reference benchmark's three layers
+# (bench/micro/bench_nn_ops.cpp:193-195) at full size.
+CONV_CASES = [(1, 8, 8, 3, 3, 16), (2, 7, 9, 16, 3, 32), (1, 5, 6, 4, 1, 5), (1, 6, 6, 8, 5, 12),
+              (2, 9, 5, 6, 2, 40), (3, 4, 4, 1, 3, 1), (1, 13, 11, 20, 3, 70), (1, 3, 3, 2, 7, 3),
+              (1, 224, 224, 3, 3, 32), (16, 56, 56, 64, 3, 128), (16, 28, 28, 128, 3, 256)]
+
+
+@pytest.mark.parametrize("N,H,W,Ci,K,Co", CONV_CASES)
+def test_conv2d(native, oracle, N, H, W, Ci, K, Co):
+    """silgpu_conv2d_f32 against the float64 restatement, GEMM bar with the
+    reduction length K*K*C_in: normwise and per element against the
+    convolution of |x| with |w|."""
+    announce(f"conv2d N={N} H={H} W={W} C_in={Ci} K={K} C_out={Co}")
+    g = rng(1900 + H * Ci + K)
+    x = g.normal(0, 1, (N, H, W, Ci)).astype(np.float32)
+    w = g.normal(0, 1, (Co, K, K, Ci)).astype(np.float32)
+    dx, dw, do = up(native, x), up(native, w), empty(native, N * H * W * Co)
+    native.conv2d(dx, dw, do, N, H, W, Ci, K, Co)
+    out = down(native, do, (N * H * W, Co))
+    ref = oracle.conv2d_f64(x, w).reshape(-1, Co)
+    refabs = oracle.conv2d_f64(np.abs(x), np.abs(w)).reshape(-1, Co)
+    ok, nw, el = gemm_tolerance_ok(out, ref, refabs, K * K * Ci)
+    assert ok, (nw, el)
+
+
+def test_conv2d_ones_closed_form(native):
+    """Ones in, ones weights: each output is C_in times the taps that fall
+    inside the image (corner, edge and interior counts of a 3x3 kernel)."""
+    announce("conv2d ones")
+    N, H, W, Ci, K, Co = 2, 6, 5, 16, 3, 8
+    do = empty(native, N * H * W * Co)
+    native.conv2d(up(native, np.ones((N, H, W, Ci), np.float32)),
+                  up(native, np.ones((Co, K, K, Ci), np.float32)), do, N, H, W, Ci, K, Co)
+    out = down(native, do, (N, H, W, Co))
+    rows = np.array([2] + [3] * (H - 2) + [2])
+    cols = np.array([2] + [3] * (W - 2) + [2])
+    ref = (Ci * rows[:, None] * cols[None, :]).astype(np.float32)
+    assert np.array_equal(out, np.broadcast_to(ref[None, :, :, None], out.shape))
+
+
+def test_conv2d_empty_reduction_writes_zeros(native):
+    announce("conv2d C_in=0")
+    do = up(native, np.full(2 * 3 * 3 * 4, np.nan, np.float32))
+    native.conv2d(None, None, do, 2, 3, 3, 0, 3, 4)
+    assert np.all(down(native, do, 72) == 0)

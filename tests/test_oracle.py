@@ -321,3 +321,63 @@ def test_layer_norm_vs_numpy_and_invariants(oracle):
     np.testing.assert_allclose(unit.var(1), (var / (var + 1e-5)).ravel(), rtol=1e-10)
     r = oracle.layer_norm_ref(x, gamma, beta)
     assert np.max(np.abs(r - f64)) / np.max(np.abs(f64)) < 1e-5
+
+
+# ---- conv2d -------------------------------------------------------------------------
+
+def _conv2d_loops(x, w):
+    """Six nested loops straight from the definition (tiny inputs only)."""
+    N, H, W, Ci = x.shape
+    Co, K, _, _ = w.shape
+    p = K // 2
+    out = np.zeros((N, H, W, Co))
+    for n in range(N):
+        for oh in range(H):
+            for ow in range(W):
+                for co in range(Co):
+                    acc = 0.0
+                    for kh in range(K):
+                        for kw in range(K):
+                            ih, iw = oh + kh - p, ow + kw - p
+                            if 0 <= ih < H and 0 <= iw < W:
+                                for ci in range(Ci):
+                                    acc += float(x[n, ih, iw, ci]) * float(w[co, kh, kw, ci])
+                    out[n, oh, ow, co] = acc
+    return out
+
+
+@pytest.mark.parametrize("shape", [(1, 4, 5, 3, 3, 2), (2, 3, 3, 2, 1, 3), (1, 5, 4, 2, 2, 2),
+                                   (1, 6, 6, 1, 5, 1)])
+def test_conv2d_oracle_matches_loops(oracle, shape):
+    N, H, W, Ci, K, Co = shape
+    g = np.random.default_rng(77)
+    x = g.normal(size=(N, H, W, Ci))
+    w = g.normal(size=(Co, K, K, Ci))
+    assert np.allclose(oracle.conv2d_f64(x, w), _conv2d_loops(x, w), rtol=1e-12, atol=1e-12)
+
+
+def test_conv2d_oracle_closed_forms(oracle):
+    # ones input and weights: C_in times the number of taps inside the image
+    x = np.ones((1, 3, 3, 2))
+    w = np.ones((1, 3, 3, 2))
+    out = oracle.conv2d_f64(x, w)[0, :, :, 0]
+    assert np.array_equal(out, [[8, 12, 8], [12, 18, 12], [8, 12, 8]])
+    # a 1x1 kernel is the product of the pixels with the weight's transpose
+    g = np.random.default_rng(3)
+    x = g.normal(size=(2, 4, 5, 6))
+    w = g.normal(size=(7, 1, 1, 6))
+    ref = (x.reshape(-1, 6) @ w.reshape(7, 6).T).reshape(2, 4, 5, 7)
+    assert np.allclose(oracle.conv2d_f64(x, w), ref, rtol=1e-12)
+
+
+def test_conv2d_oracle_single_channel_is_correlation(oracle):
+    """One channel in and out with an odd kernel: scipy's 2-D correlation
+    with zero fill and output the size of the input."""
+    from scipy.signal import correlate2d
+    g = np.random.default_rng(5)
+    for K in (1, 3, 5):
+        x = g.normal(size=(9, 7))
+        w = g.normal(size=(K, K))
+        ref = correlate2d(x, w, mode="same", boundary="fill", fillvalue=0)
+        out = oracle.conv2d_f64(x[None, :, :, None], w[None, :, :, None])[0, :, :, 0]
+        assert np.allclose(out, ref, rtol=1e-12, atol=1e-12), K
