@@ -27,7 +27,7 @@ LIB = PKG / "libsilgpu.so"
 INCLUDE = ROOT / "include"
 
 HIP_SOURCES = ["runtime.hip", "elementwise.hip", "reduce.hip", "rowops.hip", "gemm.hip",
-               "attention.hip"]
+               "attention.hip", "conv.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

@@ -205,70 +205,88 @@ __device__ __forceinline__ void store_groups(float *__restrict__ S, int t,
   }
 }
 
-// The pixels of the A rows this thread loads (fixed over the K loop): base
-// of image n in the input, output row and column, or oh = -1 past M.
-template <int R, int Cc, int NT, int NG>
-__device__ __forceinline__ void conv_rows(const gemm_args &p, int row0, int t,
-                                          const float *(&img)[NG], int (&oh)[NG],
-                                          int (&ow)[NG]) {
-  constexpr int GPR = Cc / 4;
-  const int hw = p.cv_h * p.cv_w;
+// Implicit-GEMM gather of the A tile of a convolution: row m is output
+// pixel (n, oh, ow), column k = (kh * K + kw) * C_in + ci is a tap and a
+// channel, and A[m][k] = in[n][oh + kh - pad][ow + kw - pad][ci] (zero
+// outside the image, past M and past K).  Each thread owns NG groups of 4
+// consecutive k of the tile; a walk keeps every group's (kh, kw, ci) and
+// steps it by the tile depth Cc per call, so the K loop divides nothing.
+// NE: 1 when C_in % 4 == 0 (a group is ci .. ci + 3 of one tap, one
+// float4 load), else 4 (one position per element).
+template <int R, int Cc, int NT, int NG, bool VEC>
+struct conv_walk {
+  static constexpr int NE = VEC ? 1 : 4;
+  int64_t base[NG];  // element offset of (n, oh - pad, ow - pad, 0)
+  int oh[NG], ow[NG];  // oh = -1 past M
+  int k[NG];           // reduction index of the group's first element
+  int ci[NG][NE], kw[NG][NE], kh[NG][NE];
+
+  __device__ __forceinline__ void init(const gemm_args &p, int row0, int k0, int t) {
+    constexpr int GPR = Cc / 4;
+    const int hw = p.cv_h * p.cv_w, cin = p.cv_cin;
 #pragma unroll
-  for (int i = 0; i < NG; ++i) {
-    const int m = row0 + (t + i * NT) / GPR;
-    if (m < p.M) {
-      const int n = m / hw, rem = m - n * hw;
-      oh[i] = rem / p.cv_w;
-      ow[i] = rem - oh[i] * p.cv_w;
-      img[i] = p.A + int64_t(n) * hw * p.cv_cin;
-    } else {
+    for (int i = 0; i < NG; ++i) {
+      const int m = row0 + (t + i * NT) / GPR;
       oh[i] = -1;
       ow[i] = 0;
-      img[i] = p.A;
-    }
-  }
-}
-
-// Gathers this thread's groups of the A tile [row0 .. row0 + R) x [k0 ..
-// k0 + Cc) from the input (4 k per group; zero outside the image, past M
-// and past K).  VEC: C_in % 4 == 0 and 16-byte aligned rows, so a group is
-// ci .. ci + 3 of one (kh, kw) and one float4 load.
-template <int R, int Cc, int NT, int NG, bool VEC>
-__device__ __forceinline__ void conv_gather(const gemm_args &p, int k0, int t,
-                                            const float *const (&img)[NG], const int (&oh)[NG],
-                                            const int (&ow)[NG], float (&g)[NG][4]) {
-  constexpr int GPR = Cc / 4;
-  const int cin = p.cv_cin, kk = p.cv_k, Kd = p.K;
-  auto elem = [&](int i, int k) -> float {
-    if (oh[i] < 0 || k >= Kd) return 0.0f;
-    const int khw = k / cin, ci = k - khw * cin;
-    const int kh = khw / kk, kw = khw - kh * kk;
-    const int ih = oh[i] + kh - p.cv_pad, iw = ow[i] + kw - p.cv_pad;
-    if (ih < 0 || ih >= p.cv_h || iw < 0 || iw >= p.cv_w) return 0.0f;
-    return img[i][(int64_t(ih) * p.cv_w + iw) * cin + ci];
-  };
-#pragma unroll
-  for (int i = 0; i < NG; ++i) {
-    const int k = k0 + ((t + i * NT) % GPR) * 4;
-    if constexpr (VEC) {
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (oh[i] >= 0 && k < Kd) {
-        const int khw = k / cin, ci = k - khw * cin;
-        const int kh = khw / kk, kw = khw - kh * kk;
-        const int ih = oh[i] + kh - p.cv_pad, iw = ow[i] + kw - p.cv_pad;
-        if (ih >= 0 && ih < p.cv_h && iw >= 0 && iw < p.cv_w)
-          v = *reinterpret_cast<const float4 *>(img[i] + (int64_t(ih) * p.cv_w + iw) * cin + ci);
+      base[i] = 0;
+      if (m < p.M) {
+        const int n = m / hw, rem = m - n * hw;
+        oh[i] = rem / p.cv_w;
+        ow[i] = rem - oh[i] * p.cv_w;
+        base[i] = ((int64_t(n) * p.cv_h + oh[i] - p.cv_pad) * p.cv_w + ow[i] - p.cv_pad) * cin;
       }
-      g[i][0] = v.x;
-      g[i][1] = v.y;
-      g[i][2] = v.z;
-      g[i][3] = v.w;
-    } else {
+      k[i] = k0 + ((t + i * NT) % GPR) * 4;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) g[i][j] = elem(i, k + j);
+      for (int e = 0; e < NE; ++e) {
+        const int ke = k[i] + e, khw = ke / cin;
+        ci[i][e] = ke - khw * cin;
+        kh[i][e] = khw / p.cv_k;
+        kw[i][e] = khw - kh[i][e] * p.cv_k;
+      }
     }
   }
-}
+
+  // The groups at the current k, then one step of Cc.
+  __device__ __forceinline__ void gather(const gemm_args &p, const float *A, float (&g)[NG][4]) {
+    const int cin = p.cv_cin, kk = p.cv_k, Kd = p.K;
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      if constexpr (VEC) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        const int ih = oh[i] + kh[i][0] - p.cv_pad, iw = ow[i] + kw[i][0] - p.cv_pad;
+        if (oh[i] >= 0 && k[i] < Kd && ih >= 0 && ih < p.cv_h && iw >= 0 && iw < p.cv_w)
+          v = *reinterpret_cast<const float4 *>(
+              A + base[i] + (kh[i][0] * p.cv_w + kw[i][0]) * cin + ci[i][0]);
+        g[i][0] = v.x;
+        g[i][1] = v.y;
+        g[i][2] = v.z;
+        g[i][3] = v.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int ih = oh[i] + kh[i][e] - p.cv_pad, iw = ow[i] + kw[i][e] - p.cv_pad;
+          g[i][e] = oh[i] >= 0 && k[i] + e < Kd && ih >= 0 && ih < p.cv_h && iw >= 0 &&
+                            iw < p.cv_w
+                        ? A[base[i] + (kh[i][e] * p.cv_w + kw[i][e]) * cin + ci[i][e]]
+                        : 0.0f;
+        }
+      }
+      k[i] += Cc;
+#pragma unroll
+      for (int e = 0; e < NE; ++e) {
+        ci[i][e] += Cc;
+        while (ci[i][e] >= cin) {
+          ci[i][e] -= cin;
+          if (++kw[i][e] == kk) {
+            kw[i][e] = 0;
+            ++kh[i][e];
+          }
+        }
+      }
+    }
+  }
+};
 
 template <int BM, int BN, int BK, int WM, int WN, int MI, bool TA, bool TB, bool VEC, bool EDGE,
           bool CONV = false>
@@ -304,14 +322,15 @@ __global__ __launch_bounds__(WM *WN *kWave) void sgemm_mfma_k(gemm_args p) {
 
   float ga[C::NA][4], gb[C::NB][4];
   // Convolution: the pixels of this thread's A rows, fixed over the K loop.
-  const float *cimg[CONV ? C::NA : 1];
-  int coh[CONV ? C::NA : 1], cow[CONV ? C::NA : 1];
-  if constexpr (CONV) conv_rows<BM, BK, NT, C::NA>(p, m0, t, cimg, coh, cow);
+  // Convolution: the walk of this thread's A groups through the taps.  The
+  // loads below ask for k = kbeg, kbeg + BK, ... in order, one call each.
+  conv_walk<BM, BK, NT, CONV ? C::NA : 1, VEC> cw;
+  if constexpr (CONV) cw.init(p, m0, blockIdx.y * p.klen, t);
   // Global views: A non-trans is [M][K] (contiguous K), trans is [K][M].
   //               B non-trans is [K][N] (contiguous N), trans is [N][K].
   auto load_a = [&](int k0) {
     if constexpr (CONV)
-      conv_gather<BM, BK, NT, C::NA, VEC>(p, k0, t, cimg, coh, cow, ga);
+      cw.gather(p, A, ga);
     else if constexpr (!TA)
       load_groups<BM, BK, NT, C::NA, VEC, EDGE>(A, p.lda, m0, k0, M, K, t, ga);
     else
@@ -750,7 +769,11 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
 }
 
-template <int BM, int BN, int BK, int NWV, int NS, bool TA, bool TB>
+// Sixteen bytes of zeros in device memory: the source of the LDS-direct
+// loads of convolution taps that fall into the padding.  Never written.
+__device__ __attribute__((aligned(16))) float conv_zero_page[4];
+
+template <int BM, int BN, int BK, int NWV, int NS, bool TA, bool TB, bool CONV = false>
 __global__ __launch_bounds__((dtl_cfg<BM, BN, BK, NWV, NS>::kThreads))
 __attribute__((amdgpu_waves_per_eu(dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU,
                                    dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU))) void sgemm_dtl_k(gemm_args p) {
@@ -784,18 +807,66 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU,
   // This wave loads windows wave + q*NW (q < WPA, WPB) of each operand.
   const float *a_src[WPA], *b_src[WPB];
 #pragma unroll
-  for (int q = 0; q < WPA; ++q) a_src[q] = dtl_src<AK, BM>(A, p.lda, m0, wave + q * NW, lane);
+  for (int q = 0; q < WPA; ++q)
+    a_src[q] = CONV ? A : dtl_src<AK, BM>(A, p.lda, m0, wave + q * NW, lane);
 #pragma unroll
   for (int q = 0; q < WPB; ++q) b_src[q] = dtl_src<BKc, BN>(B, p.ldb, n0, wave + q * NW, lane);
   // Advance of one K tile for each operand.
   const int64_t a_step = AK ? BK : int64_t(BK) * p.lda;
   const int64_t b_step = BKc ? BK : int64_t(BK) * p.ldb;
   constexpr int kBOff = D::kOperandA;
+  // Convolution (CONV: A is the implicit im2col matrix of an NHWC input,
+  // k = (kh * K + kw) * C_in + ci, C_in % BK == 0).  Every K tile then lies
+  // in one tap (kh, kw), the same for the whole workgroup, and a lane's
+  // channel offset within the tile is fixed: a window lane reads 4
+  // channels of its pixel shifted by the tap, or the zero page where the
+  // shifted pixel is padding.  issue() is called once per K tile, in order,
+  // and steps the tap walk (tci, tkw, tkh) by BK.
+  int64_t cv_base[CONV ? WPA : 1];
+  int cv_oh[CONV ? WPA : 1], cv_ow[CONV ? WPA : 1], cv_off[CONV ? WPA : 1];
+  int tci = 0, tkw = 0, tkh = 0;
+  if constexpr (CONV) {
+    const int hw = p.cv_h * p.cv_w;
+#pragma unroll
+    for (int q = 0; q < WPA; ++q) {
+      const int w = wave + q * NW, rr = lane / 4, kq = (lane % 4) ^ ((rr / 2) & 3);
+      const int m = m0 + 16 * (w % (BM / 16)) + rr;  // < M: full tiles only
+      const int n = m / hw, rem = m - n * hw;
+      cv_oh[q] = rem / p.cv_w;
+      cv_ow[q] = rem - cv_oh[q] * p.cv_w;
+      cv_base[q] =
+          ((int64_t(n) * p.cv_h + cv_oh[q] - p.cv_pad) * p.cv_w + cv_ow[q] - p.cv_pad) * p.cv_cin;
+      cv_off[q] = 16 * (w / (BM / 16)) + 4 * kq;
+    }
+    const int khw = kbeg / p.cv_cin;
+    tci = kbeg - khw * p.cv_cin;
+    tkh = khw / p.cv_k;
+    tkw = khw - tkh * p.cv_k;
+  }
   auto issue = [&](int kt, float *S) {
     const int64_t k = int64_t(kbeg / BK + kt);
+    if constexpr (CONV) {
+      const int tap = (tkh * p.cv_w + tkw) * p.cv_cin + tci;
 #pragma unroll
-    for (int q = 0; q < WPA; ++q)
-      dtl16(a_src[q] + k * a_step, S + dtl_window<AK, BM>(wave + q * NW));
+      for (int q = 0; q < WPA; ++q) {
+        const int ih = cv_oh[q] + tkh - p.cv_pad, iw = cv_ow[q] + tkw - p.cv_pad;
+        const bool in = unsigned(ih) < unsigned(p.cv_h) && unsigned(iw) < unsigned(p.cv_w);
+        dtl16(in ? A + cv_base[q] + tap + cv_off[q] : conv_zero_page,
+              S + dtl_window<true, BM>(wave + q * NW));
+      }
+      tci += BK;
+      if (tci == p.cv_cin) {
+        tci = 0;
+        if (++tkw == p.cv_k) {
+          tkw = 0;
+          ++tkh;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < WPA; ++q)
+        dtl16(a_src[q] + k * a_step, S + dtl_window<AK, BM>(wave + q * NW));
+    }
 #pragma unroll
     for (int q = 0; q < WPB; ++q)
       dtl16(b_src[q] + k * b_step, S + kBOff + dtl_window<BKc, BN>(wave + q * NW));
@@ -1558,6 +1629,23 @@ int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, boo
   return SILGPU_OK;
 }
 
+// Implicit-GEMM convolution on the LDS-direct kernel: full 128 x 64 tiles
+// (M % 128 == 0, C_out % 64 == 0) and C_in % 16 == 0, so every K tile of
+// BK = 32 (C_in % 32 == 0) or 16 lies in one tap.
+template <int BK>
+int launch_conv_dtl(const gemm_args &a, hipStream_t s) {
+  using D = dtl_cfg<128, 64, BK, 4, 2>;
+  auto kern = sgemm_dtl_k<128, 64, BK, 4, 2, false, true, true>;
+  gemm_args g = a;
+  g.tiles_m = a.M / 128;
+  g.tiles_n = a.N / 64;
+  g.klen = a.K;
+  dim3 grid(static_cast<unsigned>(int64_t(g.tiles_m) * g.tiles_n), 1u, 1u);
+  kern<<<grid, D::kThreads, 0, s>>>(g);
+  SILGPU_LAUNCH_CHECK("sgemm_dtl_k (conv2d)");
+  return SILGPU_OK;
+}
+
 // Implicit-GEMM convolution on the register-staged MFMA kernel (CONV): the A
 // tile is gathered from the NHWC input, B is the OHWI weight read as a
 // [C_out][K*K*C_in] matrix (transposed B), C is the NHWC output.
@@ -1825,7 +1913,7 @@ int silgpu_conv2d_f32(const float *d_in, const float *d_w, float *d_out, int64_t
                  "silgpu_conv2d_f32: extent product overflows int64");
   if (M == 0 || C_out == 0) return SILGPU_OK;
   SILGPU_REQUIRE(M <= INT32_MAX && Kd <= INT32_MAX && C_out <= INT32_MAX &&
-                     M * C_in <= INT64_MAX / 4,
+                     M * C_in <= INT64_MAX / 4 && K * W * C_in <= INT32_MAX,
                  "silgpu_conv2d_f32: extent exceeds int32");
   SILGPU_REQUIRE(d_out != nullptr, "silgpu_conv2d_f32: null output");
   SILGPU_CTX(c);
@@ -1848,7 +1936,13 @@ int silgpu_conv2d_f32(const float *d_in, const float *d_w, float *d_out, int64_t
   a.cv_cin = static_cast<int>(C_in);
   a.cv_k = static_cast<int>(K);
   a.cv_pad = static_cast<int>(K / 2);
+  if (Kd <= kConvDirectMaxK && C_out <= kConvDirectMaxCo)
+    return conv2d_direct(d_in, d_w, d_out, static_cast<int>(M), static_cast<int>(H),
+                         static_cast<int>(W), static_cast<int>(C_in), static_cast<int>(K),
+                         static_cast<int>(C_out), c->stream);
   const bool vec = C_in % 4 == 0 && aligned16(d_in) && aligned16(d_w);
+  if (vec && C_in % 16 == 0 && M % 128 == 0 && C_out % 64 == 0)
+    return C_in % 32 == 0 ? launch_conv_dtl<32>(a, c->stream) : launch_conv_dtl<16>(a, c->stream);
   if (C_out <= 32)
     return vec ? launch_conv_cfg<64, 64, 2, 2, true>(a, c->stream)
                : launch_conv_cfg<64, 64, 2, 2, false>(a, c->stream);

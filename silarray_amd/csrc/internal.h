@@ -73,6 +73,13 @@ context *ctx();
   ::silgpu::context *c = ::silgpu::ctx();                                            \
   if (!c) return SILGPU_ERR_NODEVICE
 
+// Direct convolution (conv.hip) for reductions K*K*C_in <= kConvDirectMaxK:
+// NHWC in [M = N*H*W pixels][C_in], OHWI w, NHWC out, stride 1, padding K/2.
+constexpr int kConvDirectMaxK = 64;
+constexpr int64_t kConvDirectMaxCo = int64_t(65535) * 16;  // grid.y = C_out / 16 blocks
+int conv2d_direct(const float *in, const float *w, float *out, int M, int H, int W, int cin,
+                  int K, int Co, hipStream_t s);
+
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 __device__ __forceinline__ bool aligned16_dev(const void *p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;

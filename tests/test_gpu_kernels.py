@@ -804,12 +804,21 @@ def test_attention_no_keys_gives_zero(native):
 
 # ---- conv2d (implicit GEMM) ---------------------------------------------------------
 
-# N, H, W, C_in, K, C_out: scalar gathers (C_in % 4 != 0), float4 gathers,
-# even and 1x1 kernels, ragged tiles on both GEMM axes, both tile shapes
-# (C_out <= 32 and above) and the reference benchmark's three layers
-# (bench/micro/bench_nn_ops.cpp:193-195) at full size.
-CONV_CASES = [(1, 8, 8, 3, 3, 16), (2, 7, 9, 16, 3, 32), (1, 5, 6, 4, 1, 5), (1, 6, 6, 8, 5, 12),
-              (2, 9, 5, 6, 2, 40), (3, 4, 4, 1, 3, 1), (1, 13, 11, 20, 3, 70), (1, 3, 3, 2, 7, 3),
+# N, H, W, C_in, K, C_out, by the kernel the entry point picks:
+#  direct (K*K*C_in <= 64): C_out below, at and above one 32-channel block,
+#    C_out % 4 != 0, 1x1 and even kernels;
+#  LDS-direct implicit GEMM (C_in % 16 == 0, M % 128 == 0, C_out % 64 ==
+#    0): BK 16 (C_in = 16, 48) and 32, K = 1, 2, 3, 5;
+#  register-staged implicit GEMM: float4 (C_in % 4 == 0) and scalar gathers,
+#    ragged tiles on both GEMM axes, C_out <= 32 and above;
+# and the reference benchmark's three layers (bench/micro/bench_nn_ops.cpp:
+# 193-195) at full size.
+CONV_CASES = [(1, 8, 8, 3, 3, 16), (1, 5, 6, 4, 1, 5), (2, 9, 5, 6, 2, 40), (3, 4, 4, 1, 3, 1),
+              (1, 5, 7, 2, 3, 37), (2, 6, 6, 64, 1, 33),
+              (2, 8, 8, 16, 3, 64), (1, 16, 16, 48, 3, 128), (1, 8, 16, 32, 5, 64),
+              (1, 8, 16, 32, 2, 64), (1, 16, 8, 128, 1, 128),
+              (2, 7, 9, 16, 3, 32), (1, 6, 6, 8, 5, 12), (1, 13, 11, 20, 3, 70),
+              (1, 3, 3, 2, 7, 3), (2, 8, 8, 16, 3, 60),
               (1, 224, 224, 3, 3, 32), (16, 56, 56, 64, 3, 128), (16, 28, 28, 128, 3, 256)]
 
 
