@@ -295,14 +295,15 @@ def bench_graphs(timeout: float = 300.0) -> list[dict]:
     """Whole sil::eval graphs through the C++ front end (bench_graph): the
     B4 S512 d768 H12 encoder block, the reference's single-head transformer
     and linear_sigmoid MLP benchmarks, and the 20-op affine chain at the API
-    level.  Each iteration is eval + synchronize, as the reference times it."""
+    level, and host <-> HBM copies of a 256 MiB array through its pinned host
+    mirror.  Each iteration is eval + synchronize, as the reference times it."""
     import subprocess
 
     if not GRAPH_BENCH.exists():
         raise RuntimeError(f"{GRAPH_BENCH} is not built (run __graft_entry__.build())")
     out = []
     for argv in (["encoder", "10"], ["transformer"], ["mlp"], ["train"],
-                 ["chain", str(64 << 20), "20"]):
+                 ["chain", str(64 << 20), "20"], ["transfer", str(64 << 20), "10"]):
         log(f"bench_graph {' '.join(argv)}")
         proc = subprocess.run([str(GRAPH_BENCH), *argv], capture_output=True, text=True,
                               timeout=timeout)
@@ -351,7 +352,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "multi-GPU sharding is described in DESIGN.md but not run.", file=sys.stderr)
+              "the multi-GPU sharding is a design only and is not run.", file=sys.stderr)
         return 2
     from silarray_amd import _native as nat
 
@@ -443,6 +444,12 @@ def main():
                 key = f"mlp_linear_sigmoid_batch{r['batch']}"
             elif w == "train_step":
                 key = f"train_step_768x2048_batch{r['batch']}"
+            elif w == "transfer":
+                secondary["host_transfer_256MiB"] = {
+                    "value": r["h2d_gbs"], "unit": "GB/s (host to HBM)", "d2h_gbs": r["d2h_gbs"],
+                    "timing": "median of upload/download + one kernel, kernel time subtracted",
+                    "note": "pinned host mirrors; pageable memory gives 31.7 / 18.3 GB/s here"}
+                continue
             else:
                 key = f"{w}_64M_api"
             if "gemm_tflops" in r:

@@ -90,7 +90,12 @@ int silgpu_pool_trim(void);
 /* Bytes currently handed out and bytes cached in the pool. */
 int silgpu_pool_stats(size_t *in_use, size_t *cached);
 
-/* Pinned host memory for the host mirror of a storage (hipHostMalloc). */
+/* Pinned host memory (hipHostMalloc) for the host mirror of a storage, pooled
+ * by the device pool's size classes; silgpu_host_free returns the block to
+ * the pool and silgpu_pool_trim() releases the cache.  Copies between pinned
+ * blocks and HBM run as direct DMA.  The reference's unified memory
+ * (include/unified_memory.h:38-79) needs no copies at all; this is the
+ * staging side of the discrete-memory design. */
 int silgpu_host_alloc(size_t bytes, void **h_ptr);
 int silgpu_host_free(void *h_ptr);
 

@@ -14,6 +14,10 @@
 //                                             768 -> 2048 -> 768 sigmoid MLP,
 //                                             forward, MSE gradient, backward,
 //                                             SGD update, one sil::eval
+//   bench_graph transfer [n] [reps]           host<->HBM copies of an n-float
+//                                             array through its (pinned) host
+//                                             mirror: upload after a host
+//                                             write, download on a host read
 //   bench_graph train-dump B D H DIR          one training step on seeded
 //                                             inputs, written to DIR (raw
 //                                             float32) for the parity test
@@ -34,6 +38,7 @@
 #include <cstdlib>
 #include <fstream>
 #include <string>
+#include <utility>
 #include <vector>
 
 using namespace sil;
@@ -264,6 +269,40 @@ int main(int argc, char **argv) {
                   ms, 8.0 * double(n) / (ms * 1e-3) / 1e9);
       return 0;
     }
+    if (mode == "transfer") {
+      const size_t n = argc > 2 ? std::strtoull(argv[2], nullptr, 10) : (size_t(64) << 20);
+      const int reps = argc > 3 ? std::atoi(argv[3]) : 10;
+      if (reps < 1 || n == 0) throw std::runtime_error("n and reps must be >= 1");
+      rng g(11);
+      auto x = filled({n}, g, 1.0f, true);
+      auto y = x * 2.0f;
+      eval(y);
+      const double copy_ms = median_ms(reps, [&] {  // the kernel alone
+        auto t = x + 1.0f;
+        eval(t);
+      });
+      float sink = 0.0f;
+      // Upload: a host write makes the device copy stale, the next kernel
+      // reading x uploads the whole mirror.
+      const double up_ms = median_ms(reps, [&] {
+        x.buffer_data()[0] += 1.0f;
+        auto t = x + 1.0f;
+        eval(t);
+      });
+      // Download: a fresh device result read on the host.
+      const double down_ms = median_ms(reps, [&] {
+        auto z = x * 2.0f;
+        eval(z);
+        sink += std::as_const(z).buffer_data()[n - 1];
+      });
+      const double gb = 4.0 * double(n) / 1e9;
+      std::printf("{\"workload\": \"transfer\", \"n\": %zu, \"h2d_gbs\": %.1f, "
+                  "\"d2h_gbs\": %.1f, \"kernel_ms\": %.4f, \"h2d_ms\": %.4f, "
+                  "\"d2h_ms\": %.4f, \"check\": %d}\n",
+                  n, gb / ((up_ms - copy_ms) * 1e-3), gb / ((down_ms - copy_ms) * 1e-3), copy_ms,
+                  up_ms, down_ms, int(std::isfinite(sink)));
+      return 0;
+    }
     if (mode == "encoder" || mode == "encoder-dump") {
       // argv: mode [B S D H F [reps|DIR]] or, for "encoder", mode [reps].
       size_t dims[5] = {4, 512, 768, 12, 3072};
@@ -386,7 +425,7 @@ int main(int argc, char **argv) {
       return 0;
     }
     std::fprintf(stderr,
-                 "usage: bench_graph chain|encoder|encoder-dump|transformer|mlp|train|train-dump "
+                 "usage: bench_graph chain|transfer|encoder|encoder-dump|transformer|mlp|train|train-dump "
                  "...\n");
     return 2;
   } catch (std::exception &ex) {

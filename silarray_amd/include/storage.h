@@ -73,6 +73,7 @@ struct block {
   // Handed out through storage::make(): the caller may read `data` directly
   // after synchronize(), so kernel writes are tracked for download.
   bool raw = false;
+  bool pinned = false;  // host mirror from silgpu_host_alloc
 
   explicit block(size_t n) : bytes(n) {}
   block(const block &) = delete;
@@ -84,7 +85,8 @@ struct block {
       d.blocks.erase(this);
     }
     if (dev) silgpu_free(dev);
-    std::free(host);
+    if (pinned) silgpu_host_free(host);
+    else std::free(host);
   }
 
   void *dev_ptr() {
@@ -95,13 +97,26 @@ struct block {
     return dev;
   }
 
-  // Plain (pageable) host memory: host access is the exception on this
-  // backend, and host-only work (shape logic, int reductions) then runs
-  // without a GPU at all.
+  // Mirrors of kPinnedMirrorBytes or more are pinned (pooled
+  // silgpu_host_alloc), so uploads and downloads are direct DMA; smaller
+  // ones, and every mirror when no GPU is usable (host-only work such as
+  // shape logic and int reductions runs without one), are plain pageable
+  // memory.
+  static constexpr size_t kPinnedMirrorBytes = size_t(256) << 10;
+  static bool pinning_available() {
+    static const bool ok = silgpu_init() == SILGPU_OK;
+    return ok;
+  }
   void *host_ptr() {
     if (!host) {
-      host = std::aligned_alloc(64, ((bytes ? bytes : 4) + 63) / 64 * 64);
-      if (!host) throw std::bad_alloc();
+      const size_t n = ((bytes ? bytes : 4) + 63) / 64 * 64;
+      if (n >= kPinnedMirrorBytes && pinning_available() &&
+          silgpu_host_alloc(n, &host) == SILGPU_OK) {
+        pinned = true;
+      } else {
+        host = std::aligned_alloc(64, n);
+        if (!host) throw std::bad_alloc();
+      }
     }
     return host;
   }

@@ -613,6 +613,24 @@ TEST_CASE("conv2d: same padding closed form and the 1x1 kernel as a product") {
                     "array: conv2d requires a 4D NHWC input and a 4D OHWI weight.");
 }
 
+TEST_CASE("large arrays round-trip through pinned host mirrors") {
+  // 4 MiB: above the size from which host mirrors are pinned
+  const size_t n = size_t(1) << 20;
+  std::vector<float> v(n);
+  for (size_t i = 0; i < n; i++) v[i] = float(i % 1000) * 0.5f;
+  auto x = array<float>({n}, v);
+  auto y = x * 2.0f;  // uploads x
+  eval(y);
+  bool ok = true;
+  for (size_t i = 0; i < n; i++) ok = ok && y.at(i) == v[i] * 2.0f;  // downloads y
+  CHECK(ok);
+  x.at(5) = 7.0f;  // host write: the device copy is stale and uploads again
+  auto z = x + 1.0f;
+  eval(z);
+  CHECK(z.at(5) == 8.0f);
+  CHECK(z.at(n - 1) == v[n - 1] + 1.0f);
+}
+
 HOST_CASE("view, permute and select on evaluated arrays") {
   auto m = array<int>({2, 3, 4}, iota_n(24));
   auto p = m.permute({2, 0, 1});

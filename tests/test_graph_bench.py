@@ -1,7 +1,7 @@
 """The sil::eval graph benchmark (silarray_amd/bench/bench_graph.cpp): one
 transformer encoder block written against the C++ sil::array API, lowered by
 sil::eval onto the HIP kernels, checked against a float64 numpy restatement of
-the same block.  The block combines every §-row of the hot path the reference
+the same block.  The block combines every operator of the hot path the reference
 exposes to a model (examples/transformer_*.cpp use the same operators):
 layer_norm, linear (bias epilogue), strided batched products over head views,
 row softmax, the relu epilogue fusion and fused residual adds."""
@@ -162,3 +162,13 @@ def test_train_reports_json():
                          timeout=120, check=True).stdout
     rec = json.loads(out.strip().splitlines()[-1])
     assert rec["workload"] == "train_step" and rec["batch"] == 16 and rec["ms"] > 0
+
+
+@pytest.mark.gpu
+def test_transfer_reports_json():
+    print("bench_graph transfer (4M floats)", flush=True)
+    out = subprocess.run([str(_bench()), "transfer", str(1 << 22), "3"], capture_output=True,
+                         text=True, timeout=120, check=True).stdout
+    rec = json.loads(out.strip().splitlines()[-1])
+    assert rec["workload"] == "transfer" and rec["check"] == 1
+    assert rec["h2d_ms"] > 0 and rec["d2h_ms"] > 0
