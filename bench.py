@@ -205,8 +205,11 @@ def bench_conv2d(nat, g, reps=50):
         t = Timer(nat)
         ms = t.ms_per_launch(lambda i: nat.conv2d(x, w, y, N, H, W, Ci, K, Co), reps)
         flops = 2.0 * N * H * W * Co * K * K * Ci
+        nbytes = 4.0 * (N * H * W * Ci + Co * K * K * Ci + N * H * W * Co)
         out[f"conv2d_{name}_{N}x{Ci}x{H}x{W}_k{K}_co{Co}"] = {
-            "tflops": flops / (ms / 1e3) / 1e12, "us": ms * 1e3, "ref_ms": ref_ms}
+            "tflops": flops / (ms / 1e3) / 1e12, "gbs": nbytes / (ms / 1e3) / 1e9,
+            "hbm_bound": flops / nbytes < PEAK_FP32_MFMA_TFLOPS / PEAK_HBM_GBS * 1e3,
+            "us": ms * 1e3, "ref_ms": ref_ms, "traffic_key": f"conv2d_{name}"}
     return out
 
 
@@ -393,9 +396,16 @@ def main():
     if want("conv2d"):
         for k, v in bench_conv2d(nat, g).items():
             log(f"{k} {v}")
-            secondary[k] = {"value": round(v["tflops"], 2), "unit": "TFLOP/s",
-                            "us": round(v["us"], 1), "reference_m1pro_ms": v["ref_ms"],
-                            "roofline": roofline("mfma", v["tflops"])}
+            traffic = load_traffic(v["traffic_key"])
+            if v["hbm_bound"]:  # below the ridge (19.7 flop/B): priced against HBM
+                secondary[k] = {"value": round(v["gbs"], 1), "unit": "GB/s",
+                                "tflops": round(v["tflops"], 2), "us": round(v["us"], 2),
+                                "reference_m1pro_ms": v["ref_ms"],
+                                "roofline": roofline("hbm", v["gbs"], traffic)}
+            else:
+                secondary[k] = {"value": round(v["tflops"], 2), "unit": "TFLOP/s",
+                                "us": round(v["us"], 1), "reference_m1pro_ms": v["ref_ms"],
+                                "roofline": roofline("mfma", v["tflops"], traffic)}
     if want("rowops"):
         r = bench_rowops(nat, g)
         log(f"rowops {r}")
