@@ -122,8 +122,9 @@ struct gemm_args {
   // Implicit-GEMM convolution (sgemm_mfma_k<..., CONV>): A is the virtual
   // im2col matrix of an NHWC input [batch][H][W][C_in], row m = output
   // pixel (n, oh, ow), column k = (kh, kw, ci) with ci fastest, stride 1,
-  // zero padding `pad` on every side (output H x W).
-  int cv_h, cv_w, cv_cin, cv_k, cv_pad;
+  // zero padding `pad` on every side (output H x W).  Row m of this launch
+  // is output pixel cv_m0 + m (a launch may cover a range of the rows).
+  int cv_h, cv_w, cv_cin, cv_k, cv_pad, cv_m0;
 };
 
 template <int BM, int BN, int BK, int WM, int WN, int MI>
@@ -231,7 +232,7 @@ struct conv_walk {
       ow[i] = 0;
       base[i] = 0;
       if (m < p.M) {
-        const int n = m / hw, rem = m - n * hw;
+        const int pm = p.cv_m0 + m, n = pm / hw, rem = pm - n * hw;
         oh[i] = rem / p.cv_w;
         ow[i] = rem - oh[i] * p.cv_w;
         base[i] = ((int64_t(n) * p.cv_h + oh[i] - p.cv_pad) * p.cv_w + ow[i] - p.cv_pad) * cin;
@@ -830,7 +831,7 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU,
 #pragma unroll
     for (int q = 0; q < WPA; ++q) {
       const int w = wave + q * NW, rr = lane / 4, kq = (lane % 4) ^ ((rr / 2) & 3);
-      const int m = m0 + 16 * (w % (BM / 16)) + rr;  // < M: full tiles only
+      const int m = p.cv_m0 + m0 + 16 * (w % (BM / 16)) + rr;  // full tiles only
       const int n = m / hw, rem = m - n * hw;
       cv_oh[q] = rem / p.cv_w;
       cv_ow[q] = rem - cv_oh[q] * p.cv_w;
@@ -1422,6 +1423,10 @@ enum tile_cfg {
 struct plan {
   int tile;
   int splits;
+  // Batch 1: the last tail_rows rows of C run as a second product with
+  // tail_splits K splits (the main product then fills whole rounds of CUs).
+  int tail_rows = 0;
+  int tail_splits = 1;
 };
 
 // Shape heuristic: a cost model calibrated on MI355X sweeps of the 8192^3,
@@ -1503,6 +1508,40 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dtl_ok) {
       }
     }
   }
+  // Peeling a thin last round: when the tiles of an unsplit product fill
+  // whole rounds of the 256 CUs plus part of another, the tile rows past
+  // the last whole round can run as a second product split along K, so
+  // the first launch has no partly filled round.  Same per-round model,
+  // plus one launch for the second product.
+  if (batch == 1) {
+    for (const cand &cd : cands) {
+      const int64_t tm = cdiv(M, cd.bm), tn = cdiv(N, cd.bn), wg = tm * tn;
+      if (wg <= 256 || wg % 256 == 0) continue;
+      const int64_t rows_main = (wg / 256) * 256 / tn;
+      if (rows_main < 1 || rows_main >= tm) continue;
+      auto round_time = [&](int64_t nwg, double klen) {
+        const int64_t per_cu = cdiv(nwg, 256);
+        const double conc = double(per_cu < cd.occupancy ? per_cu : cd.occupancy);
+        const double per_simd = conc * cd.waves / 4.0;
+        const double f = per_simd >= 2.0 ? 1.0 : per_simd >= 1.0 ? kSingleWave
+                                                                  : kSingleWave * per_simd;
+        return double(per_cu) * 2.0 * cd.bm * cd.bn * klen /
+               (rate_cu * cd.eff * f * (klen / (klen + kK0)));
+      };
+      const double t_main = round_time(rows_main * tn, double(cdiv(K, cd.bk) * cd.bk));
+      const int64_t mt = M - rows_main * cd.bm;
+      for (int sp : {1, 2, 3, 4, 6, 8}) {
+        if (sp > 1 && K / sp < 128) continue;
+        const double klen = double(cdiv(cdiv(K, sp), cd.bk) * cd.bk);
+        double t = t_main + round_time(cdiv(mt, cd.bm) * tn * sp, klen) + kLaunch;
+        if (sp > 1) t += double(sp + 1) * double(mt) * double(N) * 4.0 / kReduceBw + kLaunch;
+        if (t < best_t * 0.97) {
+          best_t = t;
+          best = plan{cd.tile, 1, static_cast<int>(mt), sp};
+        }
+      }
+    }
+  }
   return best;
 }
 
@@ -1564,8 +1603,24 @@ int launch_skinny(const gemm_args &a, int Q, int splits, bool tb, hipStream_t s)
             : launch_skinny_q<1, false>(a, splits, va, bvec, s);
 }
 
+int launch_split_sum(const gemm_args &a, int launched, context *c);
+
 int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, bool vec,
               context *c) {
+  if (pl.tail_rows > 0 && pl.tail_rows < a0.M && batch == 1) {
+    // Rows [0, M - tail) as one product, the last tail rows as another.
+    const int head = a0.M - pl.tail_rows;
+    gemm_args h = a0, t = a0;
+    h.M = head;
+    t.M = pl.tail_rows;
+    t.A = a0.A + (ta ? int64_t(head) : int64_t(head) * a0.lda);
+    t.C = a0.C + int64_t(head) * a0.ldc;
+    if (t.ep.res) t.ep.res += int64_t(head) * t.ep.ldr;
+    const bool tvec = vec && aligned16(t.A);
+    int rc = run_sgemm(h, 1, plan{pl.tile, 1}, ta, tb, vec, c);
+    if (rc != SILGPU_OK) return rc;
+    return run_sgemm(t, 1, plan{pl.tile, pl.tail_splits}, ta, tb, tvec, c);
+  }
   gemm_args a = a0;
   const bool skinny = pl.tile >= TILE_SKINNY && a.M <= 32 && batch == 1 && !ta;
   if (pl.tile >= TILE_SKINNY && !skinny)
@@ -1607,7 +1662,12 @@ int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, boo
     }
   }
   if (launched < 0) return launched;
-  if (launched > 1) {
+  return launched > 1 ? launch_split_sum(a, launched, c) : SILGPU_OK;
+}
+
+// Adds the `splits` partial planes a.ws[s][M][N] into C with the epilogue.
+int launch_split_sum(const gemm_args &a, int launched, context *c) {
+  {
     const bool v4 = a.N % 4 == 0 && a.ldc % 4 == 0 && aligned16(a.C);
     const int64_t groups = a.M * int64_t(a.N) / (v4 ? 4 : 1);
     const bool deep = launched >= 8 && groups < 65536;
@@ -1632,15 +1692,18 @@ int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, boo
 // Implicit-GEMM convolution on the LDS-direct kernel: full 128 x 64 tiles
 // (M % 128 == 0, C_out % 64 == 0) and C_in % 16 == 0, so every K tile of
 // BK = 32 (C_in % 32 == 0) or 16 lies in one tap.
+// splits > 1 (dividing K / BK): partial planes to a.ws, added by
+// launch_split_sum.
 template <int BK>
-int launch_conv_dtl(const gemm_args &a, hipStream_t s) {
+int launch_conv_dtl(const gemm_args &a, int splits, hipStream_t s) {
   using D = dtl_cfg<128, 64, BK, 4, 2>;
   auto kern = sgemm_dtl_k<128, 64, BK, 4, 2, false, true, true>;
   gemm_args g = a;
   g.tiles_m = a.M / 128;
   g.tiles_n = a.N / 64;
-  g.klen = a.K;
-  dim3 grid(static_cast<unsigned>(int64_t(g.tiles_m) * g.tiles_n), 1u, 1u);
+  g.klen = a.K / splits;
+  dim3 grid(static_cast<unsigned>(int64_t(g.tiles_m) * g.tiles_n), static_cast<unsigned>(splits),
+            1u);
   kern<<<grid, D::kThreads, 0, s>>>(g);
   SILGPU_LAUNCH_CHECK("sgemm_dtl_k (conv2d)");
   return SILGPU_OK;
@@ -1941,8 +2004,42 @@ int silgpu_conv2d_f32(const float *d_in, const float *d_w, float *d_out, int64_t
                          static_cast<int>(W), static_cast<int>(C_in), static_cast<int>(K),
                          static_cast<int>(C_out), c->stream);
   const bool vec = C_in % 4 == 0 && aligned16(d_in) && aligned16(d_w);
-  if (vec && C_in % 16 == 0 && M % 128 == 0 && C_out % 64 == 0)
-    return C_in % 32 == 0 ? launch_conv_dtl<32>(a, c->stream) : launch_conv_dtl<16>(a, c->stream);
+  if (vec && C_in % 16 == 0 && M % 128 == 0 && C_out % 64 == 0) {
+    // Three 128 x 64 workgroups fit a CU.  When the tiles fill whole rounds
+    // of all CUs plus a thin last round, the tile rows of that last round
+    // run as a second launch split along K (one piece per CU at most) and a
+    // split sum, instead of a round of a few workgroups at full depth.
+    const int BK = C_in % 32 == 0 ? 32 : 16;
+    const int64_t tiles_n = C_out / 64, tiles_m = M / 128, tiles = tiles_m * tiles_n;
+    const int64_t slots = int64_t(c->cu_count) * 3, rem = tiles % slots;
+    int64_t rows_main = tiles_m;
+    int splits = 1;
+    if (tiles > slots && rem > 0 && rem * 4 <= slots) {
+      const int64_t rem_rows = cdiv(rem, tiles_n), kt = Kd / BK;
+      rows_main = tiles_m - rem_rows;
+      for (int64_t sp = 2; sp <= kt; ++sp)
+        if (kt % sp == 0 && rem_rows * tiles_n * sp <= c->cu_count) splits = int(sp);
+    }
+    auto conv = [&](const gemm_args &g, int sp) {
+      return BK == 32 ? launch_conv_dtl<32>(g, sp, c->stream) : launch_conv_dtl<16>(g, sp, c->stream);
+    };
+    gemm_args main = a;
+    main.M = static_cast<int>(rows_main * 128);
+    int rc = conv(main, 1);
+    if (rc != SILGPU_OK || rows_main == tiles_m) return rc;
+    gemm_args tail = a;
+    tail.cv_m0 = main.M;
+    tail.M = static_cast<int>(M) - main.M;
+    tail.C = d_out + int64_t(main.M) * C_out;
+    if (splits > 1) {
+      rc = ensure_workspace(c, size_t(splits) * size_t(tail.M) * size_t(C_out) * sizeof(float));
+      if (rc != SILGPU_OK) return rc;
+      tail.ws = static_cast<float *>(c->workspace);
+    }
+    rc = conv(tail, splits);
+    if (rc != SILGPU_OK || splits == 1) return rc;
+    return launch_split_sum(tail, splits, c);
+  }
   if (C_out <= 32)
     return vec ? launch_conv_cfg<64, 64, 2, 2, true>(a, c->stream)
                : launch_conv_cfg<64, 64, 2, 2, false>(a, c->stream);

@@ -637,6 +637,31 @@ def test_sgemm_small_m(native, oracle, tile, splits, M, N, K, tb, lpa, lpb, lpc,
 
 # ---- silgpu_gemm: two-level batch, fused scale / residual ----------------------------
 
+# Shapes whose unsplit tiles fill whole rounds of the 256 CUs plus part of
+# another: the plan runs the last tile rows as a second product split along
+# K (2048x2304x768: 256 rows in 3 splits; 2176x4096x768 on 128x128 tiles:
+# 128 rows in 6 splits; 1152x4096x512: 128 rows in 4 splits).
+@pytest.mark.parametrize("M,N,K", [(2048, 2304, 768), (2176, 4096, 768), (1152, 4096, 512)])
+def test_sgemm_peeled_tail(native, oracle, M, N, K):
+    announce(f"sgemm peeled tail {M}x{N}x{K}")
+    g = rng(2600 + M)
+    A = g.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = g.uniform(-1, 1, (K, N)).astype(np.float32)
+    bias = g.normal(0, 1, N).astype(np.float32)
+    dA, dB, db, dC = up(native, A), up(native, B), up(native, bias), empty(native, M * N)
+    native.sgemm(0, 0, M, N, K, dA, K, 0, dB, N, 0, dC, N, 0, 1, db, N, native.EPI_BIAS)
+    Cg = down(native, dC, (M, N))
+    # every row of the last 256 (head/tail boundary and tail), random elsewhere
+    rows = np.concatenate([np.repeat(np.arange(M - 256, M), 8), g.integers(0, M, 2048)])
+    cols = g.integers(0, N, rows.size)
+    ref, refabs = oracle.sgemm_sampled_f64(A, B, rows, cols)
+    ref = ref + bias[cols]
+    refabs = refabs + np.abs(bias[cols])
+    tol = 1e-5 * math.sqrt(K)
+    diff = np.abs(Cg[rows, cols] - ref)
+    assert np.all(diff <= tol * refabs), float(np.max(diff / refabs))
+
+
 def test_gemm_two_level_batch_head_split(native, oracle):
     """Q K^T for every (batch, head) of a [B*S, 3*H*dh] qkv array in one launch:
     A and B are strided head views (outer stride per batch, inner per head)."""
@@ -659,12 +684,12 @@ def test_gemm_two_level_batch_head_split(native, oracle):
 
 
 @pytest.mark.parametrize("M,N,K", [(100, 130, 200), (256, 256, 4096), (1, 300, 257),
-                                   (512, 512, 96)])
+                                   (512, 512, 96), (2048, 2304, 768)])
 def test_gemm_fused_epilogue_bit_exact(native, oracle, M, N, K):
     """scale -> bias -> relu -> residual fused into the product equals the
     same fp32 steps run as separate kernels (affine fma, bias add, relu,
     residual add), bit for bit, on every GEMM path (MFMA tiles, split K,
-    GEMV for M == 1)."""
+    GEMV for M == 1, a peeled split tail)."""
     announce(f"gemm fused epilogue {M}x{N}x{K}")
     g = rng(2200 + M + K)
     A = g.uniform(-1, 1, (M, K)).astype(np.float32)
@@ -811,15 +836,18 @@ def test_attention_no_keys_gives_zero(native):
 #    0): BK 16 (C_in = 16, 48) and 32, K = 1, 2, 3, 5;
 #  register-staged implicit GEMM: float4 (C_in % 4 == 0) and scalar gathers,
 #    ragged tiles on both GEMM axes, C_out <= 32 and above;
-# and the reference benchmark's three layers (bench/micro/bench_nn_ops.cpp:
-# 193-195) at full size.
+# the reference benchmark's three layers (bench/micro/bench_nn_ops.cpp:
+# 193-195) at full size; and shapes whose 128 x 64 tiles fill three rounds of
+# 256 CUs plus a thin last round, which runs as a second launch (split along
+# K into 9 pieces with BK 32 and 16, or unsplit).
 CONV_CASES = [(1, 8, 8, 3, 3, 16), (1, 5, 6, 4, 1, 5), (2, 9, 5, 6, 2, 40), (3, 4, 4, 1, 3, 1),
               (1, 5, 7, 2, 3, 37), (2, 6, 6, 64, 1, 33),
               (2, 8, 8, 16, 3, 64), (1, 16, 16, 48, 3, 128), (1, 8, 16, 32, 5, 64),
               (1, 8, 16, 32, 2, 64), (1, 16, 8, 128, 1, 128),
               (2, 7, 9, 16, 3, 32), (1, 6, 6, 8, 5, 12), (1, 13, 11, 20, 3, 70),
               (1, 3, 3, 2, 7, 3), (2, 8, 8, 16, 3, 60),
-              (1, 224, 224, 3, 3, 32), (16, 56, 56, 64, 3, 128), (16, 28, 28, 128, 3, 256)]
+              (1, 224, 224, 3, 3, 32), (16, 56, 56, 64, 3, 128), (16, 28, 28, 128, 3, 256),
+              (16, 56, 56, 48, 3, 128), (1, 116, 256, 32, 3, 256)]
 
 
 @pytest.mark.parametrize("N,H,W,Ci,K,Co", CONV_CASES)
