@@ -170,8 +170,10 @@ def bench_small_batch(nat, g, reps=200):
     t = Timer(nat)
     ms = t.ms_per_launch(lambda i: nat.sgemm(0, 0, M, N, K, A, K, 0, Bs[i % copies], N, 0, C, N, 0),
                          reps, warmup=copies)
+    ms_hot = t.ms_per_launch(lambda i: nat.sgemm(0, 0, M, N, K, A, K, 0, Bs[0], N, 0, C, N, 0), reps)
     nbytes = 4 * (M * K + K * N + M * N)
-    return {"gbs": nbytes / (ms / 1e3) / 1e9, "us": ms * 1e3,
+    return {"gbs": nbytes / (ms / 1e3) / 1e9, "gbs_hot": nbytes / (ms_hot / 1e3) / 1e9,
+            "us": ms * 1e3,
             "tflops": 2 * M * N * K / (ms / 1e3) / 1e12, "bytes": nbytes}
 
 
@@ -223,15 +225,19 @@ def bench_rowops(nat, g, reps=20):
     beta = nat.DeviceBuffer.from_array(np.zeros(Cc, np.float32))
     t = Timer(nat)
     out = {}
-    ms = t.ms_per_launch(lambda i: nat.softmax_rows_f32(xs[i % pairs], ys[i % pairs], R, Cc), reps, pairs)
-    out["softmax"] = {"gbs": 8 * R * Cc / (ms / 1e3) / 1e9, "us": ms * 1e3, "bytes": 8 * R * Cc}
-    ms = t.ms_per_launch(lambda i: nat.layer_norm_rows_f32(xs[i % pairs], ys[i % pairs], gamma, beta,
-                                                           R, Cc, 1e-5), reps, pairs)
-    nb = 8 * R * Cc + 8 * Cc
-    out["layer_norm"] = {"gbs": nb / (ms / 1e3) / 1e9, "us": ms * 1e3, "bytes": nb}
-    ms = t.ms_per_launch(lambda i: nat.sum_axis_f32(xs[i % pairs], R, Cc, 1, ys[i % pairs]), reps, pairs)
-    nb = 4 * R * Cc + 4 * R
-    out["sum_axis1"] = {"gbs": nb / (ms / 1e3) / 1e9, "us": ms * 1e3, "bytes": nb}
+    # Rotated (gated) and hot (one pair, partly served by the 256 MiB
+    # Infinity Cache) rates.
+    ops = {
+        "softmax": (lambda i, j: nat.softmax_rows_f32(xs[j], ys[j], R, Cc), 8 * R * Cc),
+        "layer_norm": (lambda i, j: nat.layer_norm_rows_f32(xs[j], ys[j], gamma, beta, R, Cc, 1e-5),
+                       8 * R * Cc + 8 * Cc),
+        "sum_axis1": (lambda i, j: nat.sum_axis_f32(xs[j], R, Cc, 1, ys[j]), 4 * R * Cc + 4 * R),
+    }
+    for name, (fn, nb) in ops.items():
+        ms = t.ms_per_launch(lambda i: fn(i, i % pairs), reps, pairs)
+        ms_hot = t.ms_per_launch(lambda i: fn(i, 0), reps)
+        out[name] = {"gbs": nb / (ms / 1e3) / 1e9, "gbs_hot": nb / (ms_hot / 1e3) / 1e9,
+                     "us": ms * 1e3, "bytes": nb}
     return out
 
 
@@ -244,11 +250,14 @@ def bench_reductions(nat, g, reps=20):
     o = nat.DeviceBuffer(4096)
     t = Timer(nat)
     out = {}
-    for name, fn in [("sum", nat.sum_f32), ("min", nat.min_f32), ("max", nat.max_f32)]:
-        ms = t.ms_per_launch(lambda i, fn=fn: fn(xs[i % copies], n, o), reps, copies)
-        out[name] = {"gbs": 4 * n / (ms / 1e3) / 1e9, "us": ms * 1e3, "bytes": 4 * n}
-    ms = t.ms_per_launch(lambda i: nat.argmax_rows_f32(xs[i % copies], 1, n, o), reps, copies)
-    out["argmax"] = {"gbs": 4 * n / (ms / 1e3) / 1e9, "us": ms * 1e3, "bytes": 4 * n}
+    ops = [("sum", lambda x: nat.sum_f32(x, n, o)), ("min", lambda x: nat.min_f32(x, n, o)),
+           ("max", lambda x: nat.max_f32(x, n, o)),
+           ("argmax", lambda x: nat.argmax_rows_f32(x, 1, n, o))]
+    for name, fn in ops:
+        ms = t.ms_per_launch(lambda i: fn(xs[i % copies]), reps, copies)
+        ms_hot = t.ms_per_launch(lambda i: fn(xs[0]), reps)
+        out[name] = {"gbs": 4 * n / (ms / 1e3) / 1e9, "gbs_hot": 4 * n / (ms_hot / 1e3) / 1e9,
+                     "us": ms * 1e3, "bytes": 4 * n}
     nat.sync()
     idx = int(o.download(1, np.int32)[0])
     out["argmax"]["index_ok"] = idx == (n * 7) // 9 + 1
@@ -345,10 +354,56 @@ def cpu_baseline(seconds: float) -> dict:
         if el >= seconds:
             break
     tflops = 2.0 * S ** 3 * runs / el / 1e12
+    del A, B, Cm
+    # One thread, as a per-core figure: 2048^3 (8192^3 takes ~20 s per call
+    # on one core), whole calls for about 3 s.
+    openblas.set_threads(1)
+    S1 = 2048
+    A1, B1 = uniform(g, (S1, S1)), uniform(g, (S1, S1))
+    C1 = np.empty((S1, S1), np.float32)
+    openblas.sgemm(A1, B1, C1)
+    runs1, t1 = 0, time.perf_counter()
+    while True:
+        openblas.sgemm(A1, B1, C1)
+        runs1 += 1
+        el1 = time.perf_counter() - t1
+        if el1 >= 3.0:
+            break
+    openblas.set_threads(cores)
     return {"value": round(tflops, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
             "sample": f"cblas_sgemm (OpenBLAS, {Path(openblas.LIB_PATH).name}) {S}^3 fp32 "
                       f"row-major NN, uniform[-1,1], {runs} whole calls in {el:.1f} s after one "
-                      f"untimed call, {cores} threads"}
+                      f"untimed call, {cores} threads",
+            "host": host_cpu_info(),
+            "one_thread": {"value": round(2.0 * S1 ** 3 * runs1 / el1 / 1e12, 4),
+                           "unit": "TFLOP/s", "cores": 1,
+                           "sample": f"{S1}^3, {runs1} whole calls in {el1:.1f} s"}}
+
+
+def host_cpu_info() -> dict:
+    """nproc, the CPUs this process may use, and sockets x cores from
+    /proc/cpuinfo (Linux)."""
+    info = {"nproc": os.cpu_count()}
+    try:
+        info["affinity"] = len(os.sched_getaffinity(0))
+    except Exception:
+        pass
+    try:
+        phys, cores, model = set(), set(), None
+        cur = {}
+        for line in open("/proc/cpuinfo"):
+            if ":" in line:
+                k, v = (x.strip() for x in line.split(":", 1))
+                cur[k] = v
+            elif cur:
+                phys.add(cur.get("physical id"))
+                cores.add((cur.get("physical id"), cur.get("core id")))
+                model = model or cur.get("model name")
+                cur = {}
+        info.update({"sockets": len(phys), "physical_cores": len(cores), "model": model})
+    except Exception:
+        pass
+    return info
 
 
 def main():
@@ -384,7 +439,8 @@ def main():
         r = bench_small_batch(nat, g)
         log(f"small_batch {r}")
         secondary["sgemm_32x768x4096"] = {
-            "value": round(r["gbs"], 1), "unit": "GB/s", "tflops": round(r["tflops"], 2),
+            "value": round(r["gbs"], 1), "unit": "GB/s", "hot_cache_gbs": round(r["gbs_hot"], 1),
+            "tflops": round(r["tflops"], 2),
             "us": round(r["us"], 2),
             "roofline": roofline("hbm", r["gbs"], load_traffic("sgemm_32x768x4096"))}
     if want("linear_sigmoid"):
@@ -411,6 +467,7 @@ def main():
         log(f"rowops {r}")
         for k, v in r.items():
             secondary[f"{k}_4096x8192"] = {"value": round(v["gbs"], 1), "unit": "GB/s",
+                                           "hot_cache_gbs": round(v["gbs_hot"], 1),
                                            "us": round(v["us"], 2),
                                            "roofline": roofline("hbm", v["gbs"],
                                                                 load_traffic(f"{k}_4096x8192"))}
@@ -418,7 +475,8 @@ def main():
         r = bench_reductions(nat, g)
         log(f"reductions {r}")
         for k, v in r.items():
-            e = {"value": round(v["gbs"], 1), "unit": "GB/s", "us": round(v["us"], 2),
+            e = {"value": round(v["gbs"], 1), "unit": "GB/s",
+                 "hot_cache_gbs": round(v["gbs_hot"], 1), "us": round(v["us"], 2),
                  "roofline": roofline("hbm", v["gbs"], load_traffic(f"{k}_64M"))}
             if "index_ok" in v:
                 e["index_ok"] = v["index_ok"]
