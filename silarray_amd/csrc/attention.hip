@@ -82,32 +82,6 @@ struct attn_args {
   int64_t sq_o, sq_i, sk_o, sk_i, sv_o, sv_i, so_o, so_i;
 };
 
-// Max and sum over the 16 lanes of a DPP row (the lanes that share a row of
-// S): quad swaps, then the half-row and row mirrors.  Every lane ends with
-// the same value (each step combines a pair of lanes symmetrically).
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp<0xB1>(v));   // quad_perm [1, 0, 3, 2]
-  v = fmaxf(v, dpp<0x4E>(v));   // quad_perm [2, 3, 0, 1]
-  v = fmaxf(v, dpp<0x141>(v));  // row_half_mirror
-  return fmaxf(v, dpp<0x140>(v));  // row_mirror
-}
-__device__ __forceinline__ float row16_sum(float v) {
-  v += dpp<0xB1>(v);
-  v += dpp<0x4E>(v);
-  v += dpp<0x141>(v);
-  return v + dpp<0x140>(v);
-}
-
-// e^x as 2^(x log2 e) on v_exp_f32: relative error about |x| 2^-24 from the
-// product's rounding, far inside the tolerance of the fused path.
-__device__ __forceinline__ float exp_fast(float x) {
-  return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
-}
-
 __device__ __forceinline__ float4 ld4u(const float *p, bool vec) {
   if (vec) return *reinterpret_cast<const float4 *>(p);
   return make_float4(p[0], p[1], p[2], p[3]);
@@ -137,6 +111,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
   const int row0 = blockIdx.x * kBQ + rg * 16;    // this wavefront's first query row
   const int row = row0 + c;                       // the query row of this lane
   const int Sq = a.Sq, Sk = a.Sk;
+  const float scale2 = a.scale * 1.4426950408889634f;  // scale * log2(e)
 
   // Q fragments: lane (c, q) holds Q[row][16 g + 4 q .. + 3] for each group
   // g (rows past Sq read row Sq - 1 and are never stored).
@@ -226,15 +201,16 @@ __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
 
     // Online softmax of this lane's row over the half: the row's 32 keys are
     // the 8 registers here and in lanes c + 16, c + 32, c + 48.  Scores are
-    // acc * scale (the unfused product's rounding); e^(s - m) is taken as
-    // 2^((s - m) log2 e) on v_exp_f32 (relative error about |s - m| 2^-24).
+    // kept in the base-2 domain, x = acc * (scale log2 e), so e^(s - m) is
+    // one v_exp_f32 of x - m (relative error about |x - m| 2^-24); m is the
+    // running maximum of x.
     float v[2][4];
     float rm = -INFINITY;
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float x = st[jb][r] * a.scale;
+        float x = st[jb][r] * scale2;
         if (!full && key0 + kbase + 16 * jb + 4 * q + r >= Sk) x = -INFINITY;
         v[jb][r] = x;
         rm = fmaxf(rm, x);
@@ -243,7 +219,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
     rm = fmaxf(rm, __shfl_xor(rm, 32, kWave));
     const float mn = fmaxf(m, rm);
     const bool none = mn == -INFINITY;  // no finite score in this row yet
-    const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f((m - mn) * 1.4426950408889634f);
+    const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
     float4 p[2];
     float rs = 0.0f;
 #pragma unroll
@@ -251,7 +227,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
       float e[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        e[r] = none ? 0.0f : __builtin_amdgcn_exp2f((v[jb][r] - mn) * 1.4426950408889634f);
+        e[r] = none ? 0.0f : __builtin_amdgcn_exp2f(v[jb][r] - mn);
         rs += e[r];
       }
       p[jb] = make_float4(e[0], e[1], e[2], e[3]);
@@ -293,8 +269,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
   if (kh == 1 || row >= Sq) return;
   const float m1 = X[(D / 4) * kWave + lane], l1 = X[(D / 4 + 1) * kWave + lane];
   const float mm = fmaxf(m, m1);
-  const float e0 = mm == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m - mm) * 1.4426950408889634f);
-  const float e1 = mm == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m1 - mm) * 1.4426950408889634f);
+  const float e0 = mm == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mm);
+  const float e1 = mm == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1 - mm);
   const float lt = l * e0 + l1 * e1;
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
   float *orow = O + int64_t(row) * a.ldo + 4 * q;
