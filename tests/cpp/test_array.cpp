@@ -613,6 +613,37 @@ TEST_CASE("conv2d: same padding closed form and the 1x1 kernel as a product") {
                     "array: conv2d requires a 4D NHWC input and a 4D OHWI weight.");
 }
 
+TEST_CASE("conv2d inside an eval graph: strided input view, relu and a channel bias after it") {
+  // The input is an H <-> W transposed view (strides, no copy) that the
+  // lowering makes contiguous; the result feeds a fused elementwise tail.
+  const size_t N = 2, H = 5, W = 6, Ci = 4, K = 3, Co = 5;
+  auto base = random({N, W, H, Ci}) - 0.5f;
+  auto w = random({Co, K, K, Ci}) - 0.5f;
+  auto b = random({Co}) - 0.5f;
+  eval(base, w, b);
+  auto xin = base.permute({0, 2, 1, 3});  // {N, H, W, Ci}
+  CHECK(xin.shape() == (shape_type{N, H, W, Ci}));
+  auto y = xin.conv2d(w, K).relu() + b;
+  eval(y);
+  float worst = 0.0f;
+  for (size_t n = 0; n < N; n++)
+    for (size_t i = 0; i < H; i++)
+      for (size_t j = 0; j < W; j++)
+        for (size_t o = 0; o < Co; o++) {
+          double acc = 0.0;
+          for (size_t kh = 0; kh < K; kh++)
+            for (size_t kw = 0; kw < K; kw++) {
+              const long ih = long(i) + long(kh) - 1, iw = long(j) + long(kw) - 1;
+              if (ih < 0 || iw < 0 || ih >= long(H) || iw >= long(W)) continue;
+              for (size_t c = 0; c < Ci; c++)
+                acc += double(base.at({n, size_t(iw), size_t(ih), c})) * double(w.at({o, kh, kw, c}));
+            }
+          const double ref = std::max(acc, 0.0) + double(b.at(o));
+          worst = std::max(worst, float(std::abs(ref - double(y.at({n, i, j, o})))));
+        }
+  CHECK(worst <= 1e-5f);
+}
+
 TEST_CASE("large arrays round-trip through pinned host mirrors") {
   // 4 MiB: above the size from which host mirrors are pinned
   const size_t n = size_t(1) << 20;
