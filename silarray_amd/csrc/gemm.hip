@@ -1429,19 +1429,12 @@ struct plan {
   int tail_splits = 1;
 };
 
-// Shape heuristic: a cost model calibrated on MI355X sweeps of the 8192^3,
-// 4096^3, 2048^3, linear_sigmoid 256x4096x4096 and transformer-projection
-// shapes.  For each candidate (tile, K splits):
-//   time = flops / (peak * eff[tile] * fill * klen / (klen + k0[tile]))
-//          + splits > 1 ? (splits * M * N * 8 bytes) / 5 TB/s + 4 us : 0
-// eff is the tile's sustained fraction of fp32 MFMA peak on large shapes,
-// fill = min(1, workgroups / full[tile]) (two waves per SIMD are needed to
-// hide load and barrier latency; the 64x64 tile, one 32x32 accumulator per
-// wave, needs twice the workgroups), use = the share of the padded tile area
-// that lies inside C, k0 the per-workgroup fixed cost expressed in units of
-// K, and the split term the partial tiles' HBM round trip plus the reduce
-// launch.  M <= 32 uses the 32x128 tile with enough K splits for
-// ~256 workgroups.
+// Shape heuristic (choose_plan): a cost model of each candidate tile and K
+// split -- workgroup rounds per CU, the tile's sustained MFMA efficiency,
+// occupancy, a K-loop ramp, a per-K-step latency floor and the split-K
+// partial pass -- calibrated on MI355X sweeps (8192^3, 4096^3, 2048^3,
+// linear_sigmoid 256x4096x4096, transformer projections, small M <= 512
+// products).  M <= 32 with batch 1 goes to the small-M kernel.
 // The 32x128 tile for M <= 32, K split for about 256 workgroups.
 plan small_m_tiles(int64_t M, int64_t N, int64_t K, int64_t batch) {
   plan p{TILE_32x128, 1};
@@ -1469,39 +1462,50 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dtl_ok) {
   // workgroups, min(that, occupancy) of them at once; a SIMD holding a
   // single wavefront reaches kSingleWave of the rate it reaches with two or
   // more.  eff is the fraction of fp32 MFMA peak each tile reaches at large
-  // K, and the K loop reaches half its rate at klen = kK0.  Split-K adds the
-  // partial-sum pass: one launch plus (splits + 1) M x N fp32 passes, whose
-  // partials mostly come back from the last-level cache.  Fitted to a
-  // tile/split sweep of square and transformer-block shapes on MI355X.
+  // K, and the K loop reaches half its rate at klen = kK0.  A workgroup
+  // also takes at least lat per 16-deep K step (one global -> LDS round trip
+  // that nothing else hides when a CU holds few workgroups: the floor of
+  // small products).  Split-K adds the partial-sum pass: a launch, (splits +
+  // 1) M x N fp32 passes and a per-plane latency.  Fitted to tile/split
+  // sweeps of square, transformer-block and small (M <= 512) shapes on
+  // MI355X.
   struct cand {
     int tile, bm, bn, bk, waves, occupancy;
-    double eff;
+    double eff, lat;
   };
   // The 128x64 tile runs the LDS-direct kernel when the operands allow it
   // (fitted 0.82 of peak at three workgroups per CU on the 2048-row
   // transformer and square shapes), the register-staged one otherwise.
   const bool dtl64 = dtl_ok && M % 128 == 0 && N % 64 == 0;
-  const cand cands[] = {{TILE_256x256, 256, 256, 16, 8, 1, 0.87},
-                        {TILE_128x128, 128, 128, 16, 4, 3, 0.84},
-                        {TILE_128x64, 128, 64, 16, 4, dtl64 ? 3 : 5, dtl64 ? 0.82 : 0.75},
-                        {TILE_64x64, 64, 64, 16, 4, 8, 0.64}};
-  constexpr double kK0 = 64.0, kSingleWave = 0.76, kReduceBw = 2.0e13, kLaunch = 4.0e-6;
+  const cand cands[] = {{TILE_256x256, 256, 256, 16, 8, 1, 0.87, 1.1e-6},
+                        {TILE_128x128, 128, 128, 16, 4, 3, 0.84, 1.1e-6},
+                        {TILE_128x64, 128, 64, 16, 4, dtl64 ? 3 : 5, dtl64 ? 0.82 : 0.75, 0.57e-6},
+                        {TILE_64x64, 64, 64, 16, 4, 8, 0.64, 0.47e-6}};
+  constexpr double kK0 = 64.0, kSingleWave = 0.76, kLaunch = 4.0e-6;
   const double rate_cu = 157.3e12 / 256.0;
+  auto round_time = [&](const cand &cd, int64_t nwg, double klen) {
+    const int64_t per_cu = cdiv(nwg, 256);
+    const int64_t conc = per_cu < cd.occupancy ? per_cu : cd.occupancy;
+    const double per_simd = double(conc) * cd.waves / 4.0;
+    const double f = per_simd >= 2.0 ? 1.0 : per_simd >= 1.0 ? kSingleWave
+                                                              : kSingleWave * per_simd;
+    const double t = double(per_cu) * 2.0 * cd.bm * cd.bn * klen /
+                     (rate_cu * cd.eff * f * (klen / (klen + kK0)));
+    const double floor_t = double(cdiv(per_cu, conc)) * (klen / 16.0) * cd.lat;
+    return t > floor_t ? t : floor_t;
+  };
+  auto sum_time = [](int sp, int64_t rows, int64_t cols) {
+    return 2.0e-6 + double(sp + 1) * double(rows) * double(cols) * 4.0 / 5.0e12 + 0.25e-6 * sp;
+  };
   plan best{TILE_128x128, 1};
   double best_t = 1e30;
   for (const cand &cd : cands) {
-    for (int sp : {1, 2, 4, 8}) {
-      if (sp > 1 && (batch != 1 || K / sp < 128)) continue;
+    for (int sp : {1, 2, 4, 8, 16}) {
+      if (sp > 1 && (batch != 1 || K / sp < 64)) continue;
       const int64_t wg = tiles(cd.bm, cd.bn) * sp;
       const double klen = double(cdiv(cdiv(K, sp), cd.bk) * cd.bk);
-      const int64_t per_cu = cdiv(wg, 256);
-      const double conc = double(per_cu < cd.occupancy ? per_cu : cd.occupancy);
-      const double per_simd = conc * cd.waves / 4.0;
-      const double f = per_simd >= 2.0 ? 1.0 : per_simd >= 1.0 ? kSingleWave
-                                                                : kSingleWave * per_simd;
-      double t = double(per_cu) * 2.0 * cd.bm * cd.bn * klen /
-                 (rate_cu * cd.eff * f * (klen / (klen + kK0)));
-      if (sp > 1) t += double(sp + 1) * double(M) * double(N) * 4.0 / kReduceBw + kLaunch;
+      double t = round_time(cd, wg, klen);
+      if (sp > 1) t += sum_time(sp, M, N);
       if (t < best_t * 0.999) {
         best_t = t;
         best = plan{cd.tile, sp};
@@ -1519,22 +1523,13 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dtl_ok) {
       if (wg <= 256 || wg % 256 == 0) continue;
       const int64_t rows_main = (wg / 256) * 256 / tn;
       if (rows_main < 1 || rows_main >= tm) continue;
-      auto round_time = [&](int64_t nwg, double klen) {
-        const int64_t per_cu = cdiv(nwg, 256);
-        const double conc = double(per_cu < cd.occupancy ? per_cu : cd.occupancy);
-        const double per_simd = conc * cd.waves / 4.0;
-        const double f = per_simd >= 2.0 ? 1.0 : per_simd >= 1.0 ? kSingleWave
-                                                                  : kSingleWave * per_simd;
-        return double(per_cu) * 2.0 * cd.bm * cd.bn * klen /
-               (rate_cu * cd.eff * f * (klen / (klen + kK0)));
-      };
-      const double t_main = round_time(rows_main * tn, double(cdiv(K, cd.bk) * cd.bk));
+      const double t_main = round_time(cd, rows_main * tn, double(cdiv(K, cd.bk) * cd.bk));
       const int64_t mt = M - rows_main * cd.bm;
       for (int sp : {1, 2, 3, 4, 6, 8}) {
         if (sp > 1 && K / sp < 128) continue;
         const double klen = double(cdiv(cdiv(K, sp), cd.bk) * cd.bk);
-        double t = t_main + round_time(cdiv(mt, cd.bm) * tn * sp, klen) + kLaunch;
-        if (sp > 1) t += double(sp + 1) * double(mt) * double(N) * 4.0 / kReduceBw + kLaunch;
+        double t = t_main + round_time(cd, cdiv(mt, cd.bm) * tn * sp, klen) + kLaunch;
+        if (sp > 1) t += sum_time(sp, mt, N);
         if (t < best_t * 0.97) {
           best_t = t;
           best = plan{cd.tile, 1, static_cast<int>(mt), sp};
