@@ -301,21 +301,26 @@ GRAPH_BENCH = ROOT / "silarray_amd" / "bench" / "bench_graph"
 REF_TRANSFORMER_MS = {(256, 512): 1.53, (256, 768): 2.30, (256, 1024): 2.93, (512, 1024): 5.32}
 # The reference's training step on an M1 Pro (bench/README.md:187-188), by batch.
 REF_TRAIN_MS = {64: 1.11, 128: 1.51}
+# The reference's MNIST benchmarks on the M1 Pro, sil-gpu column
+# (bench/README.md:205-220): ms.
+REF_MNIST_MS = {"classifier_train_epoch_ms": 283.83, "classifier_inference_ms": 0.920,
+                "autoencoder_train_epoch_ms": 1080.0, "autoencoder_inference_ms": 8.65}
 
 
 def bench_graphs(timeout: float = 300.0) -> list[dict]:
     """Whole sil::eval graphs through the C++ front end (bench_graph): the
     B4 S512 d768 H12 encoder block, the reference's single-head transformer
     and linear_sigmoid MLP benchmarks, and the 20-op affine chain at the API
-    level, and host <-> HBM copies of a 256 MiB array through its pinned host
-    mirror.  Each iteration is eval + synchronize, as the reference times it."""
+    level, host <-> HBM copies of a 256 MiB array through its pinned host
+    mirror, and the reference's MNIST classifier and autoencoder benchmarks.
+    Each iteration is eval + synchronize, as the reference times it."""
     import subprocess
 
     if not GRAPH_BENCH.exists():
         raise RuntimeError(f"{GRAPH_BENCH} is not built (run __graft_entry__.build())")
     out = []
     for argv in (["encoder", "10"], ["transformer"], ["mlp"], ["train"],
-                 ["chain", str(64 << 20), "20"], ["transfer", str(64 << 20), "10"]):
+                 ["chain", str(64 << 20), "20"], ["transfer", str(64 << 20), "10"], ["mnist"]):
         log(f"bench_graph {' '.join(argv)}")
         proc = subprocess.run([str(GRAPH_BENCH), *argv], capture_output=True, text=True,
                               timeout=timeout)
@@ -512,6 +517,14 @@ def main():
                 key = f"mlp_linear_sigmoid_batch{r['batch']}"
             elif w == "train_step":
                 key = f"train_step_768x2048_batch{r['batch']}"
+            elif w == "mnist":
+                for k, ref in REF_MNIST_MS.items():
+                    secondary[f"mnist_{k[:-3]}"] = {
+                        "value": r[k], "unit": "ms", "higher_is_better": False,
+                        "reference_m1pro_ms": ref,
+                        "data": "synthetic images in [0,1) and labels, MNIST shapes "
+                                "(60000 train, 10000 test)"}
+                continue
             elif w == "transfer":
                 secondary["host_transfer_256MiB"] = {
                     "value": r["h2d_gbs"], "unit": "GB/s (host to HBM)", "d2h_gbs": r["d2h_gbs"],

@@ -18,6 +18,16 @@
 //                                             array through its (pinned) host
 //                                             mirror: upload after a host
 //                                             write, download on a host read
+//   bench_graph mnist [train test]            the reference's MNIST classifier
+//                                             (784-50-10) and autoencoder
+//                                             (784-512-256-64-256-512-784)
+//                                             benchmarks: one training epoch
+//                                             (batches of 100 sliced from the
+//                                             resident set, SGD, one eval per
+//                                             batch) and inference on the test
+//                                             set; synthetic images in [0, 1)
+//                                             and labels (the MNIST files are
+//                                             not part of the reference)
 //   bench_graph train-dump B D H DIR          one training step on seeded
 //                                             inputs, written to DIR (raw
 //                                             float32) for the parity test
@@ -173,6 +183,157 @@ double transformer_ms(size_t seq, size_t d_model, size_t d_ff, int reps) {
     eval(out);
     synchronize();
   });
+}
+
+// The reference's MNIST benchmarks (bench/mnist/bench_classifier.cpp:33-73,
+// 252-264; bench/mnist/bench_autoencoder.cpp:39-80, 243-256), with the same
+// graphs, batch, learning rates and evaluation points, on synthetic data of
+// the MNIST shapes.  Each figure is the wall time of one timed run after one
+// untimed run (the reference's measure(0, fn, 0, 1) runs the epoch once to
+// calibrate, then once timed).
+struct mnist_result {
+  double classifier_train_ms, classifier_infer_ms, autoencoder_train_ms, autoencoder_infer_ms;
+  float classifier_mse_first, classifier_mse_last;
+};
+
+template <typename F>
+double once_ms(F fn) {
+  fn();  // untimed
+  synchronize();
+  const auto t0 = std::chrono::steady_clock::now();
+  fn();
+  synchronize();
+  return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+}
+
+mnist_result mnist_bench(size_t n_train, size_t n_test) {
+  constexpr size_t D = 784, H = 50, C = 10, batch = 100;
+  rng g(31);
+  std::vector<float> img_train(n_train * D), img_test(n_test * D), labels(n_train);
+  for (auto &v : img_train) v = 0.5f * (g.uniform() + 1.0f);
+  for (auto &v : img_test) v = 0.5f * (g.uniform() + 1.0f);
+  for (auto &v : labels) v = float(g.next() % C);
+  mnist_result r{};
+  {  // classifier training (bench_classifier.cpp:33-73)
+    const float lr = 0.5f;
+    auto W1 = (random({D, H}) * 2.0f - 1.0f) * (1.0f / std::sqrt(float(D)));
+    auto b1 = zeros<float>({H});
+    auto W2 = (random({H, C}) * 2.0f - 1.0f) * (1.0f / std::sqrt(float(H)));
+    auto b2 = zeros<float>({C});
+    auto two = array<float>(2.0f);
+    auto inv_n = array<float>(1.0f / float(batch * C));
+    auto neg_lr = array<float>(-lr);
+    auto all_x = array<float>({n_train, D}, img_train.data());
+    auto all_labels = array<float>({n_train}, labels.data());
+    auto all_Y = all_labels.template one_hot<float>(C);
+    eval(W1, W2, all_x, all_Y);
+    synchronize();
+    float mse_first = 0.0f, mse_last = 0.0f;
+    auto epoch = [&] {
+      for (size_t i = 0; i + batch <= n_train; i += batch) {
+        auto x = all_x.slice(i, batch);
+        auto Y = all_Y.slice(i, batch);
+        auto n1 = x.linear(W1, b1);
+        auto o1 = n1.sigmoid();
+        auto n2 = o1.linear(W2, b2);
+        auto o2 = n2.sigmoid();
+        auto dout = (o2 - Y) * two * inv_n;
+        dout = n2.sigmoid_backward(dout);
+        auto dW2 = o1.transpose().dot(dout);
+        auto db2 = dout.sum(0);
+        auto dout1 = dout.dot(W2.transpose());
+        dout1 = n1.sigmoid_backward(dout1);
+        auto dW1 = x.transpose().dot(dout1);
+        auto db1 = dout1.sum(0);
+        W1 = W1 + dW1 * neg_lr;
+        b1 = b1 + db1 * neg_lr;
+        W2 = W2 + dW2 * neg_lr;
+        b2 = b2 + db2 * neg_lr;
+        eval(W1, b1, W2, b2);
+      }
+    };
+    auto mse = [&] {  // squared error on the first batch
+      auto x = all_x.slice(0, batch);
+      auto d = x.linear(W1, b1).sigmoid().linear(W2, b2).sigmoid() - all_Y.slice(0, batch);
+      return float((d * d).sum()) / float(batch * C);
+    };
+    mse_first = mse();
+    r.classifier_train_ms = once_ms(epoch);
+    mse_last = mse();
+    r.classifier_mse_first = mse_first;
+    r.classifier_mse_last = mse_last;
+  }
+  {  // classifier inference (bench_classifier.cpp:252-264)
+    auto W1 = random({D, H});
+    auto b1 = zeros<float>({H});
+    auto W2 = random({H, C});
+    auto b2 = zeros<float>({C});
+    auto x = array<float>({n_test, D}, img_test.data());
+    eval(W1, W2, x);
+    synchronize();
+    r.classifier_infer_ms = median_ms(20, [&] {
+      auto o1 = x.linear(W1, b1).sigmoid();
+      auto o2 = o1.linear(W2, b2).sigmoid();
+      eval(o2);
+    });
+  }
+  constexpr size_t L[] = {784, 512, 256, 64, 256, 512, 784};
+  constexpr size_t NL = 6;
+  {  // autoencoder training (bench_autoencoder.cpp:39-80)
+    const float lr = 0.01f;
+    array<float> W[NL], b[NL];
+    for (size_t l = 0; l < NL; l++) {
+      W[l] = random({L[l], L[l + 1]}) * (2.0f / std::sqrt(float(L[l])));
+      b[l] = zeros<float>({L[l + 1]});
+      eval(W[l]);
+    }
+    auto two = array<float>(2.0f);
+    auto inv_n = array<float>(1.0f / float(batch * 784));
+    auto neg_lr = array<float>(-lr);
+    auto all_x = array<float>({n_train, 784}, img_train.data());
+    eval(all_x);
+    synchronize();
+    r.autoencoder_train_ms = once_ms([&] {
+      for (size_t i = 0; i + batch <= n_train; i += batch) {
+        auto x = all_x.slice(i, batch);
+        array<float> net[NL], out[NL];
+        auto h = x;
+        for (size_t l = 0; l < NL; l++) {
+          net[l] = h.linear(W[l], b[l]);
+          out[l] = net[l].sigmoid();
+          h = out[l];
+        }
+        auto dout = (h - x) * two * inv_n;
+        for (int l = int(NL) - 1; l >= 0; l--) {
+          dout = net[l].sigmoid_backward(dout);
+          auto &input = (l > 0) ? out[l - 1] : x;
+          auto dW = input.transpose().dot(dout);
+          auto db = dout.sum(0);
+          if (l > 0) dout = dout.dot(W[l].transpose());
+          W[l] = W[l] + dW * neg_lr;
+          b[l] = b[l] + db * neg_lr;
+        }
+        eval(W[0], b[0], W[1], b[1], W[2], b[2], W[3], b[3], W[4], b[4], W[5], b[5]);
+      }
+    });
+  }
+  {  // autoencoder inference (bench_autoencoder.cpp:243-256)
+    array<float> W[NL], b[NL];
+    for (size_t l = 0; l < NL; l++) {
+      W[l] = random({L[l], L[l + 1]});
+      b[l] = zeros<float>({L[l + 1]});
+      eval(W[l]);
+    }
+    auto x = array<float>({n_test, 784}, img_test.data());
+    eval(x);
+    synchronize();
+    r.autoencoder_infer_ms = median_ms(20, [&] {
+      auto h = x;
+      for (size_t l = 0; l < NL; l++) h = h.linear(W[l], b[l]).sigmoid();
+      eval(h);
+    });
+  }
+  return r;
 }
 
 // The reference's MLP inference benchmark (bench/composite/bench_mlp.cpp:28-41):
@@ -402,6 +563,20 @@ int main(int argc, char **argv) {
       }
       return 0;
     }
+    if (mode == "mnist") {
+      const size_t n_train = argc > 2 ? std::strtoull(argv[2], nullptr, 10) : 60000;
+      const size_t n_test = argc > 3 ? std::strtoull(argv[3], nullptr, 10) : 10000;
+      if (n_train < 100 || n_test < 1) throw std::runtime_error("need >= 100 training images");
+      const auto r = mnist_bench(n_train, n_test);
+      std::printf("{\"workload\": \"mnist\", \"train_images\": %zu, \"test_images\": %zu, "
+                  "\"classifier_train_epoch_ms\": %.3f, \"classifier_inference_ms\": %.4f, "
+                  "\"autoencoder_train_epoch_ms\": %.3f, \"autoencoder_inference_ms\": %.4f, "
+                  "\"classifier_mse_first_batch\": [%.6f, %.6f]}\n",
+                  n_train, n_test, r.classifier_train_ms, r.classifier_infer_ms,
+                  r.autoencoder_train_ms, r.autoencoder_infer_ms, r.classifier_mse_first,
+                  r.classifier_mse_last);
+      return 0;
+    }
     if (mode == "train-dump") {
       if (argc < 6) throw std::runtime_error("train-dump needs B D H DIR");
       const size_t B = std::strtoull(argv[2], nullptr, 10), D = std::strtoull(argv[3], nullptr, 10),
@@ -425,7 +600,7 @@ int main(int argc, char **argv) {
       return 0;
     }
     std::fprintf(stderr,
-                 "usage: bench_graph chain|transfer|encoder|encoder-dump|transformer|mlp|train|train-dump "
+                 "usage: bench_graph chain|transfer|mnist|encoder|encoder-dump|transformer|mlp|train|train-dump "
                  "...\n");
     return 2;
   } catch (std::exception &ex) {

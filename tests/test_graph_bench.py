@@ -172,3 +172,21 @@ def test_transfer_reports_json():
     rec = json.loads(out.strip().splitlines()[-1])
     assert rec["workload"] == "transfer" and rec["check"] == 1
     assert rec["h2d_ms"] > 0 and rec["d2h_ms"] > 0
+
+
+@pytest.mark.gpu
+def test_mnist_reports_json():
+    """The reference's MNIST classifier and autoencoder loops on a small
+    synthetic set: every phase runs and the classifier's squared error on
+    its first batch goes down over the epoch (the labels are random, so
+    the network can only fit them as noise, which SGD at lr 0.5 does)."""
+    print("bench_graph mnist (2000 train, 500 test)", flush=True)
+    out = subprocess.run([str(_bench()), "mnist", "2000", "500"], capture_output=True,
+                         text=True, timeout=120, check=True).stdout
+    rec = json.loads(out.strip().splitlines()[-1])
+    assert rec["workload"] == "mnist"
+    for k in ("classifier_train_epoch_ms", "classifier_inference_ms",
+              "autoencoder_train_epoch_ms", "autoencoder_inference_ms"):
+        assert rec[k] > 0, k
+    first, last = rec["classifier_mse_first_batch"]
+    assert np.isfinite(first) and np.isfinite(last) and last < first
