@@ -413,7 +413,9 @@ def _gemm_case(native, oracle, M, N, K, ta=False, tb=False, epi=0, bias_len=0, s
 ROUTING_SHAPES = [(1, 16, 3), (15, 16, 16), (16, 16, 16), (17, 50, 17), (32, 768, 4096),
                   (33, 65, 15), (63, 64, 784), (64, 64, 64), (96, 4096, 8), (97, 1, 17),
                   (100, 768, 784), (128, 128, 16), (256, 512, 130), (1, 4096, 4096),
-                  (64, 1, 300), (3, 5, 1)]
+                  (64, 1, 300), (3, 5, 1),
+                  # small products the plan splits 8 or 16 ways along K
+                  (256, 512, 2048), (128, 768, 2048), (64, 2048, 768), (256, 512, 256)]
 
 
 @pytest.mark.parametrize("M,N,K", ROUTING_SHAPES)
