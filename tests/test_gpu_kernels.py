@@ -820,6 +820,28 @@ def test_attention_fused(native, B, H, Sq, Sk, D, layout):
     assert np.isfinite(Ov).all() and err <= tol, (err, tol)
 
 
+def test_attention_large_scores(native):
+    """Scores of several hundred (q, k ~ N(0, 8)): the online softmax's
+    running-max subtraction keeps every exponent finite and the rows close to
+    one-hot; the float64 bar widens by the scores' rounding, |s| * 2^-24."""
+    announce("attention large scores")
+    B, H, S, D = 1, 3, 97, 64
+    g = rng(5300)
+    Q = (g.normal(0, 8, (B, H, S, D))).astype(np.float32)
+    K = (g.normal(0, 8, (B, H, S, D))).astype(np.float32)
+    V = g.normal(0, 1, (B, H, S, D)).astype(np.float32)
+    scale = float(np.float32(1.0 / np.sqrt(D)))
+    dQ, dK, dV, dO = up(native, Q), up(native, K), up(native, V), empty(native, Q.size)
+    st = (H * S * D, S * D)
+    native.attention(S, S, D, scale, dQ, D, dK, D, dV, D, dO, D, B, H, st, st, st, st)
+    out = down(native, dO, Q.shape)
+    ref = _attention_f64(Q, K, V, scale)
+    smax = np.abs(np.einsum("bhqd,bhkd->bhqk", Q.astype(np.float64), K.astype(np.float64))).max() * scale
+    err = np.abs(out.astype(np.float64) - ref).max()
+    tol = (2e-5 * np.sqrt(S) + 4 * smax * 2.0 ** -24) * np.abs(V).max()
+    assert np.isfinite(out).all() and err <= tol, (err, tol, smax)
+
+
 def test_attention_no_keys_gives_zero(native):
     announce("attention Sk=0")
     ob = np.full((2, 16, 32), np.nan, np.float32)
