@@ -2000,40 +2000,51 @@ int silgpu_conv2d_f32(const float *d_in, const float *d_w, float *d_out, int64_t
                          static_cast<int>(C_out), c->stream);
   const bool vec = C_in % 4 == 0 && aligned16(d_in) && aligned16(d_w);
   if (vec && C_in % 16 == 0 && M % 128 == 0 && C_out % 64 == 0) {
-    // Three 128 x 64 workgroups fit a CU.  When the tiles fill whole rounds
-    // of all CUs plus a thin last round, the tile rows of that last round
-    // run as a second launch split along K (one piece per CU at most) and a
-    // split sum, instead of a round of a few workgroups at full depth.
+    // Three 128 x 64 workgroups fit a CU.  Between one and two tiles per CU
+    // (two on some CUs, one on others) the K range is split in two, so the
+    // pieces fill three rounds.  When the pieces fill whole rounds of all
+    // CUs plus a thin last round, the tile rows of that last round run as a
+    // second launch split further along K (one piece per CU at most) with
+    // its own split sum, instead of a round of a few workgroups at full
+    // depth.
     const int BK = C_in % 32 == 0 ? 32 : 16;
     const int64_t tiles_n = C_out / 64, tiles_m = M / 128, tiles = tiles_m * tiles_n;
-    const int64_t slots = int64_t(c->cu_count) * 3, rem = tiles % slots;
+    const int64_t cus = c->cu_count, slots = cus * 3, kt = Kd / BK;
+    // (Measured: 88.5 -> 85.2 us at 16x28x28x128 -> 256, K = 1152; with K
+    // = 576 the halves are too short and the split sum costs more than the
+    // balance gains, 48.7 -> 56.6 us at 8x56x56x64 -> 128.)
+    const int gs = tiles > cus && 2 * tiles > slots && 4 * (2 * tiles) <= 5 * slots &&
+                           kt % 2 == 0 && Kd >= 1024
+                       ? 2 : 1;
+    const int64_t pieces = tiles * gs, rem = pieces % slots;
     int64_t rows_main = tiles_m;
     int splits = 1;
-    if (tiles > slots && rem > 0 && rem * 4 <= slots) {
-      const int64_t rem_rows = cdiv(rem, tiles_n), kt = Kd / BK;
+    if (pieces > slots && rem > 0 && rem * 4 <= slots) {
+      const int64_t rem_rows = cdiv(rem, tiles_n * gs);
       rows_main = tiles_m - rem_rows;
       for (int64_t sp = 2; sp <= kt; ++sp)
-        if (kt % sp == 0 && rem_rows * tiles_n * sp <= c->cu_count) splits = int(sp);
+        if (kt % sp == 0 && rem_rows * tiles_n * sp <= cus) splits = int(sp);
     }
-    auto conv = [&](const gemm_args &g, int sp) {
-      return BK == 32 ? launch_conv_dtl<32>(g, sp, c->stream) : launch_conv_dtl<16>(g, sp, c->stream);
+    auto conv = [&](gemm_args g, int sp) {
+      if (sp > 1) {
+        int rc = ensure_workspace(c, size_t(sp) * size_t(g.M) * size_t(C_out) * sizeof(float));
+        if (rc != SILGPU_OK) return rc;
+        g.ws = static_cast<float *>(c->workspace);
+      }
+      int rc = BK == 32 ? launch_conv_dtl<32>(g, sp, c->stream)
+                        : launch_conv_dtl<16>(g, sp, c->stream);
+      if (rc != SILGPU_OK || sp == 1) return rc;
+      return launch_split_sum(g, sp, c);
     };
     gemm_args main = a;
     main.M = static_cast<int>(rows_main * 128);
-    int rc = conv(main, 1);
+    int rc = conv(main, gs);
     if (rc != SILGPU_OK || rows_main == tiles_m) return rc;
     gemm_args tail = a;
     tail.cv_m0 = main.M;
     tail.M = static_cast<int>(M) - main.M;
     tail.C = d_out + int64_t(main.M) * C_out;
-    if (splits > 1) {
-      rc = ensure_workspace(c, size_t(splits) * size_t(tail.M) * size_t(C_out) * sizeof(float));
-      if (rc != SILGPU_OK) return rc;
-      tail.ws = static_cast<float *>(c->workspace);
-    }
-    rc = conv(tail, splits);
-    if (rc != SILGPU_OK || splits == 1) return rc;
-    return launch_split_sum(tail, splits, c);
+    return conv(tail, splits);
   }
   if (C_out <= 32)
     return vec ? launch_conv_cfg<64, 64, 2, 2, true>(a, c->stream)

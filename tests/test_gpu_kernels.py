@@ -863,7 +863,10 @@ def test_attention_no_keys_gives_zero(native):
 # the reference benchmark's three layers (bench/micro/bench_nn_ops.cpp:
 # 193-195) at full size; and shapes whose 128 x 64 tiles fill three rounds of
 # 256 CUs plus a thin last round, which runs as a second launch (split along
-# K into 9 pieces with BK 32 and 16, or unsplit).
+# K into 9 pieces with BK 32 and 16, or unsplit); between one and two tiles
+# per CU with K*K*C_in >= 1024 (the deep layer; BK 16 with K = 4, C_in = 80)
+# the K range is first split in two; (16, 28, 28, 48, 3, 256) stays unsplit (BK 16,
+# an odd number of K tiles).
 CONV_CASES = [(1, 8, 8, 3, 3, 16), (1, 5, 6, 4, 1, 5), (2, 9, 5, 6, 2, 40), (3, 4, 4, 1, 3, 1),
               (1, 5, 7, 2, 3, 37), (2, 6, 6, 64, 1, 33),
               (2, 8, 8, 16, 3, 64), (1, 16, 16, 48, 3, 128), (1, 8, 16, 32, 5, 64),
@@ -871,7 +874,8 @@ CONV_CASES = [(1, 8, 8, 3, 3, 16), (1, 5, 6, 4, 1, 5), (2, 9, 5, 6, 2, 40), (3, 
               (2, 7, 9, 16, 3, 32), (1, 6, 6, 8, 5, 12), (1, 13, 11, 20, 3, 70),
               (1, 3, 3, 2, 7, 3), (2, 8, 8, 16, 3, 60),
               (1, 224, 224, 3, 3, 32), (16, 56, 56, 64, 3, 128), (16, 28, 28, 128, 3, 256),
-              (16, 56, 56, 48, 3, 128), (1, 116, 256, 32, 3, 256)]
+              (16, 56, 56, 48, 3, 128), (1, 116, 256, 32, 3, 256), (16, 28, 28, 80, 4, 256),
+              (16, 28, 28, 48, 3, 256)]
 
 
 @pytest.mark.parametrize("N,H,W,Ci,K,Co", CONV_CASES)
