@@ -196,11 +196,13 @@ CONV_LAYERS = [("imagenet_first", 1, 224, 224, 3, 3, 32, 0.564),
                ("resnet_deep", 16, 28, 28, 128, 3, 256, 2.93)]
 
 
-def bench_conv2d(nat, g, reps=50):
+def bench_conv2d(nat, g, reps=50, layers=None):
     """Implicit-GEMM conv2d (stride 1, same padding) on the reference's
-    layers; flops = 2 N H W C_out K K C_in."""
+    layers (all, or the names in `layers`); flops = 2 N H W C_out K K C_in."""
     out = {}
     for name, N, H, W, Ci, K, Co, ref_ms in CONV_LAYERS:
+        if layers and name not in layers:
+            continue
         x = nat.DeviceBuffer.from_array(uniform(g, (N, H, W, Ci)))
         w = nat.DeviceBuffer.from_array(uniform(g, (Co, K, K, Ci)))
         y = nat.DeviceBuffer(N * H * W * Co * 4)
@@ -454,8 +456,9 @@ def main():
         secondary["linear_sigmoid_256x4096x4096"] = {
             "value": round(r["tflops"], 2), "unit": "TFLOP/s", "us": round(r["us"], 1),
             "roofline": roofline("mfma", r["tflops"], load_traffic("linear_sigmoid_256x4096x4096"))}
-    if want("conv2d"):
-        for k, v in bench_conv2d(nat, g).items():
+    conv_layers = {n for n, *_ in CONV_LAYERS if f"conv2d_{n}" in only}
+    if want("conv2d") or conv_layers:
+        for k, v in bench_conv2d(nat, g, layers=conv_layers or None).items():
             log(f"{k} {v}")
             traffic = load_traffic(v["traffic_key"])
             if v["hbm_bound"]:  # below the ridge (19.7 flop/B): priced against HBM
