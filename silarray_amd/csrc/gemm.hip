@@ -1414,7 +1414,8 @@ enum tile_cfg {
   TILE_128x64 = 4,
   TILE_256x256 = 5,
   // M <= 32 (batch 1, A not transposed): sgemm_skinny_k with 32Q columns per
-  // workgroup; TILE_SKINNY (the automatic choice) is Q = 1.
+  // workgroup; the automatic choice is TILE_SKINNY (Q = 1) or, for wide and
+  // deep products, TILE_SKINNY_Q2.
   TILE_SKINNY = 6,
   TILE_SKINNY_Q2 = 7,
   TILE_SKINNY_Q4 = 8
@@ -1447,11 +1448,18 @@ plan small_m_tiles(int64_t M, int64_t N, int64_t K, int64_t batch) {
   return p;
 }
 
+int skinny_splits(int64_t M, int64_t N, int64_t K, int Q);
+
 plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dtl_ok) {
   auto tiles = [&](int bm, int bn) { return cdiv(M, bm) * cdiv(N, bn) * batch; };
   // M <= 32: the small-M kernel (splits chosen at launch), or where it does
-  // not apply (batched, A transposed) the 32x128 tile.
-  if (M <= 32 && batch == 1) return plan{TILE_SKINNY, 0};
+  // not apply (batched, A transposed) the 32x128 tile.  Where 32-column
+  // groups would each walk 2048 or more rows of B in 128-byte pieces (wide N
+  // and deep K), 64-column groups with twice the K splits read 256-byte
+  // pieces: 19.8 -> 17.9 us at 8 x 4096 x 4096 on MI355X; at N 768..3072
+  // the 32-column groups measured ahead.
+  if (M <= 32 && batch == 1)
+    return plan{K / skinny_splits(M, N, K, 1) >= 2048 ? TILE_SKINNY_Q2 : TILE_SKINNY, 0};
   if (M <= 32) return small_m_tiles(M, N, K, batch);
   // Batched products with a short K loop (attention's Q K^T at head dim 64)
   // are bound by storing C, which the many small tiles overlap with other

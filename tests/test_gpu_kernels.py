@@ -597,6 +597,8 @@ SKINNY_CASES = [
     (31, 130, 100, 0, 1, 0, 3, 4), (5, 7, 15, 0, 0, 0, 0, 0), (16, 64, 1, 0, 0, 0, 0, 3),
     (17, 96, 333, 1, 0, 1, 0, 1), (32, 100, 200, 1, 2, 2, 1, 2), (3, 260, 1000, 0, 0, 2, 4, 0),
     (32, 4096, 64, 0, 0, 0, 0, 1), (8, 36, 4100, 1, 3, 0, 0, 0),
+    # wide and deep: the automatic plan takes 64-column groups (N odd: back to 32)
+    (8, 4096, 4096, 0, 0, 0, 0, 0), (4, 4097, 4096, 0, 0, 0, 0, 0), (16, 4096, 4096, 1, 0, 0, 0, 1),
 ]
 
 
