@@ -184,6 +184,19 @@ void oracle_sum_axis_f64(const float *x, int64_t outer, int64_t axis_len, int64_
     }
 }
 
+/* array.h:1574-1578 / 2309-2314: tmp.at(p) += at(pos) over the positions in
+ * row-major order, in float: each output sums its inputs in axis order. */
+void oracle_sum_axis_ref(const float *x, int64_t outer, int64_t axis_len, int64_t inner,
+                         float *out) {
+  for (int64_t j = 0; j < outer * inner; ++j) out[j] = 0.0f;
+  for (int64_t o = 0; o < outer; ++o)
+    for (int64_t a = 0; a < axis_len; ++a) {
+      const float *src = x + (o * axis_len + a) * inner;
+      float *dst = out + o * inner;
+      for (int64_t i = 0; i < inner; ++i) dst[i] += src[i];
+    }
+}
+
 void oracle_argmax_rows(const float *x, int64_t rows, int64_t cols, int32_t *out) {
   for (int64_t r = 0; r < rows; ++r) {
     const float *row = x + r * cols;

@@ -70,6 +70,10 @@ float oracle_max(const float *x, int64_t n);
 /* out[o*inner + i] = sum_a x[(o*axis_len + a)*inner + i] in double. */
 void oracle_sum_axis_f64(const float *x, int64_t outer, int64_t axis_len, int64_t inner,
                          double *out);
+/* The reference's float path for sum(axis) (include/array.h:1574-1578,
+ * 2309-2314): out[o*inner + i] accumulated in float, axis index ascending. */
+void oracle_sum_axis_ref(const float *x, int64_t outer, int64_t axis_len, int64_t inner,
+                         float *out);
 /* First index of the row maximum; NaN never wins (an all-NaN row gives 0). */
 void oracle_argmax_rows(const float *x, int64_t rows, int64_t cols, int32_t *out);
 /* The reference CPU loop verbatim in meaning (include/array.h:1728-1745):

@@ -45,6 +45,7 @@ _SIGS = {
     "oracle_min": (C.c_float, [_vp, _i64]),
     "oracle_max": (C.c_float, [_vp, _i64]),
     "oracle_sum_axis_f64": (None, [_vp, _i64, _i64, _i64, _vp]),
+    "oracle_sum_axis_ref": (None, [_vp, _i64, _i64, _i64, _vp]),
     "oracle_argmax_rows": (None, [_vp, _i64, _i64, _vp]),
     "oracle_argmax_rows_cpu_ref": (None, [_vp, _i64, _i64, _vp]),
     "oracle_softmax_rows_f64": (None, [_vp, _i64, _i64, _vp]),
@@ -190,6 +191,16 @@ def sum_axis_f64(x, axis):
     inner = int(np.prod(shape[axis + 1:])) if axis + 1 < len(shape) else 1
     out = np.empty(outer * inner, np.float64)
     _lib.oracle_sum_axis_f64(_p(x), outer, shape[axis], inner, _p(out))
+    return out.reshape(shape[:axis] + shape[axis + 1:])
+
+
+def sum_axis_ref(x, axis):
+    x = _f32(x)
+    shape = x.shape
+    outer = int(np.prod(shape[:axis])) if axis > 0 else 1
+    inner = int(np.prod(shape[axis + 1:])) if axis + 1 < len(shape) else 1
+    out = np.empty(outer * inner, np.float32)
+    _lib.oracle_sum_axis_ref(_p(x), outer, shape[axis], inner, _p(out))
     return out.reshape(shape[:axis] + shape[axis + 1:])
 
 

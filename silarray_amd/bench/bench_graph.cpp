@@ -31,6 +31,15 @@
 //   bench_graph train-dump B D H DIR          one training step on seeded
 //                                             inputs, written to DIR (raw
 //                                             float32) for the parity test
+//   bench_graph dot-dump M N K DIR            C = A.dot(B) through sil::array
+//                                             on uniform[-1, 1) inputs (the
+//                                             reference's SGEMM config,
+//                                             bench/micro/bench_sgemm.cpp:34);
+//                                             A, B and C written to DIR
+//   bench_graph chain-dump n DIR              the 20-node chain of `chain` on
+//                                             n uniform[-1, 1) floats, one
+//                                             sil::eval; x and y written to
+//                                             DIR
 //
 // Each timed iteration is sil::eval + wait, the reference's convention
 // (bench/bench_common.h:42-68); the median of `reps` iterations is reported
@@ -599,9 +608,41 @@ int main(int argc, char **argv) {
       std::printf("{\"dumped\": \"%s\"}\n", dir.c_str());
       return 0;
     }
+    if (mode == "dot-dump") {
+      if (argc < 6) throw std::runtime_error("dot-dump needs M N K DIR");
+      const size_t M = std::strtoull(argv[2], nullptr, 10), N = std::strtoull(argv[3], nullptr, 10),
+                   K = std::strtoull(argv[4], nullptr, 10);
+      if (M == 0 || N == 0 || K == 0) throw std::runtime_error("M, N and K must be >= 1");
+      const std::string dir = argv[5];
+      rng g(2028);
+      auto A = filled({M, K}, g, 1.0f, true);
+      auto B = filled({K, N}, g, 1.0f, true);
+      auto C = A.dot(B);
+      eval(C);
+      write_raw(dir + "/A.bin", A);
+      write_raw(dir + "/B.bin", B);
+      write_raw(dir + "/C.bin", C);
+      std::printf("{\"dumped\": \"%s\"}\n", dir.c_str());
+      return 0;
+    }
+    if (mode == "chain-dump") {
+      if (argc < 4) throw std::runtime_error("chain-dump needs n DIR");
+      const size_t n = std::strtoull(argv[2], nullptr, 10);
+      if (n == 0) throw std::runtime_error("n must be >= 1");
+      const std::string dir = argv[3];
+      rng g(7);
+      auto x = filled({n}, g, 1.0f, true);
+      auto y = x;
+      for (int i = 0; i < 10; i++) y = y * (1.0f + 0.001f * float(i)) + (0.01f * float(i));
+      eval(y);
+      write_raw(dir + "/x.bin", x);
+      write_raw(dir + "/y.bin", y);
+      std::printf("{\"dumped\": \"%s\"}\n", dir.c_str());
+      return 0;
+    }
     std::fprintf(stderr,
-                 "usage: bench_graph chain|transfer|mnist|encoder|encoder-dump|transformer|mlp|train|train-dump "
-                 "...\n");
+                 "usage: bench_graph chain|transfer|mnist|encoder|encoder-dump|transformer|mlp|"
+                 "train|train-dump|dot-dump|chain-dump ...\n");
     return 2;
   } catch (std::exception &ex) {
     std::fprintf(stderr, "bench_graph: %s\n", ex.what());

@@ -8,6 +8,7 @@
 // pool of hipMalloc'd HBM blocks.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstring>
 #include <map>
@@ -25,10 +26,12 @@ thread_local char g_err[512] = "";
 
 std::mutex g_init_mu;
 context g_ctx;
-bool g_ready = false;
+// Set with release once g_ctx is complete; ctx() reads it with acquire, so a
+// thread that sees it set also sees the stream and scratch pointers.
+std::atomic<bool> g_ready{false};
 
 int init_locked() {
-  if (g_ready) return SILGPU_OK;
+  if (g_ready.load(std::memory_order_relaxed)) return SILGPU_OK;
   int n = 0;
   hipError_t e = hipGetDeviceCount(&n);
   if (e != hipSuccess || n <= 0)
@@ -48,7 +51,7 @@ int init_locked() {
   SILGPU_HIP_CHECK(hipStreamCreateWithFlags(&g_ctx.stream, hipStreamNonBlocking));
   SILGPU_HIP_CHECK(hipMalloc(&g_ctx.partials, kPartialBytes));
   SILGPU_HIP_CHECK(hipDeviceSynchronize());
-  g_ready = true;
+  g_ready.store(true, std::memory_order_release);
   return SILGPU_OK;
 }
 
@@ -115,7 +118,7 @@ int ensure_workspace(context *c, size_t bytes) {
 }
 
 context *ctx() {
-  if (g_ready) return &g_ctx;
+  if (g_ready.load(std::memory_order_acquire)) return &g_ctx;
   std::lock_guard<std::mutex> lk(g_init_mu);
   if (init_locked() != SILGPU_OK) return nullptr;
   return &g_ctx;

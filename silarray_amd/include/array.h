@@ -911,9 +911,9 @@ inline array<T> array<T>::int_binary_(detail::op o, const array &rhs) const {
     int opc = o == detail::op::add ? SILGPU_ADD : o == detail::op::sub ? SILGPU_SUB
               : o == detail::op::mul ? SILGPU_MUL : o == detail::op::div ? SILGPU_DIV
                                                                         : SILGPU_POW;
-    gpu::launched_(silgpu_binary_i32(opc, l.storage_.template dev_in<int32_t>(),
-                                     int64_t(l.storage_.len),
-                                     r.storage_.template dev_in<int32_t>(),
+    const int32_t *lp = l.storage_.template dev_in<int32_t>();
+    const int32_t *rp = r.storage_.template dev_in<int32_t>();
+    gpu::launched_(silgpu_binary_i32(opc, lp, int64_t(l.storage_.len), rp,
                                      int64_t(r.storage_.len),
                                      out.storage_.template dev_out<int32_t>(),
                                      int64_t(out.element_count())),

@@ -12,6 +12,12 @@
 //     OUT[0] holds the result (the reference's host finish over one partial
 //     returns the same value, include/array.h:1535-1545)
 //   sgemm* / sgemv / dot_f32_ex: C (ldc = N) = op(A) op(B) [+ bias][sigmoid]
+//
+// Every dispatcher takes its input pointers (dev_in) in statements of their
+// own before it takes the output pointer (dev_out): an in-place call passes
+// the same storage as input and output, and dev_out marks the device copy
+// current, so an input taken after it (C++ leaves the evaluation order of
+// call arguments unspecified) would skip a pending upload.
 
 #include <algorithm>
 #include <cstdint>
@@ -76,8 +82,9 @@ class gpu {
   static void relu(const storage &IN, storage &OUT) { unary_(SILGPU_RELU, IN, OUT); }
 
   static void sigmoid_backward(const storage &dout, const storage &x, storage &OUT, size_t n) {
-    launched_(silgpu_sigmoid_backward_f32(dout.dev_in<float>(), x.dev_in<float>(),
-                                          OUT.dev_out<float>(), int64_t(n)),
+    const float *d = dout.dev_in<float>();
+    const float *xv = x.dev_in<float>();
+    launched_(silgpu_sigmoid_backward_f32(d, xv, OUT.dev_out<float>(), int64_t(n)),
               "sigmoid_backward");
   }
 
@@ -88,9 +95,8 @@ class gpu {
   }
 
   static void affine(const storage &IN, storage &OUT, size_t n, float scale, float offset) {
-    launched_(silgpu_affine_f32(IN.dev_in<float>(), OUT.dev_out<float>(), int64_t(n), scale,
-                                offset),
-              "affine");
+    const float *in = IN.dev_in<float>();
+    launched_(silgpu_affine_f32(in, OUT.dev_out<float>(), int64_t(n), scale, offset), "affine");
   }
 
   // ---- reductions (include/gpu.h:323-470, 889-913) --------------------------
@@ -99,15 +105,18 @@ class gpu {
   static size_t max_f32_num_tg(size_t) { return 1; }
 
   static size_t sum_f32(const storage &IN, storage &OUT, size_t length) {
-    launched_(silgpu_sum_f32(IN.dev_in<float>(), int64_t(length), OUT.dev_out<float>()), "sum");
+    const float *in = IN.dev_in<float>();
+    launched_(silgpu_sum_f32(in, int64_t(length), OUT.dev_out<float>()), "sum");
     return 1;
   }
   static size_t min_f32(const storage &IN, storage &OUT, size_t length) {
-    launched_(silgpu_min_f32(IN.dev_in<float>(), int64_t(length), OUT.dev_out<float>()), "min");
+    const float *in = IN.dev_in<float>();
+    launched_(silgpu_min_f32(in, int64_t(length), OUT.dev_out<float>()), "min");
     return 1;
   }
   static size_t max_f32(const storage &IN, storage &OUT, size_t length) {
-    launched_(silgpu_max_f32(IN.dev_in<float>(), int64_t(length), OUT.dev_out<float>()), "max");
+    const float *in = IN.dev_in<float>();
+    launched_(silgpu_max_f32(in, int64_t(length), OUT.dev_out<float>()), "max");
     return 1;
   }
 
@@ -124,28 +133,30 @@ class gpu {
   // (no reference counterpart: the reference sums axis != 0 on the host).
   static void sum_axis(const storage &IN, storage &OUT, size_t outer, size_t axis_len,
                        size_t inner) {
-    launched_(silgpu_sum_axis_f32(IN.dev_in<float>(), int64_t(outer), int64_t(axis_len),
-                                  int64_t(inner), OUT.dev_out<float>()),
+    const float *in = IN.dev_in<float>();
+    launched_(silgpu_sum_axis_f32(in, int64_t(outer), int64_t(axis_len), int64_t(inner),
+                                  OUT.dev_out<float>()),
               "sum_axis");
   }
 
   static void argmax_f32(const storage &IN, storage &OUT, uint32_t rows, uint32_t cols) {
-    launched_(silgpu_argmax_rows_f32(IN.dev_in<float>(), rows, cols, OUT.dev_out<int32_t>()),
-              "argmax");
+    const float *in = IN.dev_in<float>();
+    launched_(silgpu_argmax_rows_f32(in, rows, cols, OUT.dev_out<int32_t>()), "argmax");
   }
 
   // ---- row ops (include/gpu.h:473-501, 916-942) ------------------------------
   static void layer_norm(const storage &IN, storage &OUT, const storage &gamma,
                          const storage &beta, uint32_t rows, uint32_t cols, float eps) {
-    launched_(silgpu_layer_norm_rows_f32(IN.dev_in<float>(), OUT.dev_out<float>(),
-                                         gamma.dev_in<float>(), beta.dev_in<float>(), rows, cols,
-                                         eps),
+    const float *in = IN.dev_in<float>();
+    const float *g = gamma.dev_in<float>();
+    const float *b = beta.dev_in<float>();
+    launched_(silgpu_layer_norm_rows_f32(in, OUT.dev_out<float>(), g, b, rows, cols, eps),
               "layer_norm");
   }
 
   static void softmax(const storage &IN, storage &OUT, uint32_t rows, uint32_t cols) {
-    launched_(silgpu_softmax_rows_f32(IN.dev_in<float>(), OUT.dev_out<float>(), rows, cols),
-              "softmax");
+    const float *in = IN.dev_in<float>();
+    launched_(silgpu_softmax_rows_f32(in, OUT.dev_out<float>(), rows, cols), "softmax");
   }
 
   // ---- matrix products (include/gpu.h:509-615, 1296-1328) --------------------
@@ -169,8 +180,9 @@ class gpu {
   }
 
   static void sgemv(const storage &x, const storage &B, storage &y, uint32_t N, uint32_t K) {
-    launched_(silgpu_sgemv(x.dev_in<float>(), B.dev_in<float>(), N, y.dev_out<float>(), N, K),
-              "sgemv");
+    const float *xv = x.dev_in<float>();
+    const float *b = B.dev_in<float>();
+    launched_(silgpu_sgemv(xv, b, N, y.dev_out<float>(), N, K), "sgemv");
   }
 
   static void sgemm_steel(const storage &A, const storage &B, storage &C, uint32_t M, uint32_t N,
@@ -205,11 +217,13 @@ class gpu {
                     size_t lda, size_t ldb, bool transA, bool transB, size_t batch,
                     size_t stride_a, size_t stride_b, size_t stride_c, const storage *bias,
                     size_t bias_len, int epilogue, size_t ldc = 0) {
-    launched_(silgpu_sgemm(transA, transB, int64_t(M), int64_t(N), int64_t(K), A.dev_in<float>(),
-                           int64_t(lda), int64_t(stride_a), B.dev_in<float>(), int64_t(ldb),
-                           int64_t(stride_b), C.dev_out<float>(), int64_t(ldc ? ldc : N),
-                           int64_t(stride_c), int64_t(batch),
-                           bias ? bias->dev_in<float>() : nullptr, int64_t(bias_len), epilogue),
+    const float *a = A.dev_in<float>();
+    const float *b = B.dev_in<float>();
+    const float *bs = bias ? bias->dev_in<float>() : nullptr;
+    launched_(silgpu_sgemm(transA, transB, int64_t(M), int64_t(N), int64_t(K), a, int64_t(lda),
+                           int64_t(stride_a), b, int64_t(ldb), int64_t(stride_b),
+                           C.dev_out<float>(), int64_t(ldc ? ldc : N), int64_t(stride_c),
+                           int64_t(batch), bs, int64_t(bias_len), epilogue),
               "sgemm");
   }
 
@@ -245,8 +259,9 @@ class gpu {
   // (include/gpu.h:815-833 of the reference).
   static void conv2d(const storage &input, const storage &weight, storage &output, uint32_t N,
                      uint32_t H, uint32_t W, uint32_t C_in, uint32_t K, uint32_t C_out) {
-    launched_(silgpu_conv2d_f32(input.dev_in<float>(), weight.dev_in<float>(),
-                                output.dev_out<float>(), N, H, W, C_in, K, C_out),
+    const float *in = input.dev_in<float>();
+    const float *w = weight.dev_in<float>();
+    launched_(silgpu_conv2d_f32(in, w, output.dev_out<float>(), N, H, W, C_in, K, C_out),
               "conv2d");
   }
 
@@ -259,12 +274,16 @@ class gpu {
   template <value_type T>
   static void arithmetic_(int op, const storage &A, const storage &B, storage &OUT) {
     if constexpr (std::is_same_v<T, float>) {
-      launched_(silgpu_binary_f32(op, A.dev_in<float>(), int64_t(A.len), B.dev_in<float>(),
-                                  int64_t(B.len), OUT.dev_out<float>(), int64_t(OUT.len)),
+      const float *a = A.dev_in<float>();
+      const float *b = B.dev_in<float>();
+      launched_(silgpu_binary_f32(op, a, int64_t(A.len), b, int64_t(B.len),
+                                  OUT.dev_out<float>(), int64_t(OUT.len)),
                 "arithmetic");
     } else if constexpr (std::is_same_v<T, int>) {
-      launched_(silgpu_binary_i32(op, A.dev_in<int32_t>(), int64_t(A.len), B.dev_in<int32_t>(),
-                                  int64_t(B.len), OUT.dev_out<int32_t>(), int64_t(OUT.len)),
+      const int32_t *a = A.dev_in<int32_t>();
+      const int32_t *b = B.dev_in<int32_t>();
+      launched_(silgpu_binary_i32(op, a, int64_t(A.len), b, int64_t(B.len),
+                                  OUT.dev_out<int32_t>(), int64_t(OUT.len)),
                 "arithmetic");
     } else {
       throw std::runtime_error("gpu: arithmetic on bool storage");
@@ -272,8 +291,8 @@ class gpu {
   }
 
   static void unary_(int op, const storage &IN, storage &OUT) {
-    launched_(silgpu_unary_f32(op, IN.dev_in<float>(), OUT.dev_out<float>(), int64_t(OUT.len)),
-              "unary");
+    const float *in = IN.dev_in<float>();
+    launched_(silgpu_unary_f32(op, in, OUT.dev_out<float>(), int64_t(OUT.len)), "unary");
   }
 };
 

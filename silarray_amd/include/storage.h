@@ -15,11 +15,14 @@
 // Views (slices, rows, broadcasts, transposes) share one `block` and differ
 // in `off`/`len`, as in the reference.  Raw users of `data` (the reference's
 // boundary tests write into storage::make()'s buffer and call gpu:: directly)
-// start in the host-valid state, so the first kernel that reads the storage
-// uploads it; synchronize() downloads every such raw storage a kernel has
-// written.  Array-owned blocks are downloaded only when the host reads them
+// start in the host-valid state.  Their host may rewrite `data` at any time
+// without telling the storage (the reference's unified-memory contract), so
+// every kernel that reads a raw storage whose host copy is valid uploads it
+// again; synchronize() downloads every raw storage a kernel has written.
+// Array-owned blocks are downloaded only when the host reads them
 // (buffer_data, at, iteration), so synchronize() costs no copies for them.
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 #include <cstdlib>
@@ -41,11 +44,12 @@ inline void check(int rc, const char *what) {
     throw std::runtime_error(std::string("gpu: ") + what + ": " + silgpu_last_error());
 }
 
+// silgpu_init is idempotent and thread-safe; the flag only skips the call.
 inline void ensure_init() {
-  static bool done = false;
-  if (!done) {
+  static std::atomic<bool> done{false};
+  if (!done.load(std::memory_order_acquire)) {
     check(silgpu_init(), "init");
-    done = true;
+    done.store(true, std::memory_order_release);
   }
 }
 
@@ -136,8 +140,10 @@ struct block {
     dev_valid = false;
   }
 
+  // A raw block's host copy may have been rewritten through `data` since the
+  // last upload, so while it is valid it is uploaded for every kernel read.
   void dev_read() {
-    if (!dev_valid) {
+    if (!dev_valid || (raw && host_valid)) {
       if (host_valid) check(silgpu_memcpy_h2d(dev_ptr(), host, bytes), "upload");
       dev_valid = true;
     }

@@ -731,6 +731,107 @@ TEST_CASE("msl add float / int / broadcast on raw storage") {
   CHECK(array_equal(array<float>({4}, static_cast<float *>(o.data)), {11.0f, 12.0f, 13.0f, 14.0f}));
 }
 
+TEST_CASE("raw storage rewritten through data after a kernel read is uploaded again") {
+  // The reference's unified-memory contract: the host writes `data` directly
+  // between launches, with no call that tells the storage.
+  auto a = storage::make(4 * sizeof(float));
+  auto b = storage::make(4 * sizeof(float));
+  auto o = storage::make(4 * sizeof(float));
+  a.len = b.len = o.len = 4;
+  const float av[] = {1, 2, 3, 4}, bv[] = {10, 20, 30, 40}, av2[] = {5, 6, 7, 8};
+  std::memcpy(a.data, av, sizeof(av));
+  std::memcpy(b.data, bv, sizeof(bv));
+  msl::add<float>(a, b, o);
+  synchronize();
+  CHECK(array_equal(array<float>({4}, static_cast<float *>(o.data)), {11.0f, 22.0f, 33.0f, 44.0f}));
+  std::memcpy(a.data, av2, sizeof(av2));
+  msl::add<float>(a, b, o);
+  synchronize();
+  CHECK(array_equal(array<float>({4}, static_cast<float *>(o.data)), {15.0f, 26.0f, 37.0f, 48.0f}));
+  // the output of the last call used as an input after its host copy changed
+  static_cast<float *>(o.data)[0] = 100.0f;
+  msl::add<float>(o, b, a);
+  synchronize();
+  CHECK(array_equal(array<float>({4}, static_cast<float *>(a.data)), {110.0f, 46.0f, 67.0f, 88.0f}));
+}
+
+TEST_CASE("in-place kernels on a fresh raw storage read the host data") {
+  // Input and output are the same storage: the pending upload must happen
+  // before the output is marked device-written.
+  auto x = storage::make(3 * sizeof(float));
+  x.len = 3;
+  const float xv[] = {0.0f, 1.0f, -1.0f};
+  std::memcpy(x.data, xv, sizeof(xv));
+  msl::sigmoid(x, x);
+  synchronize();
+  const float *r = static_cast<const float *>(x.data);
+  CHECK(is_close(r[0], 0.5f, 1e-6f) && is_close(r[1], 0.7310586f, 1e-6f) &&
+        is_close(r[2], 0.2689414f, 1e-6f));
+  auto y = storage::make(4 * sizeof(float));
+  y.len = 4;
+  const float yv[] = {1, 2, 3, 4};
+  std::memcpy(y.data, yv, sizeof(yv));
+  msl::mul<float>(y, y, y);
+  synchronize();
+  CHECK(array_equal(array<float>({4}, static_cast<float *>(y.data)), {1.0f, 4.0f, 9.0f, 16.0f}));
+}
+
+TEST_CASE("slice and row views of a device array feed linear, sum(0) and dot") {
+  // Zero-copy views (the reference's slice, include/array.h:1177-1187, as
+  // its MNIST benchmark uses it for batches) of an evaluated device array,
+  // against float64 sums of the same host values.
+  const size_t R = 64, K = 96, N = 40, r0 = 10, rn = 33;
+  auto X = random({R, K}) - 0.5f;
+  auto W = random({K, N}) - 0.5f;
+  auto b = random({N}) - 0.5f;
+  eval(X, W, b);
+  auto Xs = X.slice(r0, rn);
+  CHECK(Xs.shape() == (shape_type{rn, K}));
+  CHECK(std::as_const(Xs).buffer_data() == std::as_const(X).buffer_data() + r0 * K);
+  auto row = X[r0 + 7];  // a row view: a 1-D vector times a matrix (the GEMV path)
+  auto Y = Xs.linear(W, b);
+  auto S = Xs.sum(0);
+  auto yr = row.dot(W);
+  eval(Y, S, yr);
+  CHECK(Y.shape() == (shape_type{rn, N}) && S.shape() == shape_type{K} && yr.shape() == shape_type{N});
+  const float tol = 1e-5f * std::sqrt(float(K));
+  bool ok = true;
+  for (size_t i = 0; i < rn; i++)
+    for (size_t j = 0; j < N; j++) {
+      double acc = 0.0, mag = 0.0;
+      for (size_t k = 0; k < K; k++) {
+        const double t = double(X[r0 + i, k]) * double(W[k, j]);
+        acc += t;
+        mag += std::abs(t);
+      }
+      acc += double(b.at(j));
+      mag += std::abs(double(b.at(j)));
+      ok = ok && std::abs(double(Y[i, j]) - acc) <= tol * mag + 1e-30;
+    }
+  CHECK(ok);
+  bool sok = true;
+  for (size_t k = 0; k < K; k++) {
+    double acc = 0.0, mag = 0.0;
+    for (size_t i = 0; i < rn; i++) {
+      acc += double(X[r0 + i, k]);
+      mag += std::abs(double(X[r0 + i, k]));
+    }
+    sok = sok && std::abs(double(S.at(k)) - acc) <= 1e-5 * std::abs(acc) + 6e-8 * mag + 1e-30;
+  }
+  CHECK(sok);
+  bool rok = true;
+  for (size_t j = 0; j < N; j++) {
+    double acc = 0.0, mag = 0.0;
+    for (size_t k = 0; k < K; k++) {
+      const double t = double(X[r0 + 7, k]) * double(W[k, j]);
+      acc += t;
+      mag += std::abs(t);
+    }
+    rok = rok && std::abs(double(yr.at(j)) - acc) <= tol * mag + 1e-30;
+  }
+  CHECK(rok);
+}
+
 TEST_CASE("host writes after device use are uploaded") {
   auto x = ones<float>({8192});
   auto s1 = x.sum();

@@ -65,7 +65,11 @@ def encoder_f64(p, B, S, D, H, F):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("dims", [(2, 64, 128, 4, 256), (1, 37, 96, 3, 200)])
+# The last case is BASELINE config 5 at its stated size (head dim 64: the
+# fused attention kernel's D = 64 path, the head-merge relayout, the
+# out-projection and FFN products with residual epilogues).
+@pytest.mark.parametrize("dims", [(2, 64, 128, 4, 256), (1, 37, 96, 3, 200),
+                                  (4, 512, 768, 12, 3072)])
 def test_encoder_block_matches_f64(tmp_path, dims):
     B, S, D, H, F = dims
     print(f"encoder-dump {dims}", flush=True)

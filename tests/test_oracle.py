@@ -242,6 +242,29 @@ def test_sum_axis_vs_numpy(oracle):
                                    rtol=1e-12, atol=1e-12)
 
 
+def test_sum_axis_ref_order_and_goldens(oracle, ref_vectors):
+    """The float path: the reference's goldens (integer-valued, exact in
+    float), an explicit float32 loop in axis order on a small tensor, and
+    the fp64 sum within the float accumulation bound on a large row."""
+    ag = ref_vectors["aggregates"]
+    t = np.array(ag["t_3_2_3"], np.float32)
+    for ax in range(3):
+        assert np.array_equal(oracle.sum_axis_ref(t, ax), np.array(ag[f"sum{ax}"], np.float32))
+    x = rng(37).normal(0, 1, (4, 6, 5)).astype(np.float32)
+    for ax in range(3):
+        moved = np.moveaxis(x, ax, 0)
+        acc = np.zeros(moved.shape[1:], np.float32)
+        for a in range(moved.shape[0]):
+            acc = (acc + moved[a]).astype(np.float32)
+        assert np.array_equal(oracle.sum_axis_ref(x, ax), acc), ax
+    big = rng(38).uniform(-1, 1, (2, 100000)).astype(np.float32)
+    got = oracle.sum_axis_ref(big, 1).astype(np.float64)
+    exact = oracle.sum_axis_f64(big, 1)
+    bound = 100000 * np.finfo(np.float32).eps * np.abs(big).astype(np.float64).sum(1)
+    assert np.all(np.abs(got - exact) <= bound)
+    assert np.any(got != exact.astype(np.float32))  # it is float accumulation
+
+
 def test_min_max_vs_numpy(oracle):
     x = rng(31).normal(0, 1, 5001).astype(np.float32)
     assert oracle.fmin(x) == x.min() and oracle.fmax(x) == x.max()
