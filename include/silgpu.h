@@ -310,6 +310,23 @@ typedef struct silgpu_gemm_desc {
 
 int silgpu_gemm(const silgpu_gemm_desc *desc);
 
+/* silgpu_gemm that allocates nothing.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * caller passes inputs and outputs as for silgpu_gemm; the K-split partial
+ * planes and GEMV partials live in one fixed 32 MiB device array reserved
+ * when the library is loaded, whose address silgpu_init looks up.
+ *   - silgpu_init() must have returned SILGPU_OK first (SILGPU_ERR_INVALID
+ *     otherwise); the call itself makes no hipMalloc/hipFree.
+ *   - A plan whose partial planes exceed 32 MiB runs with fewer K splits
+ *     (down to none), so its rounding may differ from silgpu_gemm's within
+ *     the SGEMM tolerance; otherwise the result is bit-identical.  A vector
+ *     product (M == 1) whose N exceeds 8M columns is rejected.
+ *   - All calls on one device share the array, and it keeps the last call's
+ *     contents: calls that overlap in time on one device (several host
+ *     threads, several streams) race. */
+int silgpu_gemm_noalloc(const silgpu_gemm_desc *desc);
+
 /* Fused attention: for every batch index b = (o, i) (o < batch_outer,
  * i < batch_inner) and query row r < Sq,
  *   O[b][r][:] = sum_j softmax_j(scale * Q[b][r] . K[b][j]) * V[b][j][:]

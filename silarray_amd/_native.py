@@ -138,6 +138,7 @@ _SIGS = {
     "silgpu_sgemm_tuned": (_i, [_i, _i, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
                                 _vp, _i64, _i64, _i64, _vp, _i64, _i, _i, _i]),
     "silgpu_gemm": (_i, [C.POINTER(GemmDesc)]),
+    "silgpu_gemm_noalloc": (_i, [C.POINTER(GemmDesc)]),
     "silgpu_sgemv": (_i, [_vp, _vp, _i64, _vp, _i64, _i64]),
     "silgpu_attention_f32": (_i, [C.POINTER(AttnDesc)]),
     "silgpu_conv2d_f32": (_i, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64]),
@@ -342,8 +343,9 @@ def sgemm_tuned(ta, tb, M, N, K, A, lda, sA, B, ldb, sB, Cm, ldc, sC, batch=1, b
 
 def gemm(ta, tb, M, N, K, A, lda, B, ldb, Cm, ldc, batch_outer=1, batch_inner=1,
          strides_a=(0, 0), strides_b=(0, 0), strides_c=(0, 0), epi=EPI_NONE, scale=None,
-         bias=None, bias_len=0, residual=None, ldr=0):
-    """silgpu_gemm; strides_x = (outer, inner); scale = (scale, offset) or None."""
+         bias=None, bias_len=0, residual=None, ldr=0, noalloc=False):
+    """silgpu_gemm (silgpu_gemm_noalloc with noalloc=True); strides_x =
+    (outer, inner); scale = (scale, offset) or None."""
     d = GemmDesc()
     d.trans_a, d.trans_b, d.M, d.N, d.K = int(ta), int(tb), M, N, K
     d.A, d.lda, d.B, d.ldb, d.C, d.ldc = vp(A).value, lda, vp(B).value, ldb, vp(Cm).value, ldc
@@ -358,7 +360,7 @@ def gemm(ta, tb, M, N, K, A, lda, B, ldb, Cm, ldc, batch_outer=1, batch_inner=1,
     d.bias_len = bias_len
     d.residual = vp(residual).value if residual is not None else None
     d.ldr = ldr
-    call("silgpu_gemm", C.byref(d))
+    call("silgpu_gemm_noalloc" if noalloc else "silgpu_gemm", C.byref(d))
 
 
 def attention(Sq, Sk, D, scale, Q, ldq, K, ldk, V, ldv, O, ldo, batch_outer=1, batch_inner=1,

@@ -1608,8 +1608,18 @@ int launch_skinny(const gemm_args &a, int Q, int splits, bool tb, hipStream_t s)
 
 int launch_split_sum(const gemm_args &a, int launched, context *c);
 
+// Where a product's scratch comes from.  silgpu_gemm: the split-K workspace
+// (grown with hipMalloc on demand) and the partials area reserved at init.
+// silgpu_gemm_noalloc: one fixed device array for both, never allocated
+// per call; a K split whose partial planes would not fit it is narrowed to
+// the widest that fits (down to none).
+struct scratch_src {
+  float *fixed = nullptr;
+  size_t fixed_bytes = 0;
+};
+
 int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, bool vec,
-              context *c) {
+              context *c, const scratch_src &ss) {
   if (pl.tail_rows > 0 && pl.tail_rows < a0.M && batch == 1) {
     // Rows [0, M - tail) as one product, the last tail rows as another.
     const int head = a0.M - pl.tail_rows;
@@ -1620,9 +1630,9 @@ int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, boo
     t.C = a0.C + int64_t(head) * a0.ldc;
     if (t.ep.res) t.ep.res += int64_t(head) * t.ep.ldr;
     const bool tvec = vec && aligned16(t.A);
-    int rc = run_sgemm(h, 1, plan{pl.tile, 1}, ta, tb, vec, c);
+    int rc = run_sgemm(h, 1, plan{pl.tile, 1}, ta, tb, vec, c, ss);
     if (rc != SILGPU_OK) return rc;
-    return run_sgemm(t, 1, plan{pl.tile, pl.tail_splits}, ta, tb, tvec, c);
+    return run_sgemm(t, 1, plan{pl.tile, pl.tail_splits}, ta, tb, tvec, c, ss);
   }
   gemm_args a = a0;
   const bool skinny = pl.tile >= TILE_SKINNY && a.M <= 32 && batch == 1 && !ta;
@@ -1637,10 +1647,16 @@ int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, boo
   if (splits < 1) splits = 1;
   if (batch != 1 || a.K == 0) splits = 1;
   if (splits > 1) {
-    size_t need = size_t(splits) * size_t(a.M) * size_t(a.N) * sizeof(float);
-    int rc = ensure_workspace(c, need);
-    if (rc != SILGPU_OK) return rc;
-    a.ws = static_cast<float *>(c->workspace);
+    const size_t plane = size_t(a.M) * size_t(a.N) * sizeof(float);
+    if (ss.fixed) {
+      const size_t fit = ss.fixed_bytes / plane;
+      if (size_t(splits) > fit) splits = fit >= 2 ? static_cast<int>(fit) : 1;
+      a.ws = ss.fixed;
+    } else {
+      int rc = ensure_workspace(c, size_t(splits) * plane);
+      if (rc != SILGPU_OK) return rc;
+      a.ws = static_cast<float *>(c->workspace);
+    }
   }
   int launched;
   if (skinny) {
@@ -1738,7 +1754,9 @@ int launch_conv_cfg(const gemm_args &a, hipStream_t s) {
 }
 
 int launch_gemv_n(const float *x, const float *Bm, int64_t ldb, float *y, int64_t N,
-                  int64_t K, context *c) {
+                  int64_t K, context *c, const scratch_src &ss) {
+  float *partial = ss.fixed ? ss.fixed : static_cast<float *>(c->partials);
+  const int64_t partial_bytes = ss.fixed ? int64_t(ss.fixed_bytes) : int64_t(kPartialBytes);
   const bool vec = N % 4 == 0 && ldb % 4 == 0 && aligned16(Bm);
   const int64_t ct = cdiv(N, kGemvCols);
   const int64_t pitch = ct * kGemvCols;
@@ -1747,12 +1765,12 @@ int launch_gemv_n(const float *x, const float *Bm, int64_t ldb, float *y, int64_
   if (ks > K / 32) ks = K / 32;
   if (ks < 1) ks = 1;
   if (ks > 65535) ks = 65535;
-  while (ks > 1 && ks * pitch * int64_t(sizeof(float)) > int64_t(kPartialBytes)) ks /= 2;
-  SILGPU_REQUIRE(pitch * int64_t(sizeof(float)) <= int64_t(kPartialBytes),
-                 "silgpu_sgemv: N %lld exceeds the scratch area", (long long)N);
+  while (ks > 1 && ks * pitch * int64_t(sizeof(float)) > partial_bytes) ks /= 2;
+  SILGPU_REQUIRE(pitch * int64_t(sizeof(float)) <= partial_bytes,
+                 "silgpu_sgemv: N %lld exceeds the %lld-byte scratch area", (long long)N,
+                 (long long)partial_bytes);
   const int64_t kc = cdiv(K, ks);
   ks = cdiv(K, kc);
-  float *partial = static_cast<float *>(c->partials);
   dim3 grid(static_cast<unsigned>(ct), static_cast<unsigned>(ks));
   if (vec)
     gemv_part_k<true><<<grid, kGemvPartBlock, 0, c->stream>>>(x, Bm, ldb, N, K, kc, partial);
@@ -1812,16 +1830,18 @@ int silgpu_sgemv(const float *d_x, const float *d_B, int64_t ldb, float *d_y, in
   SILGPU_CTX(c);
   if (K == 0) return silgpu_fill_u32(d_y, 0u, N);
   SILGPU_REQUIRE(d_x && d_B, "silgpu_sgemv: null pointer");
-  return launch_gemv_n(d_x, d_B, ldb, d_y, N, K, c);
+  return launch_gemv_n(d_x, d_B, ldb, d_y, N, K, c, scratch_src{});
 }
 
 }  // extern "C"
 
 namespace {
 
-// Shared body of silgpu_sgemm / silgpu_sgemm_tuned.  `forced` (tuning only)
-// skips the vector-product routing and the shape heuristic.
-int gemm_impl(const silgpu_gemm_desc &d, const plan *forced) {
+// Shared body of silgpu_sgemm / silgpu_sgemm_tuned / silgpu_gemm_noalloc.
+// `forced` (tuning only) skips the vector-product routing and the shape
+// heuristic.  `noalloc`: the library must already be initialised, and all
+// scratch comes from the fixed array found at init.
+int gemm_impl(const silgpu_gemm_desc &d, const plan *forced, bool noalloc = false) {
   const int64_t M = d.M, N = d.N, K = d.K;
   SILGPU_REQUIRE(M >= 0 && N >= 0 && K >= 0 && d.batch_outer >= 0 && d.batch_inner >= 0,
                  "silgpu_gemm: negative extent");
@@ -1846,7 +1866,13 @@ int gemm_impl(const silgpu_gemm_desc &d, const plan *forced) {
   SILGPU_REQUIRE(!d.residual || (batch == 1 && d.ldr >= N),
                  "silgpu_gemm: a residual needs batch 1 and ldr >= N");
   SILGPU_REQUIRE(d.C != nullptr && (K == 0 || (d.A && d.B)), "silgpu_gemm: null pointer");
-  SILGPU_CTX(c);
+  context *c = noalloc ? ctx_if_ready() : ctx();
+  if (!c) return noalloc ? SILGPU_ERR_INVALID : SILGPU_ERR_NODEVICE;
+  scratch_src ss{};
+  if (noalloc) {
+    ss.fixed = c->noalloc_scratch;
+    ss.fixed_bytes = kNoAllocScratchBytes;
+  }
 
   epi_args ep{};
   ep.bias = d.bias;
@@ -1863,7 +1889,7 @@ int gemm_impl(const silgpu_gemm_desc &d, const plan *forced) {
     int rc;
     if (M == 1 && !tb && !ta) {
       // y = x * B with x = A[0..K) contiguous and B [K][N].
-      rc = launch_gemv_n(d.A, d.B, d.ldb, d.C, N, K, c);
+      rc = launch_gemv_n(d.A, d.B, d.ldb, d.C, N, K, c, ss);
       if (rc != SILGPU_OK) return rc;
       return apply_epilogue(d.C, d.ldc, 1, N, ep, c);
     } else if (M == 1 && tb) {
@@ -1902,7 +1928,7 @@ int gemm_impl(const silgpu_gemm_desc &d, const plan *forced) {
                    (batch == 1 || (d.stride_a_inner % 4 == 0 && d.stride_b_inner % 4 == 0 &&
                                    d.stride_a_outer % 4 == 0 && d.stride_b_outer % 4 == 0));
   return run_sgemm(a, batch, forced ? *forced : choose_plan(M, N, K, batch, vec && K % 16 == 0),
-                   ta, tb, vec, c);
+                   ta, tb, vec, c, ss);
 }
 
 silgpu_gemm_desc plain_desc(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
@@ -1966,6 +1992,11 @@ int silgpu_sgemm_tuned(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K
 int silgpu_gemm(const silgpu_gemm_desc *desc) {
   SILGPU_REQUIRE(desc != nullptr, "silgpu_gemm: null descriptor");
   return gemm_impl(*desc, nullptr);
+}
+
+int silgpu_gemm_noalloc(const silgpu_gemm_desc *desc) {
+  SILGPU_REQUIRE(desc != nullptr, "silgpu_gemm_noalloc: null descriptor");
+  return gemm_impl(*desc, nullptr, true);
 }
 
 int silgpu_conv2d_f32(const float *d_in, const float *d_w, float *d_out, int64_t N, int64_t H,

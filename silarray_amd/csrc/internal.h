@@ -35,9 +35,14 @@ struct context {
   // GEMM split-K workspace: grown to the largest request seen, never shrunk.
   void *workspace = nullptr;
   size_t workspace_bytes = 0;
+  // Device address of the fixed scratch array of silgpu_gemm_noalloc
+  // (kNoAllocScratchBytes), looked up once at init.
+  float *noalloc_scratch = nullptr;
 };
 
 constexpr size_t kPartialBytes = size_t(16) << 20;  // 16 MiB
+// Size of the fixed scratch array behind silgpu_gemm_noalloc.
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;  // 32 MiB
 
 // Makes c->workspace hold at least `bytes` (synchronises the stream before
 // replacing a smaller block).
@@ -45,6 +50,9 @@ int ensure_workspace(context *c, size_t bytes);
 
 // Returns the initialised context, or nullptr after recording an error.
 context *ctx();
+// The context if silgpu_init has completed, else nullptr after recording an
+// error; never initialises (for entry points that must not allocate).
+context *ctx_if_ready();
 
 // Checks a HIP call; on failure records the error and returns SILGPU_ERR_HIP.
 #define SILGPU_HIP_CHECK(call)                                                       \

@@ -24,6 +24,14 @@ namespace {
 
 thread_local char g_err[512] = "";
 
+// Scratch of silgpu_gemm_noalloc (K-split partial planes, GEMV partials): a
+// fixed array in device memory, so that entry point never allocates.  In host
+// code the name `scratch` is only a stand-in for the symbol; every host use
+// goes through the device address hipGetSymbolAddress returns at init
+// (context::noalloc_scratch).  Calls on one device share it, so calls of
+// silgpu_gemm_noalloc that overlap in time on one device race.
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
 std::mutex g_init_mu;
 context g_ctx;
 // Set with release once g_ctx is complete; ctx() reads it with acquire, so a
@@ -50,6 +58,11 @@ int init_locked() {
   // Default priority on purpose: streams of mixed priority are avoided.
   SILGPU_HIP_CHECK(hipStreamCreateWithFlags(&g_ctx.stream, hipStreamNonBlocking));
   SILGPU_HIP_CHECK(hipMalloc(&g_ctx.partials, kPartialBytes));
+  // With device 0 current: this device's copy of the no-allocation scratch.
+  void *sp = nullptr;
+  SILGPU_HIP_CHECK(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)));
+  SILGPU_REQUIRE(sp != nullptr, "init: no device address for the scratch array");
+  g_ctx.noalloc_scratch = static_cast<float *>(sp);
   SILGPU_HIP_CHECK(hipDeviceSynchronize());
   g_ready.store(true, std::memory_order_release);
   return SILGPU_OK;
@@ -122,6 +135,12 @@ context *ctx() {
   std::lock_guard<std::mutex> lk(g_init_mu);
   if (init_locked() != SILGPU_OK) return nullptr;
   return &g_ctx;
+}
+
+context *ctx_if_ready() {
+  if (g_ready.load(std::memory_order_acquire)) return &g_ctx;
+  set_error(SILGPU_ERR_INVALID, "the library is not initialised: call silgpu_init() first");
+  return nullptr;
 }
 
 }  // namespace silgpu
