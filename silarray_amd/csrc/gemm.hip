@@ -1457,9 +1457,10 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dtl_ok) {
   // groups would each walk 2048 or more rows of B in 128-byte pieces (wide N
   // and deep K), 64-column groups with twice the K splits read 256-byte
   // pieces: 19.8 -> 17.9 us at 8 x 4096 x 4096 on MI355X; at N 768..3072
-  // the 32-column groups measured ahead.
+  // the 32-column groups measured ahead, so the wider groups need N > 3072.
   if (M <= 32 && batch == 1)
-    return plan{K / skinny_splits(M, N, K, 1) >= 2048 ? TILE_SKINNY_Q2 : TILE_SKINNY, 0};
+    return plan{N > 3072 && K / skinny_splits(M, N, K, 1) >= 2048 ? TILE_SKINNY_Q2 : TILE_SKINNY,
+                0};
   if (M <= 32) return small_m_tiles(M, N, K, batch);
   // Batched products with a short K loop (attention's Q K^T at head dim 64)
   // are bound by storing C, which the many small tiles overlap with other

@@ -38,7 +38,53 @@ struct context {
   // Device address of the fixed scratch array of silgpu_gemm_noalloc
   // (kNoAllocScratchBytes), looked up once at init.
   float *noalloc_scratch = nullptr;
+  // One-launch reductions: kSlots 64-bit slots, zero between launches.  A
+  // workgroup publishes its partial result in its slot (the bitwise
+  // complement of the result's 64-bit pattern, so zero means "not written
+  // yet"); the workgroup that finishes the reduction waits for the slots it
+  // needs, reads them and sets them back to zero before the launch ends.
+  uint64_t *slots = nullptr;
 };
+
+constexpr int kSlots = 16384;
+
+// ---- slots: one 64-bit location per published value, zero at rest ----------
+//
+// A producer publishes the complement of a value's 64-bit pattern with one
+// agent-scope atomic store (never zero unless the value is all ones); a
+// consumer in the same launch waits until the slot reads non-zero, takes the
+// value and clears the slot, so the area is zero again when the launch ends.
+// Each slot is written once and read as a whole, so no fence is needed.
+// Polls of one slot before a consumer stops waiting: every producer has been
+// dispatched before its consumer and publishes unconditionally, so the wait
+// ends within a memory round trip or two; the bound only keeps a broken
+// device from hanging the stream (and lets a value that really is all ones,
+// a NaN with a full payload, through after the wait).
+constexpr int kSpinLimit = 1 << 24;
+
+__device__ __forceinline__ void slot_publish(uint64_t *slot, uint64_t bits) {
+  __hip_atomic_store(slot, ~bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t slot_peek(uint64_t *slot) {
+  return __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Completes a read started with slot_peek(): waits while the slot reads zero,
+// clears it and returns the published bits.
+__device__ __forceinline__ uint64_t slot_take(uint64_t *slot, uint64_t seen) {
+  for (int it = 0; seen == 0 && it < kSpinLimit; ++it) {
+    __builtin_amdgcn_s_sleep(1);
+    seen = slot_peek(slot);
+  }
+  __hip_atomic_store(slot, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return ~seen;
+}
+// Two floats in one slot.
+__device__ __forceinline__ uint64_t pack_f2(float a, float b) {
+  return (uint64_t(__float_as_uint(b)) << 32) | __float_as_uint(a);
+}
+__device__ __forceinline__ float2 unpack_f2(uint64_t v) {
+  return make_float2(__uint_as_float(uint32_t(v)), __uint_as_float(uint32_t(v >> 32)));
+}
 
 constexpr size_t kPartialBytes = size_t(16) << 20;  // 16 MiB
 // Size of the fixed scratch array behind silgpu_gemm_noalloc.

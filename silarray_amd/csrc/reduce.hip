@@ -3,16 +3,22 @@
 // The reference reduces with one pass that writes up to 256 per-threadgroup
 // partials, a blocking host round trip, and a host finish over the partials
 // (include/array.h:1535-1545; include/gpu.h:323-354).  Here the whole
-// reduction stays on the device and never synchronises with the host:
-//   pass 1: each workgroup streams one contiguous chunk of the input with
-//           16-byte non-temporal loads (eight in flight per thread) and
-//           writes one partial to scratch;
-//   pass 2: a small kernel reduces the partials in a fixed order.
-// The kernel boundary orders pass 2 after pass 1; an in-kernel "last
-// workgroup finishes" scheme needs agent-scope release/acquire fences
-// (L2 write-back + invalidate on every XCD), which on MI355X cost far more
-// than the second launch.  The fixed partial order makes every result
-// deterministic run to run.
+// reduction is one launch that never synchronises with the host:
+//   - each workgroup streams one contiguous chunk of the input with 16-byte
+//     non-temporal loads (eight in flight per thread) and reduces it;
+//   - every workgroup but the last publishes its partial in a 64-bit slot
+//     (one agent-scope atomic store of the value's complement, so a slot
+//     reads zero until it is written);
+//   - the last workgroup, which the dispatcher starts after all the others,
+//     reduces its own chunk, then reads every slot -- waiting on any that
+//     still reads zero -- in a fixed order, clears them and writes the
+//     result.
+// Each slot is one atomic location written once, so the finisher needs no
+// fence: it sees either zero or the whole value.  A release/acquire "last
+// workgroup" handoff would need L2 write-back and invalidate on every XCD;
+// a second launch (the earlier design) costs ~2 us of launch gap and cache
+// maintenance, 5% of a 64M-element reduction.  The fixed partial order makes
+// every result deterministic run to run.
 //
 // All kernels are HBM-bound (4 bytes read per element).
 #include <hip/hip_runtime.h>
@@ -28,9 +34,9 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
 constexpr int kUnroll = 8;          // 16-byte loads in flight per thread
-constexpr int kFullBlocks = 2048;   // pass-1 workgroups for a full reduction
-constexpr int kFinishLoads = 8;     // partials in flight per thread in pass 2
-
+constexpr int kFullBlocks = 1024;   // workgroups of a full reduction (measured best
+                                    // of 256..4096 at 64M elements)
+constexpr int kFinishLoads = 8;     // slots in flight per thread in the finish
 enum { R_SUM = 0, R_MIN = 1, R_MAX = 2 };
 
 template <int R>
@@ -38,6 +44,10 @@ struct racc;
 template <>
 struct racc<R_SUM> {
   using T = double;  // fp64 accumulation: free on an HBM-bound pass
+  // A partial sum is never the all-ones pattern: a NaN from the data keeps
+  // a float payload (low 29 bits zero), and arithmetic NaNs are canonical.
+  __device__ static uint64_t pack(T v) { return uint64_t(__double_as_longlong(v)); }
+  __device__ static T unpack(uint64_t b) { return __longlong_as_double((long long)b); }
   __device__ static T init() { return 0.0; }
   __device__ static T add(T a, float x) { return a + static_cast<double>(x); }
   __device__ static T add4(T a, float4 v) {
@@ -49,6 +59,8 @@ struct racc<R_SUM> {
 template <>
 struct racc<R_MIN> {
   using T = float;
+  __device__ static uint64_t pack(T v) { return uint64_t(__float_as_uint(v)); }
+  __device__ static T unpack(uint64_t b) { return __uint_as_float(uint32_t(b)); }
   __device__ static T init() { return INFINITY; }
   __device__ static T add(T a, float x) { return fminf(a, x); }
   __device__ static T add4(T a, float4 v) { return fminf(fminf(a, fminf(v.x, v.y)), fminf(v.z, v.w)); }
@@ -57,6 +69,8 @@ struct racc<R_MIN> {
 template <>
 struct racc<R_MAX> {
   using T = float;
+  __device__ static uint64_t pack(T v) { return uint64_t(__float_as_uint(v)); }
+  __device__ static T unpack(uint64_t b) { return __uint_as_float(uint32_t(b)); }
   __device__ static T init() { return -INFINITY; }
   __device__ static T add(T a, float x) { return fmaxf(a, x); }
   __device__ static T add4(T a, float4 v) { return fmaxf(fmaxf(a, fmaxf(v.x, v.y)), fmaxf(v.z, v.w)); }
@@ -112,14 +126,43 @@ __device__ __forceinline__ typename racc<R>::T stream4(const float4 *__restrict_
   return acc;
 }
 
-// Pass 1 of a full reduction.  Workgroup b streams float4s
+// The last workgroup's finish: partial g of the G workgroups is slot g for
+// g < G - 1 and `own` for g = G - 1, merged in a fixed order (thread t takes
+// g = t, t + kBlock, ..., kFinishLoads of them in flight), then across the
+// workgroup.
+template <int R>
+__device__ __forceinline__ void finish_full(typename racc<R>::T own, uint64_t *__restrict__ slots,
+                                            int G, float *__restrict__ out) {
+  using T = typename racc<R>::T;
+  T f = racc<R>::init();
+  for (int j0 = threadIdx.x; j0 < G; j0 += kFinishLoads * kBlock) {
+    uint64_t seen[kFinishLoads];
+#pragma unroll
+    for (int g = 0; g < kFinishLoads; ++g) {
+      const int j = j0 + g * kBlock;
+      seen[g] = j < G - 1 ? slot_peek(slots + j) : 0;
+    }
+#pragma unroll
+    for (int g = 0; g < kFinishLoads; ++g) {
+      const int j = j0 + g * kBlock;
+      T v = racc<R>::init();
+      if (j < G - 1) v = racc<R>::unpack(slot_take(slots + j, seen[g]));
+      else if (j == G - 1) v = own;
+      f = racc<R>::merge(f, v);
+    }
+  }
+  f = block_merge<R>(f);
+  if (threadIdx.x == 0) out[0] = static_cast<float>(f);
+}
+
+// A full reduction in one launch.  Workgroup b streams float4s
 // [b*chunk4, (b+1)*chunk4) of x4; workgroup 0 also takes the `head` scalars
 // before x4 and the `tail` scalars after the last float4.
 template <int R>
-__global__ __launch_bounds__(kBlock) void reduce_part_k(
+__global__ __launch_bounds__(kBlock) void reduce_k(
     const float *__restrict__ head_ptr, int head, const float4 *__restrict__ x4, int64_t n4,
-    int64_t chunk4, const float *__restrict__ tail_ptr, int tail,
-    typename racc<R>::T *__restrict__ partial) {
+    int64_t chunk4, const float *__restrict__ tail_ptr, int tail, uint64_t *__restrict__ slots,
+    float *__restrict__ out) {
   using T = typename racc<R>::T;
   const int64_t c0 = int64_t(blockIdx.x) * chunk4;
   const int64_t c1 = c0 + chunk4 < n4 ? c0 + chunk4 : n4;
@@ -128,45 +171,34 @@ __global__ __launch_bounds__(kBlock) void reduce_part_k(
     if (threadIdx.x < head) acc = racc<R>::add(acc, head_ptr[threadIdx.x]);
     if (threadIdx.x < tail) acc = racc<R>::add(acc, tail_ptr[threadIdx.x]);
   }
-  T b = block_merge<R>(acc);
-  if (threadIdx.x == 0) partial[blockIdx.x] = b;
+  const T b = block_merge<R>(acc);
+  const int G = gridDim.x;
+  if (blockIdx.x != G - 1) {
+    if (threadIdx.x == 0) slot_publish(slots + blockIdx.x, racc<R>::pack(b));
+    return;
+  }
+  finish_full<R>(b, slots, G, out);
 }
 
 // Inputs that are not 4-byte aligned (never produced by the allocator; kept
-// so every pointer is accepted): scalar loads, same partial layout.
+// so every pointer is accepted): scalar loads, same slots and finish.
 template <int R>
-__global__ __launch_bounds__(kBlock) void reduce_part_scalar_k(
-    const float *__restrict__ x, int64_t n, int64_t chunk,
-    typename racc<R>::T *__restrict__ partial) {
+__global__ __launch_bounds__(kBlock) void reduce_scalar_k(const float *__restrict__ x, int64_t n,
+                                                          int64_t chunk,
+                                                          uint64_t *__restrict__ slots,
+                                                          float *__restrict__ out) {
   using T = typename racc<R>::T;
   const int64_t c0 = int64_t(blockIdx.x) * chunk;
   const int64_t c1 = c0 + chunk < n ? c0 + chunk : n;
   T acc = racc<R>::init();
   for (int64_t i = c0 + threadIdx.x; i < c1; i += kBlock) acc = racc<R>::add(acc, x[i]);
-  T b = block_merge<R>(acc);
-  if (threadIdx.x == 0) partial[blockIdx.x] = b;
-}
-
-// Pass 2: one workgroup reduces np partials in a fixed order.
-template <int R>
-__global__ __launch_bounds__(kBlock) void reduce_finish_k(
-    const typename racc<R>::T *__restrict__ partial, int np, float *__restrict__ out) {
-  using T = typename racc<R>::T;
-  // Groups of kFinishLoads partials per thread are loaded together (one
-  // memory latency per group rather than per partial).
-  T f = racc<R>::init();
-  for (int j0 = threadIdx.x; j0 < np; j0 += kFinishLoads * kBlock) {
-    T v[kFinishLoads];
-#pragma unroll
-    for (int g = 0; g < kFinishLoads; ++g) {
-      const int j = j0 + g * kBlock;
-      v[g] = j < np ? partial[j] : racc<R>::init();
-    }
-#pragma unroll
-    for (int g = 0; g < kFinishLoads; ++g) f = racc<R>::merge(f, v[g]);
+  const T b = block_merge<R>(acc);
+  const int G = gridDim.x;
+  if (blockIdx.x != G - 1) {
+    if (threadIdx.x == 0) slot_publish(slots + blockIdx.x, racc<R>::pack(b));
+    return;
   }
-  f = block_merge<R>(f);
-  if (threadIdx.x == 0) out[0] = static_cast<float>(f);
+  finish_full<R>(b, slots, G, out);
 }
 
 template <int R>
@@ -175,18 +207,17 @@ int launch_reduce(const float *x, int64_t n, float *out) {
   SILGPU_REQUIRE(n > 0 || R == R_SUM, "reduce: min/max of an empty array");
   SILGPU_REQUIRE(out != nullptr && (n == 0 || x != nullptr), "reduce: null pointer");
   SILGPU_CTX(c);
-  using T = typename racc<R>::T;
-  T *partial = static_cast<T *>(c->partials);
   if (n == 0) return silgpu_fill_u32(out, 0u, 1);  // sum of nothing: +0.0f
   int64_t blocks;
+  static_assert(kFullBlocks <= kSlots, "a full reduction's partials need a slot each");
   if (reinterpret_cast<uintptr_t>(x) & 3) {
     blocks = cdiv(n, int64_t(kBlock) * 64);
     if (blocks > kFullBlocks) blocks = kFullBlocks;
     int64_t chunk = cdiv(n, blocks);
     blocks = cdiv(n, chunk);
-    reduce_part_scalar_k<R><<<static_cast<unsigned>(blocks), kBlock, 0, c->stream>>>(
-        x, n, chunk, partial);
-    SILGPU_LAUNCH_CHECK("reduce_part_scalar_k");
+    reduce_scalar_k<R><<<static_cast<unsigned>(blocks), kBlock, 0, c->stream>>>(
+        x, n, chunk, c->slots, out);
+    SILGPU_LAUNCH_CHECK("reduce_scalar_k");
   } else {
     int head = static_cast<int>(((16 - (reinterpret_cast<uintptr_t>(x) & 15)) & 15) / 4);
     if (head > n) head = static_cast<int>(n);
@@ -196,13 +227,11 @@ int launch_reduce(const float *x, int64_t n, float *out) {
     const int64_t group = int64_t(kUnroll) * kBlock;
     int64_t chunk4 = cdiv(cdiv(n4 > 0 ? n4 : 1, kFullBlocks), group) * group;
     blocks = n4 > 0 ? cdiv(n4, chunk4) : 1;
-    reduce_part_k<R><<<static_cast<unsigned>(blocks), kBlock, 0, c->stream>>>(
+    reduce_k<R><<<static_cast<unsigned>(blocks), kBlock, 0, c->stream>>>(
         x, head, reinterpret_cast<const float4 *>(x + head), n4, chunk4, x + head + 4 * n4,
-        tail, partial);
-    SILGPU_LAUNCH_CHECK("reduce_part_k");
+        tail, c->slots, out);
+    SILGPU_LAUNCH_CHECK("reduce_k");
   }
-  reduce_finish_k<R><<<1, kBlock, 0, c->stream>>>(partial, static_cast<int>(blocks), out);
-  SILGPU_LAUNCH_CHECK("reduce_finish_k");
   return SILGPU_OK;
 }
 
@@ -305,13 +334,14 @@ __global__ __launch_bounds__(kBlock) void axis_sum_finish_k(const double *__rest
 
 // ---- argmax per row ---------------------------------------------------------
 
+// (value, column) of a candidate maximum.  Columns fit int32 (checked at
+// the entry point), so the pair is two registers and one 64-bit slot.
 struct vi {
   float v;
-  int32_t pad;
-  int64_t i;
+  int32_t i;
 };
 
-constexpr int64_t kNoIndex = INT64_MAX;
+constexpr int32_t kNoIndex = INT32_MAX;  // above every column index
 
 // Larger value wins; equal values keep the smaller index; NaN never wins.
 __device__ __forceinline__ vi better(vi a, vi b) {
@@ -332,7 +362,7 @@ __device__ __forceinline__ vi wave_best(vi x) {
 
 __device__ __forceinline__ vi block_best(vi x) {
   __shared__ float sv[kWaves];
-  __shared__ int64_t si[kWaves];
+  __shared__ int32_t si[kWaves];
   x = wave_best(x);
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   __syncthreads();
@@ -341,82 +371,131 @@ __device__ __forceinline__ vi block_best(vi x) {
     si[wave] = x.i;
   }
   __syncthreads();
-  vi r{sv[0], 0, si[0]};
+  vi r{sv[0], si[0]};
 #pragma unroll
-  for (int w = 1; w < kWaves; ++w) r = better(r, vi{sv[w], 0, si[w]});
+  for (int w = 1; w < kWaves; ++w) r = better(r, vi{sv[w], si[w]});
   return r;
 }
 
 // Within one thread indices only increase, so a strict > keeps the first
 // maximum; NaN is replaced by any number.
 __device__ __forceinline__ void scan1(vi &best, float v, int64_t i) {
-  if (v > best.v || (best.v != best.v && v == v)) best = vi{v, 0, i};
+  if (v > best.v || (best.v != best.v && v == v)) best = vi{v, static_cast<int32_t>(i)};
+}
+
+// A (value, index) pair in one slot: the index (>= 0) in the high word, the
+// value's bits in the low word.  The high word is never all ones, so no
+// packed pair is.
+__device__ __forceinline__ uint64_t pack_vi(vi x) {
+  return (uint64_t(uint32_t(x.i)) << 32) | __float_as_uint(x.v);
+}
+__device__ __forceinline__ vi unpack_vi(uint64_t b) {
+  return vi{__uint_as_float(uint32_t(b)), int32_t(uint32_t(b >> 32))};
 }
 
 // grid = (chunks, rows); workgroup (c, r) scans columns of chunk c of row r.
+// With one chunk it writes out[r]; otherwise chunks 0..chunks-2 publish their
+// (value, index) in slots r*chunks + c and the last chunk of the row, which
+// the dispatcher starts after the row's other chunks, merges them in chunk
+// order and writes out[r].
 __global__ __launch_bounds__(kBlock) void argmax_k(const float *__restrict__ x, int64_t cols,
                                                    int64_t chunk, bool vec,
-                                                   vi *__restrict__ partial,
+                                                   uint64_t *__restrict__ slots,
                                                    int32_t *__restrict__ out) {
   const int64_t r = blockIdx.y;
   const float *row = x + r * cols;
   const int64_t c0 = int64_t(blockIdx.x) * chunk;
   const int64_t c1 = c0 + chunk < cols ? c0 + chunk : cols;
-  vi best{NAN, 0, kNoIndex};
+  vi best{NAN, kNoIndex};
   if (vec) {
-    // Compare each float4 group by its maximum (three fmaxf, which drop
-    // NaN) and, only when the group improves on the best so far (a branch
-    // the wavefront rarely takes once its maximum has settled), locate the
-    // first lane holding that maximum.  Groups are visited in increasing
-    // order and replace the best only when strictly larger, so the first
-    // maximum of this thread's columns wins, as in scan1.
+    // A thread scans batches of kUnroll float4 groups (kUnroll * kBlock
+    // apart).  Each batch is reduced to its maximum (fmaxf drops NaN) and
+    // compared once with the best so far; a batch that is strictly larger
+    // (or the first batch with a number) becomes the best and is kept in
+    // registers, and the column is located in the kept batch only after the
+    // scan -- the first element equal to the best, which is the first
+    // maximum of the thread's columns since batches are visited in order.
+    // Walking an improving batch inside the loop instead (the loop then
+    // carries the column search) measured 5% slower than a plain max scan;
+    // keeping the batch costs 1%.
     const float4 *r4 = reinterpret_cast<const float4 *>(row);
     int64_t i = c0 / 4 + threadIdx.x;
     const int64_t e4 = c1 / 4;
-    auto scan4 = [&](const float4 &v, int64_t g) {
-      const float m = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
-      if (m > best.v || (best.v != best.v && m == m)) {
-        const int j = v.x == m ? 0 : v.y == m ? 1 : v.z == m ? 2 : 3;
-        best = vi{m, 0, g * 4 + j};
-      }
-    };
+    float4 keep[kUnroll];
+    int64_t keep_i = -1;
     for (; i + (kUnroll - 1) * kBlock < e4; i += kUnroll * kBlock) {
       float4 v[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) v[u] = load_nt(r4 + i + u * kBlock);
+      // All loads issued before the first use (left to itself the scheduler
+      // starts the maxima after two loads and waits there).
+      __builtin_amdgcn_sched_barrier(0);
+      float m = fmaxf(fmaxf(v[0].x, v[0].y), fmaxf(v[0].z, v[0].w));
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) scan4(v[u], i + u * kBlock);
+      for (int u = 1; u < kUnroll; ++u)
+        m = fmaxf(m, fmaxf(fmaxf(v[u].x, v[u].y), fmaxf(v[u].z, v[u].w)));
+      if (m > best.v || (best.v != best.v && m == m)) {
+        best.v = m;
+        keep_i = i;
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) keep[u] = v[u];
+      }
     }
-    for (; i < e4; i += kBlock) scan4(load_nt(r4 + i), i);
+    if (keep_i >= 0) {
+      // the first element of the kept batch equal to its maximum
+      int64_t col = 0;
+#pragma unroll
+      for (int u = kUnroll - 1; u >= 0; --u) {
+        const float4 w = keep[u];
+        const int j = w.x == best.v ? 0 : w.y == best.v ? 1 : w.z == best.v ? 2
+                    : w.w == best.v ? 3 : -1;
+        if (j >= 0) col = (keep_i + int64_t(u) * kBlock) * 4 + j;
+      }
+      best.i = static_cast<int32_t>(col);
+    }
+    // the columns after the last whole batch, group by group
+    for (; i < e4; i += kBlock) {
+      const float4 v = load_nt(r4 + i);
+      const float m = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
+      if (m > best.v || (best.v != best.v && m == m)) {
+        const int j = v.x == m ? 0 : v.y == m ? 1 : v.z == m ? 2 : 3;
+        best = vi{m, static_cast<int32_t>(i * 4 + j)};
+      }
+    }
   } else {
     for (int64_t i = c0 + threadIdx.x; i < c1; i += kBlock) scan1(best, row[i], i);
   }
-  vi b = block_best(best);
-  if (threadIdx.x != 0) return;
-  if (gridDim.x == 1)
-    out[r] = static_cast<int32_t>(b.i == kNoIndex ? 0 : b.i);
-  else
-    partial[r * gridDim.x + blockIdx.x] = b;
-}
-
-// One workgroup per row merges that row's chunk results.
-__global__ __launch_bounds__(kBlock) void argmax_finish_k(const vi *__restrict__ partial,
-                                                          int64_t chunks,
-                                                          int32_t *__restrict__ out) {
-  const int64_t r = blockIdx.x;
-  vi f{NAN, 0, kNoIndex};
+  const vi b = block_best(best);
+  const int64_t chunks = gridDim.x;
+  if (chunks == 1) {
+    if (threadIdx.x == 0) out[r] = b.i == kNoIndex ? 0 : b.i;
+    return;
+  }
+  uint64_t *row_slots = slots + r * chunks;
+  if (blockIdx.x != chunks - 1) {
+    if (threadIdx.x == 0) slot_publish(row_slots + blockIdx.x, pack_vi(b));
+    return;
+  }
+  // The row's finish, in chunk order (thread t takes chunks t, t + kBlock, ...).
+  vi f{NAN, kNoIndex};
   for (int64_t j0 = threadIdx.x; j0 < chunks; j0 += kFinishLoads * kBlock) {
-    vi v[kFinishLoads];
+    uint64_t seen[kFinishLoads];
 #pragma unroll
     for (int g = 0; g < kFinishLoads; ++g) {
       const int64_t j = j0 + g * kBlock;
-      v[g] = j < chunks ? partial[r * chunks + j] : vi{NAN, 0, kNoIndex};
+      seen[g] = j < chunks - 1 ? slot_peek(row_slots + j) : 0;
     }
 #pragma unroll
-    for (int g = 0; g < kFinishLoads; ++g) f = better(f, v[g]);
+    for (int g = 0; g < kFinishLoads; ++g) {
+      const int64_t j = j0 + g * kBlock;
+      vi v{NAN, kNoIndex};
+      if (j < chunks - 1) v = unpack_vi(slot_take(row_slots + j, seen[g]));
+      else if (j == chunks - 1) v = b;
+      f = better(f, v);
+    }
   }
   f = block_best(f);
-  if (threadIdx.x == 0) out[r] = static_cast<int32_t>(f.i == kNoIndex ? 0 : f.i);
+  if (threadIdx.x == 0) out[r] = f.i == kNoIndex ? 0 : f.i;
 }
 
 // Short rows: one wavefront per row.
@@ -427,22 +506,26 @@ __global__ __launch_bounds__(kBlock) void argmax_wave_k(const float *__restrict_
   const int lane = threadIdx.x % kWave;
   if (r >= rows) return;
   const float *row = x + r * cols;
-  vi best{NAN, 0, kNoIndex};
+  vi best{NAN, kNoIndex};
   for (int64_t i = lane; i < cols; i += kWave) scan1(best, row[i], i);
   best = wave_best(best);
-  if (lane == 0) out[r] = static_cast<int32_t>(best.i == kNoIndex ? 0 : best.i);
+  if (lane == 0) out[r] = best.i == kNoIndex ? 0 : best.i;
 }
 
-// Chunks per row: enough workgroups (rows * chunks ~ 2048) to fill the GPU,
-// each chunk >= 16384 elements and a whole number of kUnroll*kBlock float4
-// groups; the partials must fit the scratch area.
-int64_t chunk_len(int64_t rows, int64_t cols, size_t partial_bytes, int64_t &chunks) {
-  int64_t target = 2048 / (rows > 0 ? rows : 1);
+// Chunks per row: enough workgroups (rows * chunks ~ `total`) to fill the
+// GPU, each chunk >= 16384 elements and a whole number of kUnroll*kBlock
+// float4 groups; the partials must fit the scratch area (row sums) and
+// rows * chunks the slots (argmax).
+int64_t chunk_len(int64_t rows, int64_t cols, size_t partial_bytes, int64_t &chunks,
+                  int64_t total = 2048) {
+  int64_t target = total / (rows > 0 ? rows : 1);
   if (target < 1) target = 1;
   int64_t by_size = cols / 16384;
   if (by_size < 1) by_size = 1;
   chunks = target < by_size ? target : by_size;
-  while (chunks > 1 && rows * chunks * int64_t(partial_bytes) > int64_t(kPartialBytes)) chunks /= 2;
+  while (chunks > 1 && (rows * chunks * int64_t(partial_bytes) > int64_t(kPartialBytes) ||
+                        rows * chunks > kSlots))
+    chunks /= 2;
   const int64_t group = int64_t(kUnroll) * kBlock * 4;
   int64_t chunk = cdiv(cdiv(cols, chunks), group) * group;
   chunks = cdiv(cols, chunk);
@@ -560,16 +643,13 @@ int silgpu_argmax_rows_f32(const float *d_in, int64_t rows, int64_t cols, int32_
   }
   const bool vec = cols % 4 == 0 && aligned16(d_in);
   int64_t chunks;
-  const int64_t chunk = chunk_len(rows, cols, sizeof(vi), chunks);
-  vi *partial = static_cast<vi *>(c->partials);
+  const int64_t chunk = chunk_len(rows, cols, sizeof(uint64_t), chunks, kFullBlocks);
+  if (chunks > 1 && rows * chunks > kSlots)
+    return set_error(SILGPU_ERR_INVALID, "silgpu_argmax_rows_f32: %lld x %lld partials exceed "
+                     "the %d slots", (long long)rows, (long long)chunks, kSlots);
   dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(rows));
-  argmax_k<<<grid, kBlock, 0, c->stream>>>(d_in, cols, chunk, vec, partial, d_out);
+  argmax_k<<<grid, kBlock, 0, c->stream>>>(d_in, cols, chunk, vec, c->slots, d_out);
   SILGPU_LAUNCH_CHECK("argmax_k");
-  if (chunks > 1) {
-    argmax_finish_k<<<static_cast<unsigned>(rows), kBlock, 0, c->stream>>>(partial, chunks,
-                                                                           d_out);
-    SILGPU_LAUNCH_CHECK("argmax_finish_k");
-  }
   return SILGPU_OK;
 }
 

@@ -58,6 +58,8 @@ int init_locked() {
   // Default priority on purpose: streams of mixed priority are avoided.
   SILGPU_HIP_CHECK(hipStreamCreateWithFlags(&g_ctx.stream, hipStreamNonBlocking));
   SILGPU_HIP_CHECK(hipMalloc(&g_ctx.partials, kPartialBytes));
+  SILGPU_HIP_CHECK(hipMalloc(&g_ctx.slots, kSlots * sizeof(uint64_t)));
+  SILGPU_HIP_CHECK(hipMemsetAsync(g_ctx.slots, 0, kSlots * sizeof(uint64_t), g_ctx.stream));
   // With device 0 current: this device's copy of the no-allocation scratch.
   void *sp = nullptr;
   SILGPU_HIP_CHECK(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)));

@@ -599,6 +599,9 @@ SKINNY_CASES = [
     (32, 4096, 64, 0, 0, 0, 0, 1), (8, 36, 4100, 1, 3, 0, 0, 0),
     # wide and deep: the automatic plan takes 64-column groups (N odd: back to 32)
     (8, 4096, 4096, 0, 0, 0, 0, 0), (4, 4097, 4096, 0, 0, 0, 0, 0), (16, 4096, 4096, 1, 0, 0, 0, 1),
+    # the boundary of that rule: N = 3072 and narrow N with very deep K keep
+    # 32-column groups
+    (16, 3072, 4096, 0, 0, 0, 0, 0), (32, 768, 32768, 0, 0, 0, 0, 1),
 ]
 
 
