@@ -21,6 +21,11 @@ Infinity Cache cannot serve repeated reads.
 cpu_baseline: cblas_sgemm from OpenBLAS (the x86 stand-in for the
 reference's Accelerate call, include/cpu.h:239-264) on the headline 8192^3
 workload, on the host cores of the same machine, for a sample of ~10 s.
+Every secondary row of the cpu.h path (the SGEMM sweep including config 1's
+1024^3, GEMV, the small-batch product, linear_sigmoid, the row ops, the
+reductions and the affine chain) carries its own cpu_baseline: OpenBLAS for
+the products, the oracle's single-threaded loops for the vDSP calls, each on
+a stated sample of ~1 s.
 """
 
 from __future__ import annotations
@@ -56,6 +61,8 @@ def parse():
     ap.add_argument("--only", default="", help="comma list of workloads (default: all)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-row-seconds", type=float, default=1.0,
+                    help="sample length of each secondary row's CPU baseline")
     return ap.parse_args()
 
 
@@ -387,6 +394,114 @@ def cpu_baseline(seconds: float) -> dict:
                            "sample": f"{S1}^3, {runs1} whole calls in {el1:.1f} s"}}
 
 
+def _cpu_rate(fn, units_per_call: float, seconds: float):
+    """One untimed call, then whole calls until `seconds` have elapsed;
+    returns (units per second, calls, elapsed s)."""
+    fn()
+    runs, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        runs += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            return units_per_call * runs / el, runs, el
+
+
+def cpu_rows(seconds: float) -> dict:
+    """The reference's cpu.h path restated on this host for each secondary
+    workload, keyed like the `secondary` rows: cblas_sgemm (OpenBLAS, the
+    x86 stand-in for Accelerate, include/cpu.h:239-264) on up to 16 threads
+    for the products, and the oracle's single-threaded scalar loops (-O2
+    x86-64-v3, no contraction) for the vDSP calls and the host loops: softmax
+    with the row-minimum shift (include/array.h:2140-2149), two-pass
+    layer_norm (include/cpu.h:352-373), sum over axis 1 in float
+    (include/array.h:2309-2314), sequential sum, min, max, the argmax loop
+    (include/array.h:1728-1745) and the affine chain node by node.  Each is
+    timed on a bounded sample of the GPU row's workload (stated per row) for
+    about `seconds`, in the GPU row's unit."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import openblas  # test-infrastructure baseline, oracle/openblas.py
+    import oracle  # oracle/oracle.py over liboracle.so
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except Exception:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, 16))
+    g = np.random.default_rng(SEED + 1)
+    out = {}
+
+    def row(key, rate, unit, ncores, sample, runs, el):
+        out[key] = {"value": round(rate, 4 if unit == "TFLOP/s" else 2), "unit": unit,
+                    "cores": ncores, "kind": "port",
+                    "sample": f"{sample}; {runs} whole calls in {el:.2f} s after one untimed call"}
+
+    openblas.set_threads(cores)
+    blas = f"cblas_sgemm (OpenBLAS, {Path(openblas.LIB_PATH).name}), {cores} threads"
+    for S in (1024, 2048, 4096):
+        A, B = uniform(g, (S, S)), uniform(g, (S, S))
+        Cm = np.empty((S, S), np.float32)
+        r, n, el = _cpu_rate(lambda: openblas.sgemm(A, B, Cm), 2.0 * S ** 3 / 1e12, seconds)
+        row(f"sgemm_{S}", r, "TFLOP/s", cores, f"{blas}, {S}^3 NN uniform[-1,1] (the full workload)",
+            n, el)
+    K = N = 4096
+    x = normal(g, (1, K), 0.02)
+    Bm = normal(g, (K, N), 0.02)
+    y = np.empty((1, N), np.float32)
+    nbytes = 4.0 * (K + K * N + N)
+    r, n, el = _cpu_rate(lambda: openblas.sgemm(x, Bm, y), nbytes / 1e9, seconds)
+    row("gemv_1x4096x4096", r, "GB/s", cores, f"{blas}, M=1 (the full workload)", n, el)
+    r1, n1, el1 = _cpu_rate(lambda: oracle.gemv_f32(x[0], Bm), nbytes / 1e9, seconds)
+    out["gemv_1x4096x4096"]["scalar_loop_one_thread"] = {
+        "value": round(r1, 2), "unit": "GB/s", "cores": 1,
+        "sample": f"oracle_gemv_f32 scalar loop, full workload, {n1} calls in {el1:.2f} s"}
+    M, N, K = 32, 768, 4096
+    A, Bm = normal(g, (M, K), 0.02), normal(g, (K, N), 0.02)
+    Cm = np.empty((M, N), np.float32)
+    r, n, el = _cpu_rate(lambda: openblas.sgemm(A, Bm, Cm), 4.0 * (M * K + K * N + M * N) / 1e9,
+                         seconds)
+    row("sgemm_32x768x4096", r, "GB/s", cores, f"{blas}, the full workload", n, el)
+    M, N, K = 256, 4096, 4096
+    X, W, bias = normal(g, (M, K), 0.02), normal(g, (K, N), 0.02), normal(g, N, 0.02)
+    Y = np.empty((M, N), np.float32)
+
+    def lin_sig():
+        openblas.sgemm(X, W, Y)
+        oracle.bias_sigmoid(Y, bias)
+
+    r, n, el = _cpu_rate(lin_sig, 2.0 * M * N * K / 1e12, seconds)
+    row("linear_sigmoid_256x4096x4096", r, "TFLOP/s", cores,
+        f"{blas} + oracle_bias_sigmoid loop (one thread), the full workload", n, el)
+    R, Cc = 256, 8192  # 256 of the 4096 rows of the [4096, 8192] workload
+    xr = normal(g, (R, Cc), 3.0)
+    ones, zeros = np.ones(Cc, np.float32), np.zeros(Cc, np.float32)
+    sub = f"{R} of the 4096 rows of [4096, 8192] N(0, 3), one thread"
+    r, n, el = _cpu_rate(lambda: oracle.softmax_rows_ref(xr), 8.0 * R * Cc / 1e9, seconds)
+    row("softmax_4096x8192", r, "GB/s", 1, f"oracle_softmax_rows_ref, {sub}", n, el)
+    r, n, el = _cpu_rate(lambda: oracle.layer_norm_ref(xr, ones, zeros),
+                         (8.0 * R * Cc + 8 * Cc) / 1e9, seconds)
+    row("layer_norm_4096x8192", r, "GB/s", 1, f"oracle_layer_norm_ref, {sub}", n, el)
+    r, n, el = _cpu_rate(lambda: oracle.sum_axis_ref(xr, 1), (4.0 * R * Cc + 4 * R) / 1e9,
+                         seconds)
+    row("sum_axis1_4096x8192", r, "GB/s", 1, f"oracle_sum_axis_ref, {sub}", n, el)
+    n64 = 16 * 1024 * 1024  # a quarter of the 64M-element workload
+    v = uniform(g, n64)
+    v[(n64 * 7) // 9 + 1] = 2.0
+    sub = "16M of the 64M uniform[-1,1] elements, one thread"
+    for key, fn, nm in (("sum_64M", lambda: oracle.sum_ref(v), "oracle_sum_ref"),
+                        ("min_64M", lambda: oracle.fmin(v), "oracle_min"),
+                        ("max_64M", lambda: oracle.fmax(v), "oracle_max"),
+                        ("argmax_64M", lambda: oracle.argmax_rows_cpu_ref(v.reshape(1, -1)),
+                         "oracle_argmax_rows_cpu_ref")):
+        r, n, el = _cpu_rate(fn, 4.0 * n64 / 1e9, seconds)
+        row(key, r, "GB/s", 1, f"{nm}, {sub}", n, el)
+    sc = g.uniform(0.9, 1.1, 20).astype(np.float32)
+    of = g.uniform(-0.1, 0.1, 20).astype(np.float32)
+    r, n, el = _cpu_rate(lambda: oracle.affine_chain(v, sc, of), 8.0 * n64 / 1e9, seconds)
+    row("affine_chain20_64M", r, "GB/s", 1, f"oracle_affine_chain (20 fma nodes), {sub}", n, el)
+    return out
+
+
 def host_cpu_info() -> dict:
     """nproc, the CPUs this process may use, and sockets x cores from
     /proc/cpuinfo (Linux)."""
@@ -502,7 +617,9 @@ def main():
         secondary["copy_256MiB"] = {"value": round(r["gbs"], 1), "unit": "GB/s",
                                     "us": round(r["us"], 2)}
     if want("sgemm_sweep"):
-        for s in (2048, 4096):
+        # 1024^3 is BASELINE config 1 (the reference times it through
+        # sil::array::dot, bench/micro/bench_sgemm.cpp:34)
+        for s in (1024, 2048, 4096):
             r = bench_sgemm(nat, s, 20, 3, g, min_warm_s=WARM_S)
             log(f"sgemm {s}^3 {r}")
             secondary[f"sgemm_{s}"] = {"value": round(r["tflops_kernel"], 2), "unit": "TFLOP/s",
@@ -554,6 +671,10 @@ def main():
         log("cpu baseline")
         cpu = cpu_baseline(args.cpu_seconds)
         log(f"cpu {cpu}")
+        for key, base in cpu_rows(args.cpu_row_seconds).items():
+            log(f"cpu {key} {base}")
+            if key in secondary:
+                secondary[key]["cpu_baseline"] = base
 
     line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
