@@ -247,6 +247,15 @@ def bench_rowops(nat, g, reps=20):
         ms_hot = t.ms_per_launch(lambda i: fn(i, 0), reps)
         out[name] = {"gbs": nb / (ms / 1e3) / 1e9, "gbs_hot": nb / (ms_hot / 1e3) / 1e9,
                      "us": ms * 1e3, "bytes": nb}
+    # The ceiling beside them: a plain device copy of the same 128 MiB input
+    # into the same output buffers (the runtime's copy kernel), same rotation.
+    nb = 8 * R * Cc
+    ms = t.ms_per_launch(lambda i: nat.call("silgpu_memcpy_d2d", nat.vp(ys[i % pairs]),
+                                            nat.vp(xs[i % pairs]), 4 * R * Cc), reps, pairs)
+    copy_gbs = nb / (ms / 1e3) / 1e9
+    for name in ("softmax", "layer_norm"):
+        out[name]["copy_gbs"] = copy_gbs
+        out[name]["of_copy"] = out[name]["gbs"] / copy_gbs
     return out
 
 
@@ -594,6 +603,10 @@ def main():
                                            "us": round(v["us"], 2),
                                            "roofline": roofline("hbm", v["gbs"],
                                                                 load_traffic(f"{k}_4096x8192"))}
+            if "copy_gbs" in v:
+                # same-bytes device copy timed in this run: the shape-free ceiling
+                secondary[f"{k}_4096x8192"]["copy_same_bytes_gbs"] = round(v["copy_gbs"], 1)
+                secondary[f"{k}_4096x8192"]["of_copy"] = round(v["of_copy"], 3)
     if want("reductions"):
         r = bench_reductions(nat, g)
         log(f"reductions {r}")

@@ -100,7 +100,9 @@ int silgpu_host_alloc(size_t bytes, void **h_ptr);
 int silgpu_host_free(void *h_ptr);
 
 /* Copies, ordered on the library stream.  h2d returns once the source may be
- * reused; d2h returns once the destination holds the data; d2d is async.
+ * reused; d2h returns once the destination holds the data; d2d is async, its
+ * two ranges must not overlap, and 16-byte-aligned ranges are moved by the
+ * library's own streaming kernel (the rest by the runtime's copy).
  * Together they stand in for the host's direct access to MTLBuffer contents
  * (include/unified_memory.h:76, include/array.h:951-958). */
 int silgpu_memcpy_h2d(void *d_dst, const void *h_src, size_t bytes);

@@ -23,6 +23,12 @@
 namespace silgpu {
 namespace {
 
+// exp(m - M) for a partial sum exponentiated against its own maximum m
+// (m <= M); a partial with no finite maximum contributes nothing.
+__device__ __forceinline__ float rescale(float m, float M) {
+  return m == -INFINITY ? 0.0f : expf(m - M);
+}
+
 // Reductions over a group of NT threads that own one row.  NT == 64: one
 // wavefront; NT > 64: the whole workgroup (NT threads) through LDS.
 template <int NT>
@@ -45,6 +51,62 @@ struct group {
 #pragma unroll
       for (int w = 1; w < kWaves; ++w) r = op(r, red[w]);
       return r;
+    }
+  }
+
+  // As reduce, for a kernel that makes each SLOT's reduction once: the slot
+  // has its own LDS array, so no barrier guards earlier reads of it.
+  template <int SLOT, typename T, typename F>
+  __device__ static T reduce_once(T v, F op) {
+    static_assert(NT == kWave || NT >= 256, "one group per workgroup");
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = op(v, __shfl_xor(v, o, kWave));
+    if constexpr (NT == kWave) {
+      return v;
+    } else {
+      __shared__ T red[kWaves];
+      const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+      if (lane == 0) red[wave] = v;
+      __syncthreads();
+      T r = red[0];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) r = op(r, red[w]);
+      return r;
+    }
+  }
+
+  // Softmax statistics of the group: each thread holds the maximum m of its
+  // values and the sum s of exp(value - m); returns the group's maximum M
+  // and sum S of exp(value - M).  One LDS exchange (one barrier): every
+  // wave publishes its (max, sum) pair once.  Used once per kernel.
+  __device__ static void softmax_stats(float m, double s, float &M, double &S) {
+    static_assert(NT == kWave || NT >= 256, "one group per workgroup");
+    float mw = m;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mw = fmaxf(mw, __shfl_xor(mw, o, kWave));
+    double sw = s * static_cast<double>(rescale(m, mw));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sw += __shfl_xor(sw, o, kWave);
+    if constexpr (NT == kWave) {
+      M = mw;
+      S = sw;
+    } else {
+      __shared__ float rm[kWaves];
+      __shared__ double rs[kWaves];
+      const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+      if (lane == 0) {
+        rm[wave] = mw;
+        rs[wave] = sw;
+      }
+      __syncthreads();
+      float mg = rm[0];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) mg = fmaxf(mg, rm[w]);
+      double sg = 0.0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) sg += rs[w] * static_cast<double>(rescale(rm[w], mg));
+      M = mg;
+      S = sg;
     }
   }
 };
@@ -139,29 +201,36 @@ __global__ __launch_bounds__(row_block<NT>()) void softmax_reg_k(const float *__
   const float *src = in + r * cols;
   float x[V][4];
   load_row<NT, V, M>(src, cols, t, -INFINITY, x);
+  // Each thread exponentiates against its own maximum m, so the row's
+  // maximum and sum meet in one exchange: (m, s) pairs combine as
+  // M = max m, S = sum s * exp(m - M).
   float m = -INFINITY;
 #pragma unroll
   for (int k = 0; k < V; ++k)
 #pragma unroll
     for (int j = 0; j < 4; ++j) m = fmaxf(m, x[k][j]);
-  m = group<NT>::reduce(m, fmax_op{});
+  // A thread with no finite maximum (padding, -inf entries) exponentiates
+  // against 0: its -inf entries give 0 and NaN entries stay NaN.
+  const float m_eff = m == -INFINITY ? 0.0f : m;
   double s = 0.0;
 #pragma unroll
   for (int k = 0; k < V; ++k)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float e = expf(x[k][j] - m);  // padding: exp(-inf) = 0
+      float e = expf(x[k][j] - m_eff);
       x[k][j] = e;
       s += static_cast<double>(e);
     }
-  s = group<NT>::reduce(s, dsum_op{});
-  // One reciprocal per row, then a multiply per element: within about 1 ulp of the
-  // quotient and ~2% faster on [4096, 8192] than a division per element.
-  const float inv = 1.0f / static_cast<float>(s);
+  float mr;
+  double sr;
+  group<NT>::softmax_stats(m, s, mr, sr);
+  // One reciprocal per row, then a multiply per element.
+  const float inv = 1.0f / static_cast<float>(sr);
+  const float c = rescale(m, mr) * inv;
 #pragma unroll
   for (int k = 0; k < V; ++k)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) x[k][j] = x[k][j] * inv;
+    for (int j = 0; j < 4; ++j) x[k][j] = x[k][j] * c;
   store_row<NT, V, M>(out + r * cols, cols, t, x);
 }
 
@@ -180,7 +249,7 @@ __global__ __launch_bounds__(row_block<NT>()) void layer_norm_reg_k(
   for (int k = 0; k < V; ++k)
 #pragma unroll
     for (int j = 0; j < 4; ++j) s += static_cast<double>(x[k][j]);
-  s = group<NT>::reduce(s, dsum_op{});
+  s = group<NT>::template reduce_once<0>(s, dsum_op{});
   const float mu = static_cast<float>(s / static_cast<double>(cols));
   double ss = 0.0;
 #pragma unroll
@@ -192,7 +261,7 @@ __global__ __launch_bounds__(row_block<NT>()) void layer_norm_reg_k(
       x[k][j] = d;
       if (M == kFull || c < cols) ss += static_cast<double>(d) * static_cast<double>(d);
     }
-  ss = group<NT>::reduce(ss, dsum_op{});
+  ss = group<NT>::template reduce_once<1>(ss, dsum_op{});
   const float var = static_cast<float>(ss / static_cast<double>(cols));
   const float inv_std = 1.0f / sqrtf(var + eps);
   float g[V][4], b[V][4];

@@ -88,3 +88,30 @@ def test_small_classes_and_pinned_host_pool(native):
     assert np.array_equal(down(native, d, 4), [1.0, 2.0, 3.0, 4.0])
     native.call("silgpu_host_free", C.c_void_p(h2))
     native.call("silgpu_pool_trim")
+
+
+# (bytes, source offset, destination offset): empty, below one 16-byte slot,
+# one slot, a slot plus a tail, exactly one 32 KiB workgroup block, one block
+# plus a partial block and a tail, 64 MiB + 3; offsets that keep both
+# pointers 16-byte aligned (the streaming kernel), and ones that do not (the
+# runtime's copy)
+COPY_CASES = [(0, 0, 0), (7, 0, 0), (16, 0, 0), (21, 0, 0), (32768, 0, 0), (32768 + 4096 + 5, 0, 0),
+              (64 * 1024 * 1024 + 3, 0, 0), (100_000, 16, 48), (100_000, 4, 0), (100_001, 0, 3)]
+
+
+@pytest.mark.parametrize("nbytes,so,do", COPY_CASES)
+def test_memcpy_d2d(native, nbytes, so, do):
+    announce(f"memcpy_d2d {nbytes} B, offsets {so}/{do}")
+    g = np.random.default_rng(nbytes + so)
+    src = g.integers(0, 256, nbytes + so, dtype=np.uint8)
+    s = native.DeviceBuffer(max(nbytes + so, 1))
+    d = native.DeviceBuffer(nbytes + do + 64)
+    if nbytes + so:
+        s.upload(src)
+    guard = np.full(nbytes + do + 64, 0xA5, np.uint8)
+    d.upload(guard)
+    native.call("silgpu_memcpy_d2d", C.c_void_p(d.at(do)), C.c_void_p(s.at(so)), C.c_size_t(nbytes))
+    out = d.download(nbytes + do + 64, np.uint8)
+    assert np.array_equal(out[do:do + nbytes], src[so:so + nbytes])
+    # nothing outside the destination range is touched
+    assert np.all(out[:do] == 0xA5) and np.all(out[do + nbytes:] == 0xA5)
