@@ -683,11 +683,12 @@ __global__ __launch_bounds__(kSkWaves *kWave) void sgemm_skinny_k(gemm_args p) {
 // model (tests/test_gemm_layout.py).  256 x 256: 8 waves (2 x 4) of 128 x 64;
 // 128 x 128: 4 waves (2 x 2) of 64 x 64; 128 x 64: 4 waves of 64 x 32.  The
 // next K tile's loads are issued before the current tile is multiplied, and
-// one s_waitcnt + barrier ends each tile.  256 x 256 tiles run four 16-deep
-// stages (130 KB of the 160 KB LDS), so each barrier waits only for the
-// stage consumed next while two more load; the smaller tiles run two
-// stages, 32 deep where K allows (four 16-deep stages measured slower for
-// them: 2048^3 123.9 against 126.2 TFLOP/s with 128 x 64 tiles).
+// one s_waitcnt + barrier ends each tile.  256 x 128 tiles run three 16-deep
+// stages (75 KB of LDS, two workgroups per CU), so each barrier waits only
+// for the stage consumed next while one more loads; 256 x 256 tiles (8
+// waves) four stages (130 KB); the smaller tiles two stages, 32 deep where
+// K allows (four 16-deep stages measured slower for them: 2048^3 123.9
+// against 126.2 TFLOP/s with 128 x 64 tiles).
 constexpr int kDtlBK = 16;  // K granularity of the path (BK = 16 or 32)
 
 // Pitch (floats) of an M/N-contiguous window for a tile extent X: one k row
@@ -699,10 +700,10 @@ constexpr int dtl_pitch() {
   return X == 256 ? 260 : X == 128 ? 264 : 272;
 }
 
-// BM x BN tiles, NW waves in a 2 x NW/2 grid: 256 x 256 with 8 waves (128 x
-// 64 each, two waves per SIMD) or 4 waves (128 x 128, one wave per SIMD with
-// 256 accumulators per lane); 128 x 128 with 4 waves of 64 x 64; 128 x 64
-// with 4 waves of 64 x 32.
+// BM x BN tiles, NW waves in a 2 x NW/2 grid: 256 x 128 with 4 waves of 128
+// x 64 (two workgroups per CU, so two waves per SIMD), 256 x 256 with 8
+// waves of 128 x 64 (one workgroup per CU); 128 x 128 with 4 waves of 64 x
+// 64; 128 x 64 with 4 waves of 64 x 32.
 template <int BM, int BN, int BK, int NW = (BM == 256 ? 8 : 4), int NS = 2>
 struct dtl_cfg {
   static constexpr int WM = 2, WN = NW / 2;
@@ -715,10 +716,10 @@ struct dtl_cfg {
   static constexpr int kStage = kOperandA + kOperandB;
   static constexpr int kLdsBytes = NS * kStage * 4;  // static, NS arrays of kStage floats
   // Waves per SIMD the register allocation aims at: one 8-wave workgroup per
-  // CU (LDS allows no second) for 256 x 256, three 4-wave workgroups for the
-  // smaller tiles.  Without it the compiler squeezes the 256 tile toward
+  // CU (LDS allows no second) for 256 x 256, two 4-wave workgroups for 256 x
+  // 128, three for the smaller tiles.  Without it the compiler squeezes the 256 tile toward
   // three waves and serialises the first fragment reads of every K tile.
-  static constexpr int kWavesPerEU = (BM == 256 && BN == 256) ? NW / 4 : 3;
+  static constexpr int kWavesPerEU = (BM == 256 && BN == 256) ? NW / 4 : BM == 256 ? 2 : 3;
   static_assert(BK % kDtlBK == 0 && kWinA % (WM * WN) == 0 && kWinB % (WM * WN) == 0,
                 "windows per wave");
   static_assert(kLdsBytes <= 160 * 1024, "LDS");
@@ -782,7 +783,7 @@ __global__ __launch_bounds__((dtl_cfg<BM, BN, BK, NWV, NS>::kThreads))
 __attribute__((amdgpu_waves_per_eu(dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU,
                                    dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU))) void sgemm_dtl_k(gemm_args p) {
   using D = dtl_cfg<BM, BN, BK, NWV, NS>;
-  static_assert(NS == 2 || NS == 4, "stages");
+  static_assert(NS >= 2 && NS <= 4, "stages");
   using F = mfma<16>;
   constexpr int TM = D::TM, TN = D::TN, NW = D::WM * D::WN;
   constexpr int WPA = D::kWinA / NW, WPB = D::kWinB / NW;  // windows per wave
@@ -794,7 +795,7 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU,
   __shared__ __attribute__((aligned(16))) float lds0[D::kStage];
   __shared__ __attribute__((aligned(16))) float lds1[D::kStage];
   __shared__ __attribute__((aligned(16))) float lds2[NS > 2 ? D::kStage : 4];
-  __shared__ __attribute__((aligned(16))) float lds3[NS > 2 ? D::kStage : 4];
+  __shared__ __attribute__((aligned(16))) float lds3[NS > 3 ? D::kStage : 4];
   const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
   const int wm = wave / D::WN, wn = wave % D::WN;
   int tm, tn;
@@ -956,8 +957,10 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU,
   };
   if (KT > 0) {
     issue(0, lds0);
-    if constexpr (NS == 4) {
+    if constexpr (NS >= 3) {
       if (1 < KT) issue(1, lds1);
+    }
+    if constexpr (NS == 4) {
       if (2 < KT) issue(2, lds2);
     }
     land(0);
@@ -997,6 +1000,12 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU,
     for (int kt = 0; kt < KT; kt += 2) {
       tile(lds0, lds1, kt);
       if (kt + 1 < KT) tile(lds1, lds0, kt + 1);
+    }
+  } else if constexpr (NS == 3) {
+    for (int kt = 0; kt < KT; kt += 3) {
+      tile(lds0, lds2, kt);
+      if (kt + 1 < KT) tile(lds1, lds0, kt + 1);
+      if (kt + 2 < KT) tile(lds2, lds1, kt + 2);
     }
   } else {
     for (int kt = 0; kt < KT; kt += 4) {
@@ -1317,11 +1326,12 @@ int launch_tb(const gemm_args &a, int64_t batch, int splits, bool vec, hipStream
                 (BM == 128 && BN == 64)) {
     if (vec && a.M % BM == 0 && a.N % BN == 0 && a.K % kDtlBK == 0) {
       if constexpr (BM == 256) {
-        // Four 16-deep stages rather than two 32-deep ones: the barrier
-        // after each stage waits only for the loads of the stage that is
-        // consumed next, with two more in flight (8192^3: 141.2 against
-        // 139.6 TFLOP/s; 4096^3: 138.3 against 136.5, MI355X).
-        return launch_dtl<BM, BN, kDtlBK, 8, 4, TA, TB>(a, batch, splits, s);
+        // The 256 x 256 plan runs as 256 x 128 tiles of 4 waves with three
+        // 16-deep stages (75 KB of LDS), two workgroups per CU: each waits
+        // at its own barriers while the other keeps the matrix cores busy
+        // (8192^3: 142.5 TFLOP/s against 141.4 for one 256 x 256 workgroup
+        // of 8 waves with four stages; 4096^3: 138.9 against 137.7, MI355X).
+        return launch_dtl<BM, BN / 2, kDtlBK, 4, 3, TA, TB>(a, batch, splits, s);
       } else if constexpr (BN == 128) {
         return launch_dtl<BM, BN, kDtlBK, 4, 2, TA, TB>(a, batch, splits, s);
       } else {
