@@ -323,6 +323,21 @@ REF_TRAIN_MS = {64: 1.11, 128: 1.51}
 # (bench/README.md:205-220): ms.
 REF_MNIST_MS = {"classifier_train_epoch_ms": 283.83, "classifier_inference_ms": 0.920,
                 "autoencoder_train_epoch_ms": 1080.0, "autoencoder_inference_ms": 8.65}
+# The reference's GPU micro-benchmarks on the M1 Pro, sil-gpu column
+# (bench/README.md:96-153): us per iteration (the op, its eval and the wait).
+REF_MICRO_US = {
+    "broadcast (1024x1024)+(1024)": 327, "broadcast (4096x512)+(512)": 412,
+    "broadcast (4096x4096)+(4096)": 1050,
+    "add (1000000)": 317, "add (10000000)": 967, "mul (1000000)": 316, "mul (10000000)": 993,
+    "div (1000000)": 319, "div (10000000)": 1050, "pow (1000000)": 324, "pow (10000000)": 981,
+    "softmax (256x512)": 246, "softmax (1024x1024)": 307, "softmax (4096x2048)": 763,
+    "softmax (256x8192)": 458, "layer_norm (256x512)": 235, "layer_norm (1024x1024)": 277,
+    "layer_norm (4096x2048)": 611, "bmm attention (8h, seq=128, d=64)": 228,
+    "bmm attention (8h, seq=512, d=64)": 301, "bmm attention (16h, seq=256, d=128)": 292,
+    "sum (1000000)": 230, "sum (10000000)": 445, "sum axis=0 (1024x256)": 213,
+    "sum axis=0 (4096x256)": 231, "min (1000000)": 229, "min (10000000)": 455,
+    "max (1000000)": 229, "max (10000000)": 443, "argmax (1024x256)": 240,
+    "argmax (4096x256)": 333}
 
 
 def bench_graphs(timeout: float = 300.0) -> list[dict]:
@@ -330,15 +345,17 @@ def bench_graphs(timeout: float = 300.0) -> list[dict]:
     B4 S512 d768 H12 encoder block, the reference's single-head transformer
     and linear_sigmoid MLP benchmarks, and the 20-op affine chain at the API
     level, host <-> HBM copies of a 256 MiB array through its pinned host
-    mirror, and the reference's MNIST classifier and autoencoder benchmarks.
-    Each iteration is eval + synchronize, as the reference times it."""
+    mirror, the reference's MNIST classifier and autoencoder benchmarks and
+    its GPU micro-benchmarks at their shapes.  Each iteration is eval +
+    synchronize, as the reference times it."""
     import subprocess
 
     if not GRAPH_BENCH.exists():
         raise RuntimeError(f"{GRAPH_BENCH} is not built (run __graft_entry__.build())")
     out = []
     for argv in (["encoder", "10"], ["transformer"], ["mlp"], ["train"],
-                 ["chain", str(64 << 20), "20"], ["transfer", str(64 << 20), "10"], ["mnist"]):
+                 ["chain", str(64 << 20), "20"], ["transfer", str(64 << 20), "10"], ["mnist"],
+                 ["micro"]):
         log(f"bench_graph {' '.join(argv)}")
         proc = subprocess.run([str(GRAPH_BENCH), *argv], capture_output=True, text=True,
                               timeout=timeout)
@@ -657,6 +674,16 @@ def main():
                         "reference_m1pro_ms": ref,
                         "data": "synthetic images in [0,1) and labels, MNIST shapes "
                                 "(60000 train, 10000 test)"}
+                continue
+            elif w == "micro":
+                name = r["name"]
+                key = "micro_" + "".join(ch if ch.isalnum() else "_" for ch in name).strip("_")
+                while "__" in key:
+                    key = key.replace("__", "_")
+                secondary[key] = {"value": r["us"], "unit": "us", "higher_is_better": False,
+                                  "reference_m1pro_us": REF_MICRO_US.get(name),
+                                  "timing": "median of op + eval + synchronize iterations",
+                                  "reference_case": name}
                 continue
             elif w == "transfer":
                 secondary["host_transfer_256MiB"] = {

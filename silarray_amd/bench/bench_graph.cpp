@@ -36,6 +36,13 @@
 //                                             reference's SGEMM config,
 //                                             bench/micro/bench_sgemm.cpp:34);
 //                                             A, B and C written to DIR
+//   bench_graph micro                         the reference's GPU
+//                                             micro-benchmarks (bench/micro/
+//                                             bench_broadcast.cpp,
+//                                             bench_elementwise.cpp,
+//                                             bench_nn_ops.cpp,
+//                                             bench_reduction.cpp) at their
+//                                             shapes: one JSON line each
 //   bench_graph chain-dump n DIR              the 20-node chain of `chain` on
 //                                             n uniform[-1, 1) floats, one
 //                                             sil::eval; x and y written to
@@ -420,9 +427,114 @@ void write_raw(const std::string &path, const array<float> &a) {
 
 }  // namespace
 
+// The reference's GPU micro-benchmarks, same operations and shapes, each
+// iteration computing the result and waiting for it: element-wise add / mul /
+// div / pow on ones (bench_elementwise.cpp:29-41, 249-258), the (N, M) + (M)
+// bias broadcast (bench_broadcast.cpp:26-41), softmax and layer_norm of
+// random rows (bench_nn_ops.cpp:24-35, 80-93), batched products
+// (bench_nn_ops.cpp:252-270), full sum / min / max (bench_reduction.cpp:
+// 28-34, 210-220; the scalar result is the wait), sum(0) and argmax of
+// [m, 256] (bench_reduction.cpp:115-124, 290-300).
+void micro() {
+  auto report = [](const std::string &name, double ms) {
+    std::printf("{\"workload\": \"micro\", \"name\": \"%s\", \"us\": %.2f}\n", name.c_str(),
+                ms * 1e3);
+    std::fflush(stdout);
+  };
+  const int reps = 50;
+  for (auto [r, c] : {std::pair<size_t, size_t>{1024, 1024}, {4096, 512}, {4096, 4096}}) {
+    auto a = ones<float>({r, c});
+    auto b = ones<float>({c});
+    array<float> y;
+    report("broadcast (" + std::to_string(r) + "x" + std::to_string(c) + ")+(" +
+               std::to_string(c) + ")",
+           median_ms(reps, [&] {
+             y = a + b;
+             eval(y);
+             synchronize();
+           }));
+  }
+  for (size_t n : {size_t(1000000), size_t(10000000)}) {
+    auto a = ones<float>({n});
+    auto b = ones<float>({n});
+    array<float> y;
+    const std::string sz = " (" + std::to_string(n) + ")";
+    report("add" + sz, median_ms(reps, [&] { y = a + b; eval(y); synchronize(); }));
+    report("mul" + sz, median_ms(reps, [&] { y = a * b; eval(y); synchronize(); }));
+    report("div" + sz, median_ms(reps, [&] { y = a / b; eval(y); synchronize(); }));
+    report("pow" + sz, median_ms(reps, [&] { y = a.pow(b); eval(y); synchronize(); }));
+  }
+  for (auto [r, c] : {std::pair<size_t, size_t>{256, 512}, {1024, 1024}, {4096, 2048}, {256, 8192}}) {
+    auto x = random({r, c});
+    array<float> y;
+    report("softmax (" + std::to_string(r) + "x" + std::to_string(c) + ")",
+           median_ms(reps, [&] {
+             y = x.softmax();
+             eval(y);
+             synchronize();
+           }));
+  }
+  for (auto [r, c] : {std::pair<size_t, size_t>{256, 512}, {1024, 1024}, {4096, 2048}}) {
+    auto x = random({r, c});
+    auto gamma = ones<float>({c});
+    auto beta = zeros<float>({c});
+    array<float> y;
+    report("layer_norm (" + std::to_string(r) + "x" + std::to_string(c) + ")",
+           median_ms(reps, [&] {
+             y = x.layer_norm(gamma, beta);
+             eval(y);
+             synchronize();
+           }));
+  }
+  struct bm {
+    size_t h, m, n, k;
+  };
+  for (auto [h, m, n, k] : {bm{8, 128, 128, 64}, bm{8, 512, 512, 64}, bm{16, 256, 256, 128}}) {
+    auto a = random({h, m, k});
+    auto b = random({h, k, n});
+    array<float> y;
+    report("bmm attention (" + std::to_string(h) + "h, seq=" + std::to_string(m) +
+               ", d=" + std::to_string(k) + ")",
+           median_ms(reps, [&] {
+             y = a.batched_dot(b);
+             eval(y);
+             synchronize();
+           }));
+  }
+  volatile float sink = 0.0f;
+  for (size_t n : {size_t(1000000), size_t(10000000)}) {
+    auto a = random({n});
+    const std::string sz = " (" + std::to_string(n) + ")";
+    report("sum" + sz, median_ms(reps, [&] { sink = a.sum(); }));
+    report("min" + sz, median_ms(reps, [&] { sink = a.min(); }));
+    report("max" + sz, median_ms(reps, [&] { sink = a.max(); }));
+  }
+  for (size_t m : {size_t(1024), size_t(4096)}) {
+    auto a = random({m, size_t(256)});
+    array<float> s;
+    array<int> idx;
+    const std::string sz = " (" + std::to_string(m) + "x256)";
+    report("sum axis=0" + sz, median_ms(reps, [&] {
+             s = a.sum(0);
+             eval(s);
+             synchronize();
+           }));
+    report("argmax" + sz, median_ms(reps, [&] {
+             idx = a.argmax();
+             eval(idx);
+             synchronize();
+           }));
+  }
+  (void)sink;
+}
+
 int main(int argc, char **argv) {
   const std::string mode = argc > 1 ? argv[1] : "encoder";
   try {
+    if (mode == "micro") {
+      micro();
+      return 0;
+    }
     if (mode == "chain") {
       const size_t n = argc > 2 ? std::strtoull(argv[2], nullptr, 10) : (size_t(64) << 20);
       const int reps = argc > 3 ? std::atoi(argv[3]) : 20;

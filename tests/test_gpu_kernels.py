@@ -195,6 +195,123 @@ def test_program_general_graph(native, oracle):
     assert np.all(np.abs(out - ref) <= 4 * np.finfo(np.float32).eps * scale + 1e-30)
 
 
+# How the program kernel reads each input: contiguous (16-byte aligned or
+# not), a block repeated along the leading axes (period a multiple of 4 or
+# not, aligned or not), general strides, a scalar.  (shape, [(base offset in
+# elements, strides)], buffer lengths): out = (in0 * in1 + in2) - in0, which is
+# correctly rounded in fp32 on both sides.
+PROGRAM_MODE_CASES = [
+    ("contig aligned, ragged", (2048 * 3 + 5,), [(0, (1,)), (0, (1,)), (0, (1,))]),
+    ("contig unaligned", (4099,), [(1, (1,)), (3, (1,)), (0, (1,))]),
+    ("row period 512", (33, 512), [(0, (512, 1)), (0, (0, 1)), (0, (512, 1))]),
+    ("row period 129", (37, 129), [(0, (129, 1)), (0, (0, 1)), (1, (0, 1))]),
+    ("row period unaligned", (20, 64), [(0, (64, 1)), (1, (0, 1)), (0, (0, 0))]),
+    ("matrix period", (3, 17, 24), [(0, (408, 24, 1)), (0, (0, 24, 1)), (0, (0, 0, 1))]),
+    ("transposed", (31, 45), [(0, (1, 31)), (0, (45, 1)), (2, (0, 1))]),
+    ("column broadcast", (40, 36), [(0, (36, 1)), (0, (1, 0)), (0, (0, 0))]),
+]
+
+
+def _strided_view(buf_flat, base, strides, shape):
+    idx = np.zeros(shape, np.int64) + base
+    for d, st in enumerate(strides):
+        sh = [1] * len(shape)
+        sh[d] = shape[d]
+        idx = idx + (np.arange(shape[d]) * st).reshape(sh)
+    return buf_flat[idx]
+
+
+@pytest.mark.parametrize("name,shape,ins", PROGRAM_MODE_CASES, ids=[c[0] for c in PROGRAM_MODE_CASES])
+def test_program_input_modes(native, name, shape, ins):
+    announce(f"program input modes: {name} {shape}")
+    g = rng(720)
+    P = native
+    bufs, vals = [], []
+    for base, strides in ins:
+        span = base + 1 + sum((e - 1) * st for e, st in zip(shape, strides))
+        h = g.normal(0, 1, span + 3).astype(np.float32)
+        bufs.append((up(native, h), base, strides))
+        vals.append(_strided_view(h, base, strides, shape))
+    n = int(np.prod(shape))
+    do = empty(native, n)
+    instrs = [(P.PI_LOAD, 0, 0), (P.PI_LOAD, 1, 1), (P.PI_MUL, 2, 0, 1), (P.PI_LOAD, 3, 2),
+              (P.PI_ADD, 2, 2, 3), (P.PI_SUB, 2, 2, 0)]
+    prog = P.make_program(shape, [(b.ptr + 4 * base, st) for b, base, st in bufs], instrs,
+                          out_reg=2)
+    P.program_f32(prog, do)
+    a, b, c = vals
+    ref = ((a * b) + c) - a
+    assert np.array_equal(down(native, do, shape), ref.astype(np.float32))
+
+
+# A program that is one binary operation on two loaded inputs runs on the
+# binary kernels: (shape, (base, strides) of the left and right inputs,
+# register order of the loads).
+PROGRAM_BINARY_CASES = [
+    ((4096,), (0, (1,)), (0, (1,)), False),
+    ((4099,), (0, (1,)), (0, (1,)), True),
+    ((64, 64), (0, (64, 1)), (0, (0, 0)), False),
+    ((64, 64), (0, (0, 0)), (0, (64, 1)), True),
+    ((16, 256), (0, (256, 1)), (0, (0, 1)), False),
+    ((16, 256), (0, (0, 1)), (0, (256, 1)), False),
+    ((30, 129), (0, (129, 1)), (0, (0, 1)), False),
+    ((4096,), (1, (1,)), (0, (1,)), False),
+]
+
+
+@pytest.mark.parametrize("op", [ADD, SUB, MUL, DIV])
+@pytest.mark.parametrize("shape,lhs,rhs,swap", PROGRAM_BINARY_CASES)
+def test_program_single_binary_op(native, oracle, op, shape, lhs, rhs, swap):
+    announce(f"program binary op={op} {shape} {lhs} {rhs} swap={swap}")
+    g = rng(740 + op)
+    P = native
+    vals, ptrs = [], []
+    for base, strides in (lhs, rhs):
+        span = base + 1 + sum((e - 1) * st for e, st in zip(shape, strides))
+        h = g.uniform(0.25, 2, span + 3).astype(np.float32) * np.where(
+            g.random(span + 3) < 0.5, -1, 1).astype(np.float32)
+        buf = up(native, h)
+        ptrs.append((buf, base, strides))
+        vals.append(_strided_view(h, base, strides, shape))
+    n = int(np.prod(shape))
+    do = empty(native, n)
+    pi = {ADD: P.PI_ADD, SUB: P.PI_SUB, MUL: P.PI_MUL, DIV: P.PI_DIV}[op]
+    # registers: left in r3, right in r1; the loads in either order
+    loads = [(P.PI_LOAD, 3, 0), (P.PI_LOAD, 1, 1)]
+    if swap:
+        loads.reverse()
+    prog = P.make_program(shape, [(b.ptr + 4 * base, st) for b, base, st in ptrs],
+                          loads + [(pi, 5, 3, 1)], out_reg=5)
+    P.program_f32(prog, do)
+    a, b = (v.ravel() for v in vals)
+    assert np.array_equal(down(native, do, n), oracle.binary_mod_f32(op, a, b, n))
+
+
+def test_program_period_beyond_32bit_index(native):
+    """More than 2^32 output elements: the repeated-block offset takes 64-bit
+    arithmetic.  out[r, c] = row[c] * 2 + s over a [4294980, 1000] output
+    (16 GiB), checked on slices at both ends and across element 2^32."""
+    announce("program over 2^32 elements")
+    P = native
+    rows = (1 << 32) // 1000 + 13
+    n = rows * 1000
+    row = rng(730).normal(0, 1, 1000).astype(np.float32)
+    drow, ds = up(native, row), up(native, np.array([0.25], np.float32))
+    out = native.DeviceBuffer(4 * n)
+    try:
+        instrs = [(P.PI_LOAD, 0, 0), (P.PI_MULI, 0, 0, 0, 2.0), (P.PI_LOAD, 1, 1),
+                  (P.PI_ADD, 0, 0, 1)]
+        prog = P.make_program((rows, 1000), [(drow, (0, 1)), (ds, (0, 0))], instrs)
+        P.program_f32(prog, out)
+        expect = np.tile(row * np.float32(2.0) + np.float32(0.25), 3)
+        for start in (0, (1 << 32) // 1000 * 1000 - 1000, n - 3000):
+            got = out.download(3000, offset_bytes=4 * start)
+            assert np.array_equal(got, expect), start
+    finally:
+        out.free()
+        native.call("silgpu_pool_trim")
+
+
 # ---- reductions ------------------------------------------------------------------
 
 @pytest.mark.parametrize("n,offset", [(1, 0), (7, 0), (1000, 1), (65536, 0), (1 << 22, 3),

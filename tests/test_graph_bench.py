@@ -194,3 +194,17 @@ def test_mnist_reports_json():
         assert rec[k] > 0, k
     first, last = rec["classifier_mse_first_batch"]
     assert np.isfinite(first) and np.isfinite(last) and last < first
+
+
+@pytest.mark.gpu
+def test_micro_reports_every_reference_case():
+    """`bench_graph micro` times the reference's GPU micro-benchmarks: one
+    JSON line per case, named as bench.py's table of published figures."""
+    print("bench_graph micro", flush=True)
+    import bench
+
+    out = subprocess.run([str(_bench()), "micro"], capture_output=True, text=True, timeout=240,
+                         check=True).stdout
+    recs = [json.loads(l) for l in out.splitlines() if l.startswith("{")]
+    assert all(r["workload"] == "micro" and r["us"] > 0 for r in recs)
+    assert sorted(r["name"] for r in recs) == sorted(bench.REF_MICRO_US)
