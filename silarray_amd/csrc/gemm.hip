@@ -690,6 +690,9 @@ __global__ __launch_bounds__(kSkWaves *kWave) void sgemm_skinny_k(gemm_args p) {
 // K allows (four 16-deep stages measured slower for them: 2048^3 123.9
 // against 126.2 TFLOP/s with 128 x 64 tiles).
 constexpr int kDtlBK = 16;  // K granularity of the path (BK = 16 or 32)
+// Leading dimensions below 2^26 floats keep a window lane's 32-bit byte
+// offset (at most 15 rows of the operand) in range.
+constexpr int64_t kDtlMaxLd = int64_t(1) << 26;
 
 // Pitch (floats) of an M/N-contiguous window for a tile extent X: one k row
 // per window for 256, two for 128, four for 64 (the rows of one window at
@@ -725,10 +728,30 @@ struct dtl_cfg {
   static_assert(kLdsBytes <= 160 * 1024, "LDS");
 };
 
+// One 16-byte LDS-direct load per lane (global_load_lds_dwordx4): the
+// data goes from memory straight into LDS at lds_dst + 16 * lane.
 __device__ __forceinline__ void dtl16(const float *src, float *lds_dst) {
   __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
                                    (__attribute__((address_space(3))) void *)lds_dst, 16, 0, 0);
 }
+
+// The same load in its SGPR-base form: address = sbase (uniform, SGPRs) +
+// voff (32-bit, per lane).  The compiler only emits the 64-bit VGPR-address
+// form for the builtin, which costs one vector add per load and K tile; this
+// form advances the K tile with scalar adds alone (8192^3: 144.1 -> 147.2
+// TFLOP/s, MI355X).  M0 holds the LDS destination; one wait state separates
+// its write from the load.  M0 is otherwise unused by this kernel (gfx9 LDS
+// instructions do not read it), so clobbering it here is safe.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dtl16_s(const float *sbase, uint32_t voff, float *lds_dst) {
+  const uint32_t m0v = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) float *)lds_dst));
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0v),
+               "v"(voff), "s"(sbase)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
 
 // Source of lane `lane` for window w of an operand tile of extent X starting
 // at x0 (rows x0.. of a [rows][K] operand when KCONTIG, else columns x0.. of
@@ -746,6 +769,31 @@ __device__ __forceinline__ const float *dtl_src(const float *base, int64_t ld, i
     return base + int64_t(2 * w + lane / 32) * ld + x0 + 4 * (lane % 32);
   } else {
     return base + int64_t(4 * w + lane / 16) * ld + x0 + 4 * (lane % 16);
+  }
+}
+// The same source split into a part uniform over the wave (`uni`, elements
+// from the operand base: window w depends only on the wave) and a lane part
+// (`lane_bytes`, 32-bit), for the SGPR-base form of the load (dtl16_s):
+// advancing the K tile then costs scalar adds only, and no vector
+// instruction competes with the MFMAs for issue.  The host keeps
+// 16 * ld * 4 bytes below 2^32.
+template <bool KCONTIG, int X>
+__device__ __forceinline__ void dtl_src_split(int64_t ld, int x0, int w, int lane, int64_t &uni,
+                                              uint32_t &lane_bytes) {
+  if constexpr (KCONTIG) {
+    const int rr = lane / 4, kq = (lane % 4) ^ ((rr / 2) & 3);
+    const int rg = w % (X / 16), kh = w / (X / 16);
+    uni = int64_t(x0 + 16 * rg) * ld + 16 * kh;
+    lane_bytes = (uint32_t(rr) * uint32_t(ld) + 4u * uint32_t(kq)) * 4u;
+  } else if constexpr (X == 256) {
+    uni = int64_t(w) * ld + x0;
+    lane_bytes = 16u * uint32_t(lane);
+  } else if constexpr (X == 128) {
+    uni = int64_t(2 * w) * ld + x0;
+    lane_bytes = (uint32_t(lane / 32) * uint32_t(ld) + 4u * uint32_t(lane % 32)) * 4u;
+  } else {
+    uni = int64_t(4 * w) * ld + x0;
+    lane_bytes = (uint32_t(lane / 16) * uint32_t(ld) + 4u * uint32_t(lane % 16)) * 4u;
   }
 }
 template <bool KCONTIG, int X>
@@ -796,7 +844,11 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU,
   __shared__ __attribute__((aligned(16))) float lds1[D::kStage];
   __shared__ __attribute__((aligned(16))) float lds2[NS > 2 ? D::kStage : 4];
   __shared__ __attribute__((aligned(16))) float lds3[NS > 3 ? D::kStage : 4];
-  const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+  // The wave index through readfirstlane: the compiler then keeps it, and
+  // every window and LDS address derived from it, in SGPRs.
+  // (Not for the convolution: its gathers measured 1.5-2% slower so.)
+  const int t = threadIdx.x, lane = t % kWave;
+  const int wave = CONV ? t / kWave : __builtin_amdgcn_readfirstlane(t / kWave);
   const int wm = wave / D::WN, wn = wave % D::WN;
   int tm, tn;
   tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
@@ -810,12 +862,23 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU,
   const int kend = min(p.K, kbeg + p.klen);
   const int KT = kend > kbeg ? (kend - kbeg) / BK : 0;  // K % BK == 0 on this path
   // This wave loads windows wave + q*NW (q < WPA, WPB) of each operand.
-  const float *a_src[WPA], *b_src[WPB];
+  int64_t a_uni[WPA], b_uni[WPB];
+  uint32_t a_lane[WPA], b_lane[WPB];
 #pragma unroll
-  for (int q = 0; q < WPA; ++q)
-    a_src[q] = CONV ? A : dtl_src<AK, BM>(A, p.lda, m0, wave + q * NW, lane);
+  for (int q = 0; q < WPA; ++q) {
+    if constexpr (CONV) {
+      a_uni[q] = 0;
+      a_lane[q] = 0;
+    } else {
+      dtl_src_split<AK, BM>(p.lda, m0, wave + q * NW, lane, a_uni[q], a_lane[q]);
+    }
+  }
+  const float *b_src[WPB];  // the convolution's B: per-lane pointers
 #pragma unroll
-  for (int q = 0; q < WPB; ++q) b_src[q] = dtl_src<BKc, BN>(B, p.ldb, n0, wave + q * NW, lane);
+  for (int q = 0; q < WPB; ++q) {
+    dtl_src_split<BKc, BN>(p.ldb, n0, wave + q * NW, lane, b_uni[q], b_lane[q]);
+    b_src[q] = CONV ? dtl_src<BKc, BN>(B, p.ldb, n0, wave + q * NW, lane) : nullptr;
+  }
   // Advance of one K tile for each operand.
   const int64_t a_step = AK ? BK : int64_t(BK) * p.lda;
   const int64_t b_step = BKc ? BK : int64_t(BK) * p.ldb;
@@ -870,11 +933,16 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU,
     } else {
 #pragma unroll
       for (int q = 0; q < WPA; ++q)
-        dtl16(a_src[q] + k * a_step, S + dtl_window<AK, BM>(wave + q * NW));
+        dtl16_s(A + a_uni[q] + k * a_step, a_lane[q], S + dtl_window<AK, BM>(wave + q * NW));
     }
 #pragma unroll
-    for (int q = 0; q < WPB; ++q)
-      dtl16(b_src[q] + k * b_step, S + kBOff + dtl_window<BKc, BN>(wave + q * NW));
+    for (int q = 0; q < WPB; ++q) {
+      if constexpr (CONV)
+        dtl16(b_src[q] + k * b_step, S + kBOff + dtl_window<BKc, BN>(wave + q * NW));
+      else
+        dtl16_s(B + b_uni[q] + k * b_step, b_lane[q],
+                S + kBOff + dtl_window<BKc, BN>(wave + q * NW));
+    }
   };
   typename F::acc_t acc[TM][TN];
 #pragma unroll
@@ -1324,7 +1392,8 @@ int launch_tb(const gemm_args &a, int64_t batch, int splits, bool vec, hipStream
   // Full tiles of 16-byte aligned operands: LDS-direct loads.
   if constexpr ((BM == 256 && BN == 256) || (BM == 128 && BN == 128) ||
                 (BM == 128 && BN == 64)) {
-    if (vec && a.M % BM == 0 && a.N % BN == 0 && a.K % kDtlBK == 0) {
+    if (vec && a.M % BM == 0 && a.N % BN == 0 && a.K % kDtlBK == 0 && a.lda < kDtlMaxLd &&
+        a.ldb < kDtlMaxLd) {
       if constexpr (BM == 256) {
         // The 256 x 256 plan runs as 256 x 128 tiles of 4 waves with three
         // 16-deep stages (75 KB of LDS), two workgroups per CU: each waits
@@ -1944,7 +2013,8 @@ int gemm_impl(const silgpu_gemm_desc &d, const plan *forced, bool noalloc = fals
                    (ta ? M % 4 == 0 : K % 4 == 0) && (tb ? K % 4 == 0 : N % 4 == 0) &&
                    (batch == 1 || (d.stride_a_inner % 4 == 0 && d.stride_b_inner % 4 == 0 &&
                                    d.stride_a_outer % 4 == 0 && d.stride_b_outer % 4 == 0));
-  return run_sgemm(a, batch, forced ? *forced : choose_plan(M, N, K, batch, vec && K % 16 == 0),
+  const bool dtl_ok = vec && K % 16 == 0 && d.lda < kDtlMaxLd && d.ldb < kDtlMaxLd;
+  return run_sgemm(a, batch, forced ? *forced : choose_plan(M, N, K, batch, dtl_ok),
                    ta, tb, vec, c, ss);
 }
 
