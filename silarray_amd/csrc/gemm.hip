@@ -495,6 +495,10 @@ struct vecf<4> {
   }
 };
 
+__device__ __forceinline__ const float *lane_at(const float *base, uint32_t lane_bytes) {
+  return reinterpret_cast<const float *>(reinterpret_cast<const char *>(base) + lane_bytes);
+}
+
 template <int Q, bool TB, bool VA, bool VB>
 struct skinny_chunk {
   float a[8];
@@ -503,10 +507,53 @@ struct skinny_chunk {
   // Loads chunk k0 (k0 + 16 <= kend unless MASK).  arow: A row of this lane
   // (clamped); bcol: first B column of this lane (clamped so the Q columns
   // are in range).
+  //
+  // The unmasked loads address memory as (wave-uniform base) + (32-bit lane
+  // byte offset): a_lane = (arow lda + 8 s) 4 and b_lane[q] =
+  // ((bcol + q) ldb + 8 s) 4 (TB) or (8 s ldb + bcol) 4, so each load's base
+  // is scalar arithmetic and the loads take the SGPR-base form, with no
+  // 64-bit vector address math per load.
   template <bool MASK>
   __device__ __forceinline__ void load(const float *__restrict__ A, int64_t lda,
                                        const float *__restrict__ B, int64_t ldb, int arow,
-                                       int bcol, int k0, int s, int kend) {
+                                       int bcol, int k0, int s, int kend, uint32_t a_lane,
+                                       const uint32_t (&b_lane)[Q]) {
+    if constexpr (!MASK) {
+      const float *ap = lane_at(A + k0, a_lane);
+      if constexpr (VA) {
+        const float4 x0 = *reinterpret_cast<const float4 *>(ap);
+        const float4 x1 = *reinterpret_cast<const float4 *>(ap + 4);
+        a[0] = x0.x; a[1] = x0.y; a[2] = x0.z; a[3] = x0.w;
+        a[4] = x1.x; a[5] = x1.y; a[6] = x1.z; a[7] = x1.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a[j] = ap[j];
+      }
+      if constexpr (!TB) {
+        typedef typename vecf<Q>::t V;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const V v = *reinterpret_cast<const V *>(lane_at(B + int64_t(k0 + j) * ldb, b_lane[0]));
+#pragma unroll
+          for (int q = 0; q < Q; ++q) b[q][j] = vecf<Q>::get(v, q);
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+          const float *bp = lane_at(B + k0, b_lane[q]);
+          if constexpr (VB) {
+            const float4 x0 = *reinterpret_cast<const float4 *>(bp);
+            const float4 x1 = *reinterpret_cast<const float4 *>(bp + 4);
+            b[q][0] = x0.x; b[q][1] = x0.y; b[q][2] = x0.z; b[q][3] = x0.w;
+            b[q][4] = x1.x; b[q][5] = x1.y; b[q][6] = x1.z; b[q][7] = x1.w;
+          } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) b[q][j] = bp[j];
+          }
+        }
+      }
+      return;
+    }
     const int kb = k0 + 8 * s;
     const float *ap = A + int64_t(arow) * lda;
     if constexpr (VA && !MASK) {
@@ -568,7 +615,8 @@ __global__ __launch_bounds__(kSkWaves *kWave) void sgemm_skinny_k(gemm_args p) {
   constexpr int STRIDE = kSkChunk * kSkWaves;
   static_assert(16 % kSkWaves == 0 && kSkWaves * Q * 16 * kWave * 4 <= 65536, "LDS");
   __shared__ float red[kSkWaves][Q * 16][kWave];
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int c = lane % 32, s = lane / 32;
   const int M = p.M, N = p.N, K = p.K;
   const int n0 = blockIdx.x * (32 * Q);
@@ -577,6 +625,12 @@ __global__ __launch_bounds__(kSkWaves *kWave) void sgemm_skinny_k(gemm_args p) {
   if (bcol + Q > N) bcol = 0;  // whole vector out of range (N % Q == 0 when Q > 1)
   const int kbeg = blockIdx.y * p.klen;
   const int kend = min(K, kbeg + p.klen);
+  const uint32_t a_lane = (uint32_t(arow) * uint32_t(p.lda) + 8u * uint32_t(s)) * 4u;
+  uint32_t b_lane[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+    b_lane[q] = TB ? (uint32_t(bcol + q) * uint32_t(p.ldb) + 8u * uint32_t(s)) * 4u
+                   : (8u * uint32_t(s) * uint32_t(p.ldb) + uint32_t(bcol)) * 4u;
 
   floatx16 acc[Q];
 #pragma unroll
@@ -592,7 +646,8 @@ __global__ __launch_bounds__(kSkWaves *kWave) void sgemm_skinny_k(gemm_args p) {
 #pragma unroll
   for (int u = 0; u < U; ++u)
     if (u < nf)
-      ch[u].template load<false>(p.A, p.lda, p.B, p.ldb, arow, bcol, k0 + u * STRIDE, s, kend);
+      ch[u].template load<false>(p.A, p.lda, p.B, p.ldb, arow, bcol, k0 + u * STRIDE, s, kend,
+                                 a_lane, b_lane);
   int i = 0;
   for (; i + U <= nf; i += U) {
 #pragma unroll
@@ -600,7 +655,7 @@ __global__ __launch_bounds__(kSkWaves *kWave) void sgemm_skinny_k(gemm_args p) {
       ch[u].mma(acc);
       if (i + u + U < nf)
         ch[u].template load<false>(p.A, p.lda, p.B, p.ldb, arow, bcol,
-                                   k0 + (i + u + U) * STRIDE, s, kend);
+                                   k0 + (i + u + U) * STRIDE, s, kend, a_lane, b_lane);
     }
   }
 #pragma unroll
@@ -609,7 +664,7 @@ __global__ __launch_bounds__(kSkWaves *kWave) void sgemm_skinny_k(gemm_args p) {
   const int kt = k0 + nf * STRIDE;  // a partial last chunk, if any
   if (kt < kend) {
     skinny_chunk<Q, TB, VA, VB> t;
-    t.template load<true>(p.A, p.lda, p.B, p.ldb, arow, bcol, kt, s, kend);
+    t.template load<true>(p.A, p.lda, p.B, p.ldb, arow, bcol, kt, s, kend, a_lane, b_lane);
     t.mma(acc);
   }
 
@@ -1721,7 +1776,11 @@ int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, boo
     return run_sgemm(t, 1, plan{pl.tile, pl.tail_splits}, ta, tb, tvec, c, ss);
   }
   gemm_args a = a0;
-  const bool skinny = pl.tile >= TILE_SKINNY && a.M <= 32 && batch == 1 && !ta;
+  // The small-M kernel's per-lane byte offsets are 32-bit.
+  const int64_t kLane = int64_t(1) << 30;
+  const bool lane32 = int64_t(a.M) * a.lda + 8 < kLane &&
+                      (tb ? (int64_t(a.N) + 4) * a.ldb + 8 : 8 * a.ldb + a.N) < kLane;
+  const bool skinny = pl.tile >= TILE_SKINNY && a.M <= 32 && batch == 1 && !ta && lane32;
   if (pl.tile >= TILE_SKINNY && !skinny)
     pl = pl.splits >= 1 ? plan{TILE_32x128, pl.splits} : small_m_tiles(a.M, a.N, a.K, batch);
   int splits = pl.splits;
