@@ -1209,7 +1209,11 @@ __global__ __launch_bounds__(kGemvPartBlock) void gemv_part_k(const float *__res
                                                               int64_t kc,
                                                               float *__restrict__ partial) {
   __shared__ float4 red[kGemvPartWaves][kWave];
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  // The wave index through readfirstlane: the row a wave reads is then
+  // scalar, x[k] a scalar load, and each B load a uniform row base plus the
+  // lane's 16-byte column offset.
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int64_t c0 = int64_t(blockIdx.x) * kGemvCols;
   const int64_t k0 = int64_t(blockIdx.y) * kc;
   const int64_t k1 = k0 + kc < K ? k0 + kc : K;
@@ -1218,6 +1222,8 @@ __global__ __launch_bounds__(kGemvPartBlock) void gemv_part_k(const float *__res
     const int64_t col = c0 + lane * 4;
     if (col < N) {
       const float *bp = Bm + col;
+      const float *bt = Bm + c0;  // the tile's first column, uniform
+      const uint32_t lane_bytes = 16u * uint32_t(lane);
       int64_t k = k0 + wave;
       constexpr int U = kGemvUnroll, W = kGemvPartWaves;
       for (; k + (U - 1) * W < k1; k += U * W) {
@@ -1225,7 +1231,7 @@ __global__ __launch_bounds__(kGemvPartBlock) void gemv_part_k(const float *__res
         float xv[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          v[u] = load_nt4(bp + (k + u * W) * ldb);
+          v[u] = load_nt4(lane_at(bt + (k + u * W) * ldb, lane_bytes));
           xv[u] = x[k + u * W];
         }
 #pragma unroll
