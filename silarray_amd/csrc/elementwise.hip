@@ -11,6 +11,7 @@
 
 #include "internal.h"
 
+
 namespace silgpu {
 namespace {
 
@@ -511,36 +512,52 @@ struct chain_launch {
   float offset[SILGPU_PROG_MAX_INSTRS];
 };
 
-constexpr int kChainVec = 1;  // float4s per thread per grid-stride step
+// float4s per thread per grid-stride step: on 64M floats (20 steps) 4 moved
+// 6.00 TB/s, 1 (one grid-stride vector) 5.93, 8 5.73.
+constexpr int kChainVec = 4;
 
+// Applies the chain to four floats.
+__device__ __forceinline__ float4 chain4(const chain_launch &L, float4 v) {
+  for (int s = 0; s < L.n_steps; ++s) {
+    const float a = L.scale[s], b = L.offset[s];
+    v.x = fmaf(v.x, a, b);
+    v.y = fmaf(v.y, a, b);
+    v.z = fmaf(v.z, a, b);
+    v.w = fmaf(v.w, a, b);
+  }
+  return v;
+}
+
+// A workgroup moves one contiguous block of kBlock * kChainVec float4s per
+// step, each thread kChainVec of them strided by the workgroup width, all
+// loads issued before the first store.  Whole blocks carry no per-slot
+// checks (with them the compiler makes the first store wait for every load).
 template <bool NT>
 __global__ __launch_bounds__(kBlock) void affine_chain_k(chain_launch L,
                                                          float4 *__restrict__ out,
                                                          int64_t n4) {
   const float4 *in = reinterpret_cast<const float4 *>(L.in);
-  int64_t stride = int64_t(gridDim.x) * kBlock * kChainVec;
-  for (int64_t base = int64_t(blockIdx.x) * kBlock * kChainVec + threadIdx.x; base < n4;
-       base += stride) {
+  constexpr int64_t kSpan = int64_t(kBlock) * kChainVec;
+  const int64_t stride = int64_t(gridDim.x) * kSpan;
+  for (int64_t b0 = int64_t(blockIdx.x) * kSpan; b0 < n4; b0 += stride) {
+    const int64_t base = b0 + threadIdx.x;
     float4 v[kChainVec];
+    if (b0 + kSpan <= n4) {
 #pragma unroll
-    for (int u = 0; u < kChainVec; ++u) {
-      int64_t i = base + int64_t(u) * kBlock;
-      v[u] = i < n4 ? ld4<NT>(in + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    for (int s = 0; s < L.n_steps; ++s) {
-      float a = L.scale[s], b = L.offset[s];
+      for (int u = 0; u < kChainVec; ++u) v[u] = ld4<NT>(in + base + u * kBlock);
+#pragma unroll
+      for (int u = 0; u < kChainVec; ++u) st4<NT>(out + base + u * kBlock, chain4(L, v[u]));
+    } else {
 #pragma unroll
       for (int u = 0; u < kChainVec; ++u) {
-        v[u].x = fmaf(v[u].x, a, b);
-        v[u].y = fmaf(v[u].y, a, b);
-        v[u].z = fmaf(v[u].z, a, b);
-        v[u].w = fmaf(v[u].w, a, b);
+        const int64_t i = base + int64_t(u) * kBlock;
+        v[u] = i < n4 ? ld4<NT>(in + i) : make_float4(0.f, 0.f, 0.f, 0.f);
       }
-    }
 #pragma unroll
-    for (int u = 0; u < kChainVec; ++u) {
-      int64_t i = base + int64_t(u) * kBlock;
-      if (i < n4) st4<NT>(out + i, v[u]);
+      for (int u = 0; u < kChainVec; ++u) {
+        const int64_t i = base + int64_t(u) * kBlock;
+        if (i < n4) st4<NT>(out + i, chain4(L, v[u]));
+      }
     }
   }
 }
