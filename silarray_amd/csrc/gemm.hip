@@ -1173,7 +1173,7 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU,
 //
 // HBM-bound: B (K*N floats) is read once.  Pass 1: workgroup (ct, ks) covers
 // 256 columns (one float4 per lane) and rows [ks*kc, (ks+1)*kc); its eight
-// wavefronts take interleaved rows with four 16-byte non-temporal loads in
+// wavefronts take interleaved rows with eight 16-byte non-temporal loads in
 // flight per lane, add their results in LDS and write one partial row
 // partial[ks][ct*256 ..] to scratch.  The K split gives ~1024 workgroups to
 // fill the GPU.  Pass 2 adds the partials per column.  Finishing inside
@@ -1187,7 +1187,7 @@ constexpr int kGemvWaves = kGemvBlock / kWave;
 constexpr int kGemvPartWaves = 8;  // partial kernel: 8 waves x 4 loads in flight
 constexpr int kGemvPartBlock = kGemvPartWaves * kWave;
 constexpr int kGemvCols = 256;  // columns per workgroup (64 lanes x float4)
-constexpr int kGemvUnroll = 4;
+constexpr int kGemvUnroll = 8;  // rows in flight per lane: every wave issues its 8 rows at once
 constexpr int kGemvFinishLoads = 16;  // partial rows in flight per lane in pass 2
 
 __device__ __forceinline__ float4 load_nt4(const float *p) {
