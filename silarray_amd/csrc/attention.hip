@@ -293,13 +293,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
 template <int D>
 int launch_attention(const attn_args &a, int64_t batch, hipStream_t s) {
   using C = attn_cfg<D>;
-  static bool attr_done = false;
-  if (!attr_done) {
-    SILGPU_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(attention_k<D>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         C::kLdsBytes));
-    attr_done = true;
-  }
+  // Once per process (a thread-safe static), before the first launch.
+  static const hipError_t attr_rc =
+      hipFuncSetAttribute(reinterpret_cast<const void *>(attention_k<D>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
+  SILGPU_HIP_CHECK(attr_rc);
   dim3 grid(static_cast<unsigned>(cdiv(a.Sq, kBQ)), static_cast<unsigned>(batch));
   attention_k<D><<<grid, kAttnThreads, C::kLdsBytes, s>>>(a);
   SILGPU_LAUNCH_CHECK("attention_k");

@@ -97,13 +97,12 @@ int launch_direct(const float *in, const float *w, float *out, int M, int H, int
   const int64_t halo = int64_t(pad) * (int64_t(W) + 1);
   const size_t staged = wbytes + size_t(kDirThreads + 2 * halo) * cin * sizeof(float);
   if (staged <= kDirStagedLds) {
-    static bool attr_done = false;
-    if (!attr_done) {
-      SILGPU_HIP_CHECK(hipFuncSetAttribute(
-          reinterpret_cast<const void *>(conv_direct_k<VEC, true>),
-          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kDirStagedLds)));
-      attr_done = true;
-    }
+    // Once per process (a thread-safe static), before the first launch.
+    static const hipError_t attr_rc =
+        hipFuncSetAttribute(reinterpret_cast<const void *>(conv_direct_k<VEC, true>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(kDirStagedLds));
+    SILGPU_HIP_CHECK(attr_rc);
     conv_direct_k<VEC, true><<<grid, kDirThreads, staged, s>>>(in, w, out, M, H, W, cin, K, pad,
                                                                Co, Kd, static_cast<int>(halo));
   } else {

@@ -1408,13 +1408,11 @@ template <int BM, int BN, int BK, int WM, int WN, int MI, bool TA, bool TB, bool
 int launch_cfg(const gemm_args &a, int64_t batch, int splits, hipStream_t s) {
   using C = cfg<BM, BN, BK, WM, WN, MI>;
   auto kern = sgemm_mfma_k<BM, BN, BK, WM, WN, MI, TA, TB, VEC, EDGE>;
-  static bool attr_done = false;
-  if (!attr_done) {
-    SILGPU_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         C::kLdsBytes));
-    attr_done = true;
-  }
+  // Once per process (a thread-safe static), before the first launch.
+  static const hipError_t attr_rc =
+      hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
+  SILGPU_HIP_CHECK(attr_rc);
   gemm_args g = a;
   g.tiles_m = static_cast<int>(cdiv(a.M, BM));
   g.tiles_n = static_cast<int>(cdiv(a.N, BN));
@@ -1886,13 +1884,11 @@ template <int BM, int BN, int WM, int WN, bool VEC>
 int launch_conv_cfg(const gemm_args &a, hipStream_t s) {
   using C = cfg<BM, BN, 16, WM, WN, 16>;
   auto kern = sgemm_mfma_k<BM, BN, 16, WM, WN, 16, false, true, VEC, true, true>;
-  static bool attr_done = false;
-  if (!attr_done) {
-    SILGPU_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         C::kLdsBytes));
-    attr_done = true;
-  }
+  // Once per process (a thread-safe static), before the first launch.
+  static const hipError_t attr_rc =
+      hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
+  SILGPU_HIP_CHECK(attr_rc);
   gemm_args g = a;
   g.tiles_m = static_cast<int>(cdiv(a.M, BM));
   g.tiles_n = static_cast<int>(cdiv(a.N, BN));
