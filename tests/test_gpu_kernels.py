@@ -1038,3 +1038,55 @@ def test_conv2d_empty_reduction_writes_zeros(native):
     do = up(native, np.full(2 * 3 * 3 * 4, np.nan, np.float32))
     native.conv2d(None, None, do, 2, 3, 3, 0, 3, 4)
     assert np.all(down(native, do, 72) == 0)
+
+
+def _random_gemm_cases(n=60, seed=2026):
+    """Seeded shapes across every route: the LDS-direct tiles (M, N multiples
+    of 64/128/256, K a multiple of 16), the register-staged tiles (any
+    shape), small-M products, GEMV; random transposes, leading dimensions
+    padded by 0-7 floats, operands offset by 0-3 floats (so some lose 16-byte
+    alignment), and batches of 1-3."""
+    g = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        kind = i % 4
+        if kind == 0:    # LDS-direct eligible
+            M = int(g.choice([128, 256, 384, 512, 768, 1024]))
+            N = int(g.choice([64, 128, 256, 384, 512]))
+            K = int(16 * g.integers(1, 64))
+        elif kind == 1:  # ragged
+            M, N, K = (int(x) for x in g.integers(1, 700, 3))
+        elif kind == 2:  # small M
+            M, N, K = int(g.integers(1, 33)), int(g.integers(64, 2048)), int(g.integers(64, 3000))
+        else:            # products near GEMV
+            M, N, K = int(g.choice([1, 2])), int(g.integers(1, 4096)), int(g.integers(1, 4096))
+        ta, tb = bool(g.integers(0, 2)), bool(g.integers(0, 2))
+        pad_a, pad_b = int(g.integers(0, 8)), int(g.integers(0, 8))
+        off_a, off_b = int(g.choice([0, 0, 1, 3])), int(g.choice([0, 0, 2]))
+        batch = int(g.choice([1, 1, 2, 3]))
+        cases.append((M, N, K, ta, tb, pad_a, pad_b, off_a, off_b, batch))
+    return cases
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb,pad_a,pad_b,off_a,off_b,batch", _random_gemm_cases())
+def test_sgemm_random_shapes(native, oracle, M, N, K, ta, tb, pad_a, pad_b, off_a, off_b, batch):
+    announce(f"sgemm random {M}x{N}x{K} ta={ta} tb={tb} pads={pad_a},{pad_b} "
+             f"offs={off_a},{off_b} batch={batch}")
+    g = rng(M * 7 + N * 3 + K + batch)
+    ra, ca = (K, M) if ta else (M, K)
+    rb, cb = (N, K) if tb else (K, N)
+    lda, ldb = ca + pad_a, cb + pad_b
+    sA, sB = ra * lda, rb * ldb
+    A = g.uniform(-1, 1, off_a + batch * sA).astype(np.float32)
+    B = g.uniform(-1, 1, off_b + batch * sB).astype(np.float32)
+    dA, dB, dC = up(native, A), up(native, B), empty(native, batch * M * N)
+    native.sgemm(ta, tb, M, N, K, dA.ptr + 4 * off_a, lda, sA, dB.ptr + 4 * off_b, ldb, sB, dC, N,
+                 M * N, batch)
+    Cg = down(native, dC, (batch, M, N))
+    for b in range(batch):
+        Ab = A[off_a + b * sA: off_a + (b + 1) * sA].reshape(ra, lda)[:, :ca]
+        Bb = B[off_b + b * sB: off_b + (b + 1) * sB].reshape(rb, ldb)[:, :cb]
+        C64, Cabs = oracle.sgemm_f64(np.ascontiguousarray(Ab), np.ascontiguousarray(Bb), ta=ta,
+                                     tb=tb, with_abs=True)
+        ok, nw, el = gemm_tolerance_ok(Cg[b], C64, Cabs, K)
+        assert ok, (b, nw, el)
