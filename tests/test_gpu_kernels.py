@@ -1090,3 +1090,100 @@ def test_sgemm_random_shapes(native, oracle, M, N, K, ta, tb, pad_a, pad_b, off_
                                      tb=tb, with_abs=True)
         ok, nw, el = gemm_tolerance_ok(Cg[b], C64, Cabs, K)
         assert ok, (b, nw, el)
+
+
+def _random_programs(n=40, seed=77):
+    """Seeded elementwise programs: 2-D or 3-D outputs, 1-4 inputs, each read
+    contiguous, as a scalar, as a repeated row or matrix block, as a column
+    broadcast or transposed, and 3-10 instructions of the correctly rounded
+    ops (so the result is bit-exact against numpy float32)."""
+    g = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        nd = int(g.integers(2, 4))
+        shape = tuple(int(x) for x in g.integers(1, 70, nd))
+        if g.random() < 0.3:
+            shape = shape[:-1] + (int(g.choice([64, 128, 512])),)
+        ins = []
+        for _k in range(int(g.integers(1, 5))):
+            kind = g.choice(["contig", "scalar", "row", "col", "trans"])
+            ins.append((str(kind), int(g.choice([0, 0, 1, 2]))))
+        prog = []
+        regs = []  # registers holding a value
+        for k in range(len(ins)):
+            prog.append(("load", k, k))
+            regs.append(k)
+        for _i in range(int(g.integers(1, 7))):
+            op = str(g.choice(["add", "sub", "mul", "div", "addi", "muli", "rsubi", "rdivi", "relu"]))
+            a, b = int(g.choice(regs)), int(g.choice(regs))
+            dst = int(g.integers(0, 8))
+            prog.append((op, dst, a, b, float(np.float32(g.uniform(0.5, 2.0)))))
+            if dst not in regs:
+                regs.append(dst)
+        out = prog[-1][1]
+        cases.append((shape, ins, prog, out))
+    return cases
+
+
+def _input_view(kind, shape, g):
+    """(host buffer, strides, numpy view of the output shape) for one input."""
+    nd = len(shape)
+    if kind == "scalar":
+        h = g.uniform(0.5, 2, 4).astype(np.float32)
+        return h, (0,) * nd, lambda base: np.broadcast_to(h[base], shape)
+    if kind == "row":   # the last axis repeated over the leading ones
+        L = shape[-1]
+        h = g.uniform(0.5, 2, L + 4).astype(np.float32)
+        return h, (0,) * (nd - 1) + (1,), lambda base: np.broadcast_to(h[base:base + L], shape)
+    if kind == "col":   # the first axis, broadcast along the others
+        L = shape[0]
+        h = g.uniform(0.5, 2, L + 4).astype(np.float32)
+        return h, (1,) + (0,) * (nd - 1), lambda base: np.broadcast_to(
+            h[base:base + L].reshape((L,) + (1,) * (nd - 1)), shape)
+    n = int(np.prod(shape))
+    h = g.uniform(0.5, 2, n + 4).astype(np.float32)
+    if kind == "contig":
+        st = tuple(int(np.prod(shape[d + 1:])) for d in range(nd))
+        return h, st, lambda base: h[base:base + n].reshape(shape)
+    # trans: column-major storage
+    st = tuple(int(np.prod(shape[:d])) for d in range(nd))
+    return h, st, lambda base: h[base:base + n].reshape(shape[::-1]).transpose(
+        tuple(range(nd))[::-1])
+
+
+@pytest.mark.parametrize("case", range(40))
+def test_program_random(native, case):
+    shape, ins, prog, out_reg = _random_programs()[case]
+    announce(f"program random {case}: shape {shape}, inputs {ins}, {len(prog)} instructions")
+    g = rng(900 + case)
+    P = native
+    inputs, views, keep = [], [], []
+    for kind, base in ins:
+        h, st, view = _input_view(kind, shape, g)
+        d = up(native, h)
+        keep.append(d)
+        inputs.append((d.ptr + 4 * base, st))
+        views.append(view(base).astype(np.float32))
+    code = {"add": P.PI_ADD, "sub": P.PI_SUB, "mul": P.PI_MUL, "div": P.PI_DIV,
+            "addi": P.PI_ADDI, "muli": P.PI_MULI, "rsubi": P.PI_RSUBI, "rdivi": P.PI_RDIVI,
+            "relu": P.PI_RELU}
+    instrs, regs = [], {}
+    with np.errstate(all="ignore"):
+        for ins_ in prog:
+            if ins_[0] == "load":
+                instrs.append((P.PI_LOAD, ins_[1], ins_[2]))
+                regs[ins_[1]] = views[ins_[2]]
+                continue
+            op, dst, a, b, imm = ins_
+            instrs.append((code[op], dst, a, b, imm))
+            x, y, c = regs[a], regs[b], np.float32(imm)
+            regs[dst] = {"add": lambda: x + y, "sub": lambda: x - y, "mul": lambda: x * y,
+                         "div": lambda: x / y, "addi": lambda: x + c, "muli": lambda: x * c,
+                         "rsubi": lambda: c - x, "rdivi": lambda: c / x,
+                         "relu": lambda: np.maximum(x, np.float32(0))}[op]().astype(np.float32)
+    n = int(np.prod(shape))
+    do = empty(native, n)
+    P.program_f32(P.make_program(shape, inputs, instrs, out_reg=out_reg), do)
+    got = down(native, do, shape)
+    ref = np.broadcast_to(regs[out_reg], shape)
+    assert np.array_equal(got, ref, equal_nan=True)
