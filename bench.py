@@ -611,6 +611,11 @@ def main():
                 secondary[k] = {"value": round(v["tflops"], 2), "unit": "TFLOP/s",
                                 "us": round(v["us"], 1), "reference_m1pro_ms": v["ref_ms"],
                                 "roofline": roofline("mfma", v["tflops"], traffic)}
+            # no cpu_baseline: the reference's conv2d has no CPU path
+            secondary[k]["cpu_baseline"] = None
+            secondary[k]["cpu_baseline_note"] = (
+                "the reference evaluates conv2d on the GPU only (include/array.h:2259-2272 "
+                "calls gpu::conv2d on every device)")
     if want("rowops"):
         r = bench_rowops(nat, g)
         log(f"rowops {r}")
