@@ -130,7 +130,7 @@ context *ctx_if_ready();
 // Direct convolution (conv.hip) for reductions K*K*C_in <= kConvDirectMaxK:
 // NHWC in [M = N*H*W pixels][C_in], OHWI w, NHWC out, stride 1, padding K/2.
 constexpr int kConvDirectMaxK = 64;
-constexpr int64_t kConvDirectMaxCo = int64_t(65535) * 16;  // grid.y = C_out / 16 blocks
+constexpr int64_t kConvDirectMaxCo = int64_t(65535) * 64;  // grid.y = ceil(C_out / 64) blocks
 int conv2d_direct(const float *in, const float *w, float *out, int M, int H, int W, int cin,
                   int K, int Co, hipStream_t s);
 

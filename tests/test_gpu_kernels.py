@@ -997,7 +997,11 @@ CONV_CASES = [(1, 8, 8, 3, 3, 16), (1, 5, 6, 4, 1, 5), (2, 9, 5, 6, 2, 40), (3, 
               (1, 3, 3, 2, 7, 3), (2, 8, 8, 16, 3, 60),
               (1, 224, 224, 3, 3, 32), (16, 56, 56, 64, 3, 128), (16, 28, 28, 128, 3, 256),
               (16, 56, 56, 48, 3, 128), (1, 116, 256, 32, 3, 256), (16, 28, 28, 80, 4, 256),
-              (16, 28, 28, 48, 3, 256)]
+              (16, 28, 28, 48, 3, 256),
+              # direct path (K*K*C_in <= 64): every step count, 1/2/4 channel
+              # blocks, two channel-block rows, ragged pixel tiles across images
+              (2, 7, 5, 2, 2, 20), (1, 9, 11, 4, 3, 24), (2, 5, 5, 1, 5, 70), (3, 5, 3, 3, 3, 17),
+              (4, 12, 10, 1, 1, 3), (2, 33, 17, 7, 3, 64)]
 
 
 @pytest.mark.parametrize("N,H,W,Ci,K,Co", CONV_CASES)
