@@ -1001,7 +1001,7 @@ CONV_CASES = [(1, 8, 8, 3, 3, 16), (1, 5, 6, 4, 1, 5), (2, 9, 5, 6, 2, 40), (3, 
               # direct path (K*K*C_in <= 64): every step count, 1/2/4 channel
               # blocks, two channel-block rows, ragged pixel tiles across images
               (2, 7, 5, 2, 2, 20), (1, 9, 11, 4, 3, 24), (2, 5, 5, 1, 5, 70), (3, 5, 3, 3, 3, 17),
-              (4, 12, 10, 1, 1, 3), (2, 33, 17, 7, 3, 64)]
+              (4, 12, 10, 1, 1, 3), (2, 33, 17, 7, 3, 64), (1, 1, 9, 2, 3, 5), (2, 6, 1, 2, 5, 4)]
 
 
 @pytest.mark.parametrize("N,H,W,Ci,K,Co", CONV_CASES)
