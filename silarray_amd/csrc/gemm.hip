@@ -1585,9 +1585,9 @@ struct plan {
 // Shape heuristic (choose_plan): a cost model of each candidate tile and K
 // split -- workgroup rounds per CU, the tile's sustained MFMA efficiency,
 // occupancy, a K-loop ramp, a per-K-step latency floor and the split-K
-// partial pass -- calibrated on MI355X sweeps (8192^3, 4096^3, 2048^3,
-// linear_sigmoid 256x4096x4096, transformer projections, small M <= 512
-// products).  M <= 32 with batch 1 goes to the small-M kernel.
+// partial pass -- calibrated on MI355X tile x split sweeps (squares up to
+// 4096^3, linear_sigmoid 256x4096x4096, transformer projections, small and
+// ragged products).  M <= 32 with batch 1 goes to the small-M kernel.
 // The 32x128 tile for M <= 32, K split for about 256 workgroups.
 plan small_m_tiles(int64_t M, int64_t N, int64_t K, int64_t batch) {
   plan p{TILE_32x128, 1};
@@ -1623,13 +1623,16 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dtl_ok) {
   // workgroups, min(that, occupancy) of them at once; a SIMD holding a
   // single wavefront reaches kSingleWave of the rate it reaches with two or
   // more.  eff is the fraction of fp32 MFMA peak each tile reaches at large
-  // K, and the K loop reaches half its rate at klen = kK0.  A workgroup
-  // also takes at least lat per 16-deep K step (one global -> LDS round trip
-  // that nothing else hides when a CU holds few workgroups: the floor of
-  // small products).  Split-K adds the partial-sum pass: a launch, (splits +
-  // 1) M x N fp32 passes and a per-plane latency.  Fitted to tile/split
-  // sweeps of square, transformer-block and small (M <= 512) shapes on
-  // MI355X.
+  // K -- for the LDS-direct kernel where the operands allow it, else for the
+  // register-staged one -- and the K loop reaches half its rate at klen =
+  // kK0.  A workgroup also takes at least lat per 16-deep K step (one global
+  // -> LDS round trip that nothing else hides when a CU holds few
+  // workgroups: the floor of small products).  Split-K adds the partial-sum
+  // pass: a launch, (splits + 1) M x N fp32 passes and a per-plane latency.
+  // Fitted on MI355X to full tile x split sweeps of 42 shapes (30 the
+  // LDS-direct kernel takes, from 64 x 768 x 2048 to 4096^3, and 12 ragged
+  // ones): the plan costs on average 0.2% (aligned; at most 2.2%) and 2.3%
+  // (ragged) more than the best fixed plan.
   struct cand {
     int tile, bm, bn, bk, waves, occupancy;
     double eff, lat;
@@ -1637,12 +1640,13 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dtl_ok) {
   // The 128x64 tile runs the LDS-direct kernel when the operands allow it
   // (fitted 0.82 of peak at three workgroups per CU on the 2048-row
   // transformer and square shapes), the register-staged one otherwise.
+  const bool dtl128 = dtl_ok && M % 128 == 0 && N % 128 == 0;
   const bool dtl64 = dtl_ok && M % 128 == 0 && N % 64 == 0;
-  const cand cands[] = {{TILE_256x256, 256, 256, 16, 8, 1, 0.87, 1.1e-6},
-                        {TILE_128x128, 128, 128, 16, 4, 3, 0.84, 1.1e-6},
-                        {TILE_128x64, 128, 64, 16, 4, dtl64 ? 3 : 5, dtl64 ? 0.82 : 0.75, 0.57e-6},
-                        {TILE_64x64, 64, 64, 16, 4, 8, 0.64, 0.47e-6}};
-  constexpr double kK0 = 64.0, kSingleWave = 0.76, kLaunch = 4.0e-6;
+  const cand cands[] = {{TILE_256x256, 256, 256, 16, 8, 1, 0.87, 1.15e-6},
+                        {TILE_128x128, 128, 128, 16, 4, 3, dtl128 ? 0.81 : 0.70, 1.25e-6},
+                        {TILE_128x64, 128, 64, 16, 4, dtl64 ? 3 : 5, dtl64 ? 0.86 : 0.71, 0.57e-6},
+                        {TILE_64x64, 64, 64, 16, 4, 8, 0.64, 0.52e-6}};
+  constexpr double kK0 = 48.0, kSingleWave = 0.85, kLaunch = 4.0e-6;
   const double rate_cu = 157.3e12 / 256.0;
   auto round_time = [&](const cand &cd, int64_t nwg, double klen) {
     const int64_t per_cu = cdiv(nwg, 256);
@@ -1656,7 +1660,7 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dtl_ok) {
     return t > floor_t ? t : floor_t;
   };
   auto sum_time = [](int sp, int64_t rows, int64_t cols) {
-    return 2.0e-6 + double(sp + 1) * double(rows) * double(cols) * 4.0 / 5.0e12 + 0.25e-6 * sp;
+    return 0.8e-6 + double(sp + 1) * double(rows) * double(cols) * 4.0 / 5.0e12 + 0.05e-6 * sp;
   };
   plan best{TILE_128x128, 1};
   double best_t = 1e30;
