@@ -1604,6 +1604,18 @@ __global__ __launch_bounds__(256) void splitk_sum_k(const float *__restrict__ ws
   float v[P];
 #pragma unroll
   for (int q = 0; q < P; ++q) v[q] = 0.0f;
+  // The epilogue's bias and residual values are loaded with the planes, not
+  // after their sum, so their latency overlaps the plane loads'.
+  const int64_t e = gi * P, m = e / N, n = e % N;
+  const bool has_bias = ep.epi == SILGPU_EPI_BIAS || ep.epi == SILGPU_EPI_BIAS_SIGMOID ||
+                        ep.epi == SILGPU_EPI_BIAS_RELU;
+  float bv[P], rv[P];
+#pragma unroll
+  for (int q = 0; q < P; ++q) {
+    const bool mine = gi < groups && (!DEEP || wave == 0);
+    bv[q] = mine && has_bias ? ep.bias[(n + q) % ep.bias_len] : 0.0f;
+    rv[q] = mine && ep.res ? ep.res[m * ep.ldr + n + q] : 0.0f;
+  }
   if (gi < groups) {
     const float *src = ws + gi * P;
     // Groups of G planes, all loads of a group in flight together (the last
@@ -1634,9 +1646,8 @@ __global__ __launch_bounds__(256) void splitk_sum_k(const float *__restrict__ ws
       for (int q = 0; q < P; ++q) v[q] += red[w][q][lane];
   }
   if (gi >= groups) return;
-  const int64_t e = gi * P, m = e / N, n = e % N;
 #pragma unroll
-  for (int q = 0; q < P; ++q) v[q] = apply_epi(v[q], m, n + q, ep);
+  for (int q = 0; q < P; ++q) v[q] = apply_epi_vals(v[q], bv[q], rv[q], ep);
   float *dst = C + m * ldc + n;
   if constexpr (VEC)
     *reinterpret_cast<float4 *>(dst) = make_float4(v[0], v[1], v[2], v[3]);
