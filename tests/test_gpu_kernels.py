@@ -808,12 +808,15 @@ def test_gemm_two_level_batch_head_split(native, oracle):
 
 
 @pytest.mark.parametrize("M,N,K", [(100, 130, 200), (256, 256, 4096), (1, 300, 257),
-                                   (512, 512, 96), (2048, 2304, 768)])
+                                   (512, 512, 96), (2048, 2304, 768), (2048, 3072, 768),
+                                   (4096, 4096, 512), (1500, 513, 120)])
 def test_gemm_fused_epilogue_bit_exact(native, oracle, M, N, K):
     """scale -> bias -> relu -> residual fused into the product equals the
     same fp32 steps run as separate kernels (affine fma, bias add, relu,
     residual add), bit for bit, on every GEMM path (MFMA tiles, split K,
-    GEMV for M == 1, a peeled split tail)."""
+    GEMV for M == 1, a peeled split tail; unsplit LDS-direct 128 x 64 and
+    256 x 128 tiles and a ragged register-staged product, whose epilogues
+    load bias and residual ahead of the stores)."""
     announce(f"gemm fused epilogue {M}x{N}x{K}")
     g = rng(2200 + M + K)
     A = g.uniform(-1, 1, (M, K)).astype(np.float32)
