@@ -16,10 +16,11 @@
 // all resident) and each wavefront's running softmax covers half the keys;
 // the two halves of a row group are merged through LDS at the end
 // (m = max(m0, m1), l and O rescaled by exp(m_h - m)).  The block's K
-// (row-major, pitch D + 8) and V (transposed, Vt[d][key], pitch 72) are
-// staged in LDS; the next block's loads are issued before the current block
-// is multiplied.  Both products are computed transposed on
-// v_mfma_f32_16x16x4f32, so that each lane owns one query row:
+// (row-major, pitch D + 8) and V (row-major, pitch D + 4) are staged in LDS
+// with one 16-byte write per loaded float4; the next block's loads are
+// issued before the current block is multiplied.  Both products are
+// computed transposed on v_mfma_f32_16x16x4f32, so that each lane owns one
+// query row:
 //   S^T (32 keys x 16 rows) = K Q^T: the head dim in groups of 16 whose k
 //     values go to the lane's k slot q as 16 g + 4 q + j at step j (any
 //     assignment of k to slots adds the same products), so Q^T sits in
@@ -31,7 +32,10 @@
 //     one factor per lane;
 //   O^T (D x 16 rows) += V^T P^T: the exponentiated scores are already the
 //     B operand (key 16 jb + 4 q + j of row c at step j), so P never leaves
-//     registers; V^T is one ds_read_b128 from Vt per block and key group.
+//     registers; lane (c, q) reads its V^T operands V[key 16 jb + 4 q + j]
+//     [d 16 jd + c] for j < 4 as four ds_read_b32 (row-major V needs no
+//     transposing writes: 38.8 against 40.9 us at the encoder shape, 51.5
+//     against 56.1 at head dim 128).
 // O is divided by l at the end and stored through the output strides (the
 // head-merged [B*S, H*D] layout included) as a float4 per lane and block.
 #include <hip/hip_runtime.h>
@@ -50,10 +54,12 @@ constexpr int kAttnThreads = kAttnWaves * kWave;
 constexpr int kBQ = 32;       // query rows per workgroup (two row groups of 16)
 constexpr int kBKey = 64;     // keys per block (two halves of 32)
 constexpr int kHalf = kBKey / 2;
-// LDS row pitches.  K and Vt are read with ds_read_b128 by lanes (c, q) at
-// row c, float 4 q: with the pitch a multiple of 8 floats but not of 16
-// ((pitch / 4) % 4 == 2), the 16 lanes of each b128 pass hit distinct
-// 16-byte bank groups.
+// LDS row pitches.  K is read with ds_read_b128 by lanes (c, q) at row c,
+// float 4 q: with the pitch a multiple of 8 floats but not of 16 ((pitch /
+// 4) % 4 == 2), the 16 lanes of each b128 pass hit distinct 16-byte bank
+// groups.  V is read with ds_read_b32 by lanes (c, q) at row 4 q + j, float
+// c: a pitch of 4 mod 8 floats puts the two q of each half-wave pass on
+// disjoint halves of the 32 banks.
 constexpr int kPadKV = 8;
 
 template <int D>
@@ -61,13 +67,13 @@ struct attn_cfg {
   static_assert(D % 16 == 0 && D >= 16 && D <= 128, "head dim");
   static constexpr int kG = D / 16;                  // 16-deep groups of D = 16-column blocks of O
   static constexpr int kKPitch = D + kPadKV;         // Ks[key][d]
-  static constexpr int kVPitch = kBKey + kPadKV;     // Vt[d][key]
+  static constexpr int kVPitch = D + 4;              // Vs[key][d]
   static constexpr int kKs = kBKey * kKPitch;
-  static constexpr int kVt = D * kVPitch;
-  static constexpr int kLdsBytes = (kKs + kVt) * 4;
+  static constexpr int kVs = kBKey * kVPitch;
+  static constexpr int kLdsBytes = (kKs + kVs) * 4;
   // Merge of the key halves: per lane, O (D/4 floats), m and l.
   static constexpr int kXfer = (D / 4 + 2) * kWave * 2;  // two row groups
-  static_assert(kXfer <= kKs + kVt, "merge area");
+  static_assert(kXfer <= kKs + kVs, "merge area");
   static constexpr int kLoads = kBKey * (D / 4) / kAttnThreads;  // float4 per thread per operand
   static_assert(kLoads * kAttnThreads * 4 == kBKey * D, "block load split");
 };
@@ -99,7 +105,7 @@ template <int D>
 __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
   using C = attn_cfg<D>;
   extern __shared__ __attribute__((aligned(16))) float lds[];
-  float *Ks = lds, *Vt = lds + C::kKs;
+  float *Ks = lds, *Vs = lds + C::kKs;
   const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
   const int c = lane % 16, q = lane / 16;
   const int64_t zo = blockIdx.y / a.binner, zi = blockIdx.y % a.binner;
@@ -123,8 +129,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
   }
 
   // Staging registers of one key block: thread t loads float4 f = t + 256 u
-  // of K as (key f / (D/4), d4 f % (D/4)) and of V as (key f % 64,
-  // d4 f / 64), so the transposed LDS writes of V are conflict-free.
+  // of K and of V as (key f / (D/4), d4 f % (D/4)): whole rows per group of
+  // lanes, coalesced, and one ds_write_b128 each.
   // Per-thread source pointers at key 0, advanced by whole blocks.
   float4 kst[C::kLoads], vst[C::kLoads];
   const float *kp[C::kLoads], *vp[C::kLoads];
@@ -132,7 +138,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
   for (int u = 0; u < C::kLoads; ++u) {
     const int f = t + kAttnThreads * u;
     kp[u] = K + int64_t(f / (D / 4)) * a.ldk + 4 * (f % (D / 4));
-    vp[u] = V + int64_t(f % kBKey) * a.ldv + 4 * (f / kBKey);
+    vp[u] = V + int64_t(f / (D / 4)) * a.ldv + 4 * (f % (D / 4));
   }
   auto load_block = [&](int key0) {
     const int64_t ko = int64_t(key0) * a.ldk, vo = int64_t(key0) * a.ldv;
@@ -148,7 +154,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
         const int f = t + kAttnThreads * u;
         const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
         kst[u] = key0 + f / (D / 4) < Sk ? ld4u(kp[u] + ko, a.vec) : z;
-        vst[u] = key0 + f % kBKey < Sk ? ld4u(vp[u] + vo, a.vec) : z;
+        vst[u] = key0 + f / (D / 4) < Sk ? ld4u(vp[u] + vo, a.vec) : z;
       }
     }
   };
@@ -157,12 +163,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
     for (int u = 0; u < C::kLoads; ++u) {
       const int f = t + kAttnThreads * u;
       const int kk = f / (D / 4), kd = f % (D / 4);
-      const int vk = f % kBKey, vd = f / kBKey;
       *reinterpret_cast<float4 *>(Ks + kk * C::kKPitch + 4 * kd) = kst[u];
-      Vt[(4 * vd + 0) * C::kVPitch + vk] = vst[u].x;
-      Vt[(4 * vd + 1) * C::kVPitch + vk] = vst[u].y;
-      Vt[(4 * vd + 2) * C::kVPitch + vk] = vst[u].z;
-      Vt[(4 * vd + 3) * C::kVPitch + vk] = vst[u].w;
+      *reinterpret_cast<float4 *>(Vs + kk * C::kVPitch + 4 * kd) = vst[u];
     }
   };
 
@@ -239,15 +241,16 @@ __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
 #pragma unroll
     for (int jd = 0; jd < C::kG; ++jd) acc_o[jd] *= alpha;
 
-    // O^T += V^T P^T: A operand V^T (ds_read_b128 from Vt), B operand P^T,
+    // O^T += V^T P^T: A operand V^T (four ds_read_b32 from Vs), B operand P^T,
     // which is p: register r of key block jb is key 16 jb + 4 q + r of this
     // lane's row, the operand layout the MFMA asks for.
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
       for (int jd = 0; jd < C::kG; ++jd) {
-        const float4 vb = *reinterpret_cast<const float4 *>(
-            Vt + (16 * jd + c) * C::kVPitch + kbase + 16 * jb + 4 * q);
+        const float *vr = Vs + (kbase + 16 * jb + 4 * q) * C::kVPitch + 16 * jd + c;
+        const float4 vb = make_float4(vr[0], vr[C::kVPitch], vr[2 * C::kVPitch],
+                                      vr[3 * C::kVPitch]);
         acc_o[jd] = mma4(acc_o[jd], vb, p[jb]);
       }
   }
