@@ -217,8 +217,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
         v[jb][r] = x;
         rm = fmaxf(rm, x);
       }
-    rm = fmaxf(rm, __shfl_xor(rm, 16, kWave));
-    rm = fmaxf(rm, __shfl_xor(rm, 32, kWave));
+    const auto fmax2 = [](float a, float b) { return fmaxf(a, b); };
+    const auto add2 = [](float a, float b) { return a + b; };
+    rm = pair_reduce<32>(pair_reduce<16>(rm, fmax2), fmax2);
     const float mn = fmaxf(m, rm);
     const bool none = mn == -INFINITY;  // no finite score in this row yet
     const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
@@ -234,8 +235,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_k(attn_args a) {
       }
       p[jb] = make_float4(e[0], e[1], e[2], e[3]);
     }
-    rs += __shfl_xor(rs, 16, kWave);
-    rs += __shfl_xor(rs, 32, kWave);
+    rs = pair_reduce<32>(pair_reduce<16>(rs, add2), add2);
     l = l * alpha + rs;
     m = mn;
 #pragma unroll

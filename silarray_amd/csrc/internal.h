@@ -145,26 +145,74 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 constexpr int kWave = 64;
 
-// Butterfly reductions across the 64 lanes of a wavefront.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+// Register-only exchanges within a wavefront (no LDS round trip).  DPP
+// controls act within each row of 16 lanes: quad_perm [1,0,3,2] and [2,3,0,1]
+// read lane i ^ 1 and i ^ 2, row_half_mirror lane 7 - i of each group of 8,
+// row_mirror lane 15 - i of the row.
+constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppHalfMirror = 0x141,
+              kDppRowMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
 }
-__device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+template <int CTRL>
+__device__ __forceinline__ double dpp_mov(double v) {
+  return __hiloint2double(__builtin_amdgcn_mov_dpp(__double2hiint(v), CTRL, 0xF, 0xF, false),
+                          __builtin_amdgcn_mov_dpp(__double2loint(v), CTRL, 0xF, 0xF, false));
 }
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ double lane_value(double v, int lane) {
+  return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), lane),
+                          __builtin_amdgcn_readlane(__double2loint(v), lane));
+}
+
+// All-reduce over the 64 lanes of a wavefront, every lane active.  After the
+// four DPP steps each lane's value covers its whole row of 16 lanes (the
+// steps pair lanes across 2, 4, 8 and 16); the rows then combine in a fixed
+// order from lanes 0, 16, 32 and 48 (scalar reads), so every lane returns the
+// same value.
+template <typename T, typename F>
+__device__ __forceinline__ T wave_allreduce(T v, F op) {
+  v = op(v, dpp_mov<kDppQuadXor1>(v));
+  v = op(v, dpp_mov<kDppQuadXor2>(v));
+  v = op(v, dpp_mov<kDppHalfMirror>(v));
+  v = op(v, dpp_mov<kDppRowMirror>(v));
+  return op(op(lane_value(v, 0), lane_value(v, 16)), op(lane_value(v, 32), lane_value(v, 48)));
+}
+
+// op over lanes i and i ^ 16 (ROWS = 16) or i and i ^ 32 (ROWS = 32) through
+// gfx950's v_permlane16_swap / v_permlane32_swap with v as both operands: the
+// two results hold, on both lanes of each pair, the pair's lower- and
+// upper-half values, so both lanes compute op(lower, upper) and agree.
+template <int ROWS, typename F>
+__device__ __forceinline__ float pair_reduce(float v, F op) {
+  static_assert(ROWS == 16 || ROWS == 32, "lane distance 16 or 32");
+  const unsigned u = __float_as_uint(v);
+  if constexpr (ROWS == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+}
+
+// Reductions across the 64 lanes of a wavefront (every lane active); every
+// lane returns the result.
+struct add_op {
+  template <typename T>
+  __device__ T operator()(T a, T b) const { return a + b; }
+};
+__device__ __forceinline__ float wave_sum(float v) { return wave_allreduce(v, add_op{}); }
+__device__ __forceinline__ double wave_sum(double v) { return wave_allreduce(v, add_op{}); }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
+  return wave_allreduce(v, [](float a, float b) { return fmaxf(a, b); });
 }
 __device__ __forceinline__ float wave_min(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, kWave));
-  return v;
+  return wave_allreduce(v, [](float a, float b) { return fminf(a, b); });
 }
 
 __device__ __forceinline__ float sigmoidf_dev(float x) { return 1.0f / (1.0f + expf(-x)); }

@@ -29,6 +29,13 @@ __device__ __forceinline__ float rescale(float m, float M) {
   return m == -INFINITY ? 0.0f : expf(m - M);
 }
 
+struct fmax_op {
+  __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+struct dsum_op {
+  __device__ double operator()(double a, double b) const { return a + b; }
+};
+
 // Reductions over a group of NT threads that own one row.  NT == 64: one
 // wavefront; NT > 64: the whole workgroup (NT threads) through LDS.
 template <int NT>
@@ -37,8 +44,7 @@ struct group {
 
   template <typename T, typename F>
   __device__ static T reduce(T v, F op) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = op(v, __shfl_xor(v, o, kWave));
+    v = wave_allreduce(v, op);
     if constexpr (NT == kWave) {
       return v;
     } else {
@@ -59,8 +65,7 @@ struct group {
   template <int SLOT, typename T, typename F>
   __device__ static T reduce_once(T v, F op) {
     static_assert(NT == kWave || NT >= 256, "one group per workgroup");
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = op(v, __shfl_xor(v, o, kWave));
+    v = wave_allreduce(v, op);
     if constexpr (NT == kWave) {
       return v;
     } else {
@@ -81,12 +86,8 @@ struct group {
   // wave publishes its (max, sum) pair once.  Used once per kernel.
   __device__ static void softmax_stats(float m, double s, float &M, double &S) {
     static_assert(NT == kWave || NT >= 256, "one group per workgroup");
-    float mw = m;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mw = fmaxf(mw, __shfl_xor(mw, o, kWave));
-    double sw = s * static_cast<double>(rescale(m, mw));
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) sw += __shfl_xor(sw, o, kWave);
+    const float mw = wave_allreduce(m, fmax_op{});
+    const double sw = wave_allreduce(s * static_cast<double>(rescale(m, mw)), dsum_op{});
     if constexpr (NT == kWave) {
       M = mw;
       S = sw;
@@ -109,13 +110,6 @@ struct group {
       S = sg;
     }
   }
-};
-
-struct fmax_op {
-  __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
-};
-struct dsum_op {
-  __device__ double operator()(double a, double b) const { return a + b; }
 };
 
 // Access modes of a row: scalar (any cols, any alignment), float4 with
