@@ -88,9 +88,8 @@ __device__ __forceinline__ float4 load_nt(const float4 *p) {
 
 template <int R>
 __device__ __forceinline__ typename racc<R>::T wave_merge(typename racc<R>::T v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = racc<R>::merge(v, __shfl_xor(v, o, kWave));
-  return v;
+  using T = typename racc<R>::T;
+  return wave_allreduce(v, [](T a, T b) { return racc<R>::merge(a, b); });
 }
 
 // Workgroup-wide merge; the result is valid in every thread.
@@ -349,15 +348,21 @@ __device__ __forceinline__ vi better(vi a, vi b) {
   return take_b ? b : a;
 }
 
+// The wave's best (value, index) in every lane, as wave_allreduce: four DPP
+// steps per 16-lane row, then the rows from lanes 0, 16, 32 and 48.  A lane
+// holds a NaN only as {NaN, kNoIndex}, so `better` selects by one total order
+// (value, then smaller index) and the pairing does not change the result.
+template <int CTRL>
+__device__ __forceinline__ vi dpp_vi(vi x) {
+  return vi{dpp_mov<CTRL>(x.v), __builtin_amdgcn_mov_dpp(x.i, CTRL, 0xF, 0xF, false)};
+}
 __device__ __forceinline__ vi wave_best(vi x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    vi y;
-    y.v = __shfl_xor(x.v, o, kWave);
-    y.i = __shfl_xor(x.i, o, kWave);
-    x = better(x, y);
-  }
-  return x;
+  x = better(x, dpp_vi<kDppQuadXor1>(x));
+  x = better(x, dpp_vi<kDppQuadXor2>(x));
+  x = better(x, dpp_vi<kDppHalfMirror>(x));
+  x = better(x, dpp_vi<kDppRowMirror>(x));
+  const auto at = [&](int l) { return vi{lane_value(x.v, l), __builtin_amdgcn_readlane(x.i, l)}; };
+  return better(better(at(0), at(16)), better(at(32), at(48)));
 }
 
 __device__ __forceinline__ vi block_best(vi x) {
