@@ -434,6 +434,61 @@ def test_argmax_golden_nan_negative(native, oracle, ref_vectors):
     assert list(down(native, do, 2, np.int32)) == list(oracle.argmax_rows(z)) == [2, 4]
 
 
+def test_wave_exchange_lane_patterns(native, oracle):
+    """Rows whose deciding values sit in single lanes of different 16-lane
+    rows of a wavefront (and of different wavefronts for 512-thread rows), so
+    the in-register exchanges must carry them across rows and waves.  In the
+    one-wavefront argmax, column c is scanned by lane c % 64; in the row ops,
+    thread t holds columns 4(k NT + t) .. + 3."""
+    announce("wave exchange lane patterns")
+    cols = 256
+    x = np.full((7, cols), -1.0, np.float32)
+    x[0, [48, 32, 16, 64]] = 5.0            # lanes 48, 32, 16, 0: first index (16)
+    x[1, [127, 66, 250]] = 5.0              # lanes 63, 2, 58: 66
+    x[2, :] = np.nan                        # no number: index 0
+    x[3, 0:16] = np.nan
+    x[3, 175] = 0.5                         # lane 47 past a row of NaN lanes
+    x[4, 99] = -0.0                         # lane 35
+    x[4, 20] = 0.0                          # lane 20: equal to -0, first index wins
+    x[5, :] = -np.inf
+    x[5, 61] = -3e38                        # the only number, lane 61
+    x[6, :] = np.nan
+    x[6, 200] = -np.inf                     # lane 8: -inf beats no number
+    dx, do = up(native, x), empty(native, 7, np.int32)
+    native.argmax_rows_f32(dx, 7, cols, do)
+    ref = oracle.argmax_rows(x)
+    assert list(ref) == [16, 66, 0, 175, 20, 61, 200]
+    assert np.array_equal(down(native, do, 7, np.int32), ref)
+
+    # softmax / layer_norm: one-wavefront rows (256 columns: thread t holds
+    # 4t .. 4t + 3) and 512-thread rows (8192 columns, 8 wavefronts)
+    for rows, cols, spots in [(3, 256, [(201, 2.0), (13, 1.0)]),
+                              (3, 8192, [(4 * (2 * 512 + 357) + 1, 2.0), (13, 1.0),
+                                         (4 * (3 * 512 + 511) + 3, 0.5)])]:
+        y = np.full((rows, cols), -np.inf, np.float32)
+        for c, v in spots:
+            y[0, c] = v                       # finite values in two or three lanes only
+        y[1] = rng(77).normal(0, 1, cols)
+        y[1, cols - 1] = 30.0                 # the last lane's value dominates
+        y[2] = rng(78).normal(0, 3, cols)
+        dy, do = up(native, y), empty(native, rows * cols)
+        native.softmax_rows_f32(dy, do, rows, cols)
+        out = down(native, do, (rows, cols)).astype(np.float64)
+        sref = oracle.softmax_rows_f64(y)
+        assert np.all(np.abs(out - sref) <= 1e-5 * sref + 1e-30), cols
+        z = np.zeros((rows, cols), np.float32)
+        for c, v in spots:
+            z[0, c] = 100.0 * v                # outliers in single lanes
+        z[1], z[2] = y[1], y[2]
+        gamma = np.ones(cols, np.float32)
+        beta = np.zeros(cols, np.float32)
+        dz, dg, db = up(native, z), up(native, gamma), up(native, beta)
+        native.layer_norm_rows_f32(dz, do, dg, db, rows, cols, 1e-5)
+        out = down(native, do, (rows, cols)).astype(np.float64)
+        lref = oracle.layer_norm_f64(z, gamma, beta, 1e-5)
+        assert np.all(np.abs(out - lref) <= 1e-5 * np.maximum(1.0, np.abs(lref))), cols
+
+
 # ---- row ops ----------------------------------------------------------------------
 
 # Every register configuration in its three modes: rows that exactly fill the
