@@ -314,8 +314,11 @@ def test_program_period_beyond_32bit_index(native):
 
 # ---- reductions ------------------------------------------------------------------
 
+# Sizes of whole 4096-float load groups (25,165,824) and ones that end a
+# few floats into a group (8,388,612, 20,480,012, and 20,480,013 unaligned).
 @pytest.mark.parametrize("n,offset", [(1, 0), (7, 0), (1000, 1), (65536, 0), (1 << 22, 3),
-                                      (12345679, 2)])
+                                      (12345679, 2), (25165824, 0), (8388612, 0),
+                                      (20480012, 0), (20480013, 1)])
 def test_sum_min_max(native, oracle, n, offset):
     announce(f"sum/min/max n={n} offset={offset}")
     g = rng(800 + n % 97)
@@ -539,6 +542,25 @@ def test_layer_norm_rows(native, oracle, rows, cols):
     # |y - y64| <= 1e-5 * max(1, |y64|): relative 1e-5 at the unit scale the
     # normalisation produces
     assert np.all(np.abs(out - ref) <= 1e-5 * np.maximum(1.0, np.abs(ref)))
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 8192), (17, 768), (33, 3000), (5, 1001), (3, 50000)])
+def test_layer_norm_outlier_and_constant_rows(native, oracle, rows, cols):
+    """A first value 100 sigma out, and a constant row (variance exactly 0,
+    so the output is beta), match the float64 two-pass statistics."""
+    announce(f"layer_norm outlier first value {rows}x{cols}")
+    x = rng(1300 + cols).normal(0, 3, (rows, cols)).astype(np.float32)
+    x[:, 0] = 300.0
+    x[1, 0] = -300.0
+    x[2, :] = 1.25
+    gamma = np.ones(cols, np.float32)
+    beta = np.linspace(-1, 1, cols).astype(np.float32)
+    dx, dg, db, do = up(native, x), up(native, gamma), up(native, beta), empty(native, rows * cols)
+    native.layer_norm_rows_f32(dx, do, dg, db, rows, cols, 1e-5)
+    out = down(native, do, (rows, cols)).astype(np.float64)
+    ref = oracle.layer_norm_f64(x, gamma, beta, 1e-5)
+    assert np.all(np.abs(out - ref) <= 1e-5 * np.maximum(1.0, np.abs(ref)))
+    assert np.array_equal(out[2], beta.astype(np.float64))
 
 
 def test_layer_norm_golden(native, ref_vectors):
