@@ -194,7 +194,15 @@ __global__ __launch_bounds__(row_block<NT>()) void softmax_reg_k(const float *__
   if (NT == kWave && r >= rows) return;  // whole wavefronts exit together
   const float *src = in + r * cols;
   float x[V][4];
+  // A wave-per-row softmax with 32 values per lane raises the wave's issue
+  // priority while it issues its row's loads, so a newly started row's loads
+  // go out ahead of the exponentials of rows already loaded (4096 x 2048:
+  // 12.9 -> 10.6 us); with 4 or fewer float4 per lane (16384 x 1024,
+  // 65536 x 256) and with 512-thread rows it measured about 1% slower.
+  constexpr bool kLoadPrio = NT == kWave && V >= 8;
+  if constexpr (kLoadPrio) __builtin_amdgcn_s_setprio(3);
   load_row<NT, V, M>(src, cols, t, -INFINITY, x);
+  if constexpr (kLoadPrio) __builtin_amdgcn_s_setprio(0);
   // Each thread exponentiates against its own maximum m, so the row's
   // maximum and sum meet in one exchange: (m, s) pairs combine as
   // M = max m, S = sum s * exp(m - M).
@@ -237,7 +245,12 @@ __global__ __launch_bounds__(row_block<NT>()) void layer_norm_reg_k(
   const int t = threadIdx.x % NT;
   if (NT == kWave && r >= rows) return;
   float x[V][4];
+  // Raised issue priority while the row's loads go out, for workgroup rows
+  // only (4096 x 8192: 46.2 -> 45.8 us, 8192 x 4096: 46.2 -> 43.3;
+  // wave-per-row rows measured 5% slower with it).
+  if constexpr (NT > kWave) __builtin_amdgcn_s_setprio(3);
   load_row<NT, V, M>(in + r * cols, cols, t, 0.0f, x);
+  if constexpr (NT > kWave) __builtin_amdgcn_s_setprio(0);
   double s = 0.0;
 #pragma unroll
   for (int k = 0; k < V; ++k)
