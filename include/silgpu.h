@@ -230,6 +230,27 @@ int silgpu_sum_axis_f32(const float *d_in, int64_t outer, int64_t axis_len,
 int silgpu_argmax_rows_f32(const float *d_in, int64_t rows, int64_t cols,
                            int32_t *d_out);
 
+/* Failure reporting of the one-launch reductions (sum, min, max, argmax).
+ * Their finishing workgroup waits on the device for the other workgroups'
+ * partial results; the reference finishes on the host instead
+ * (include/gpu.h:331-354, include/array.h:1535-1545) and never waits on the
+ * device.  The wait is bounded by the device wall clock (50 ms); a finisher
+ * that gives up records the failure in a host-mapped word, and the next
+ * silgpu_sync (or sum/min/max/argmax call) returns SILGPU_ERR_HIP with a
+ * message and clears the partial-result slots for later calls.
+ *
+ * Test hooks for that path, with no counterpart in the reference:
+ *   silgpu_slot_wait_selftest launches a finisher over slots [0, nslots) that
+ *   nothing writes, waiting wait_us before it gives up; with late_us > 0 a
+ *   second workgroup publishes slot 0 after late_us (a producer later than
+ *   the deadline).  *d_taken (device, uint32) is increased by the number of
+ *   slots the finisher did receive.  Every wait in it ends on the wall clock.
+ *   silgpu_slots_in_use synchronises and counts the slots that are not zero
+ *   (zero between launches when nothing has failed). */
+int silgpu_slot_wait_selftest(int nslots, int64_t wait_us, int64_t late_us,
+                              uint32_t *d_taken);
+int silgpu_slots_in_use(int64_t *count);
+
 /* ---- row ops ------------------------------------------------------------ */
 
 /* Row softmax of a contiguous [rows, cols] array: exp(x - rowmax) / sum.
@@ -328,6 +349,15 @@ int silgpu_gemm(const silgpu_gemm_desc *desc);
  *     contents: calls that overlap in time on one device (several host
  *     threads, several streams) race. */
 int silgpu_gemm_noalloc(const silgpu_gemm_desc *desc);
+
+/* The matrix products the last silgpu_sgemm / silgpu_sgemm_tuned /
+ * silgpu_gemm / silgpu_gemm_noalloc call on this thread launched: *n of them
+ * (0 for a vector product, which runs the GEMV kernels; 2 when the last
+ * rows of C ran as a second product), and for each its tile configuration
+ * (the numbering of silgpu_sgemm_tuned), the K splits it launched and its
+ * rows of C.  The arrays hold at least two entries.  No reference
+ * counterpart: a diagnostic for tests and tile sweeps. */
+int silgpu_gemm_last_plan(int *n, int *tiles, int *splits, int *rows);
 
 /* Fused attention: for every batch index b = (o, i) (o < batch_outer,
  * i < batch_inner) and query row r < Sq,

@@ -131,6 +131,8 @@ _SIGS = {
     "silgpu_max_f32": (_i, [_vp, _i64, _vp]),
     "silgpu_sum_axis_f32": (_i, [_vp, _i64, _i64, _i64, _vp]),
     "silgpu_argmax_rows_f32": (_i, [_vp, _i64, _i64, _vp]),
+    "silgpu_slot_wait_selftest": (_i, [_i, _i64, _i64, _vp]),
+    "silgpu_slots_in_use": (_i, [C.POINTER(_i64)]),
     "silgpu_softmax_rows_f32": (_i, [_vp, _vp, _i64, _i64]),
     "silgpu_layer_norm_rows_f32": (_i, [_vp, _vp, _vp, _vp, _i64, _i64, _f]),
     "silgpu_sgemm": (_i, [_i, _i, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp,
@@ -139,6 +141,8 @@ _SIGS = {
                                 _vp, _i64, _i64, _i64, _vp, _i64, _i, _i, _i]),
     "silgpu_gemm": (_i, [C.POINTER(GemmDesc)]),
     "silgpu_gemm_noalloc": (_i, [C.POINTER(GemmDesc)]),
+    "silgpu_gemm_last_plan": (_i, [C.POINTER(_i), C.POINTER(_i), C.POINTER(_i),
+                                   C.POINTER(_i)]),
     "silgpu_sgemv": (_i, [_vp, _vp, _i64, _vp, _i64, _i64]),
     "silgpu_attention_f32": (_i, [C.POINTER(AttnDesc)]),
     "silgpu_conv2d_f32": (_i, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64]),
@@ -361,6 +365,15 @@ def gemm(ta, tb, M, N, K, A, lda, B, ldb, Cm, ldc, batch_outer=1, batch_inner=1,
     d.residual = vp(residual).value if residual is not None else None
     d.ldr = ldr
     call("silgpu_gemm_noalloc" if noalloc else "silgpu_gemm", C.byref(d))
+
+
+def last_plan() -> list[tuple[int, int, int]]:
+    """(tile, K splits, rows of C) of each product the last GEMM call on this
+    thread launched (silgpu_gemm_last_plan)."""
+    n = _i()
+    tiles, splits, rows = (_i * 2)(), (_i * 2)(), (_i * 2)()
+    call("silgpu_gemm_last_plan", C.byref(n), tiles, splits, rows)
+    return [(tiles[i], splits[i], rows[i]) for i in range(n.value)]
 
 
 def attention(Sq, Sk, D, scale, Q, ldq, K, ldk, V, ldv, O, ldo, batch_outer=1, batch_inner=1,

@@ -1873,6 +1873,17 @@ struct scratch_src {
   size_t fixed_bytes = 0;
 };
 
+// The products the last GEMM entry-point call on this thread launched, for
+// silgpu_gemm_last_plan: up to two (the main product and a peeled last
+// round of rows), each with its tile configuration, K splits and rows of C.
+struct launch_record {
+  int n = 0;
+  int tile[2] = {0, 0};
+  int splits[2] = {0, 0};
+  int rows[2] = {0, 0};
+};
+thread_local launch_record g_last_launch;
+
 int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, bool vec,
               context *c, const scratch_src &ss) {
   if (pl.tail_rows > 0 && pl.tail_rows < a0.M && batch == 1) {
@@ -1940,6 +1951,16 @@ int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, boo
     }
   }
   if (launched < 0) return launched;
+  launch_record &rec = g_last_launch;
+  if (rec.n < 2) {
+    const bool known = pl.tile == TILE_64x64 || pl.tile == TILE_32x128 ||
+                       pl.tile == TILE_128x64 || pl.tile == TILE_256x256;
+    rec.tile[rec.n] = skinny ? (q == 4 ? TILE_SKINNY_Q4 : q == 2 ? TILE_SKINNY_Q2 : TILE_SKINNY)
+                             : known ? pl.tile : TILE_128x128;
+    rec.splits[rec.n] = launched;
+    rec.rows[rec.n] = a.M;
+    ++rec.n;
+  }
   return launched > 1 ? launch_split_sum(a, launched, c) : SILGPU_OK;
 }
 
@@ -2099,6 +2120,7 @@ namespace {
 // heuristic.  `noalloc`: the library must already be initialised, and all
 // scratch comes from the fixed array found at init.
 int gemm_impl(const silgpu_gemm_desc &d, const plan *forced, bool noalloc = false) {
+  g_last_launch = launch_record{};
   const int64_t M = d.M, N = d.N, K = d.K;
   SILGPU_REQUIRE(M >= 0 && N >= 0 && K >= 0 && d.batch_outer >= 0 && d.batch_inner >= 0,
                  "silgpu_gemm: negative extent");
@@ -2255,6 +2277,18 @@ int silgpu_gemm(const silgpu_gemm_desc *desc) {
 int silgpu_gemm_noalloc(const silgpu_gemm_desc *desc) {
   SILGPU_REQUIRE(desc != nullptr, "silgpu_gemm_noalloc: null descriptor");
   return gemm_impl(*desc, nullptr, true);
+}
+
+int silgpu_gemm_last_plan(int *n, int *tiles, int *splits, int *rows) {
+  SILGPU_REQUIRE(n && tiles && splits && rows, "silgpu_gemm_last_plan: null argument");
+  const launch_record &rec = g_last_launch;
+  *n = rec.n;
+  for (int i = 0; i < rec.n; ++i) {
+    tiles[i] = rec.tile[i];
+    splits[i] = rec.splits[i];
+    rows[i] = rec.rows[i];
+  }
+  return SILGPU_OK;
 }
 
 int silgpu_conv2d_f32(const float *d_in, const float *d_w, float *d_out, int64_t N, int64_t H,

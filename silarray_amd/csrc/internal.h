@@ -44,9 +44,42 @@ struct context {
   // yet"); the workgroup that finishes the reduction waits for the slots it
   // needs, reads them and sets them back to zero before the launch ends.
   uint64_t *slots = nullptr;
+  // Failure word in pinned, coherent host memory (fail_host for the host,
+  // fail_dev for kernels): a finishing workgroup that gives up waiting for a
+  // slot stores kFailSlotWait there.  silgpu_sync and the reduction entry
+  // points read it, report the failure and clear the slots again.
+  uint32_t *fail_host = nullptr;
+  uint32_t *fail_dev = nullptr;
+  // Device wall-clock ticks (wall_clock64) per microsecond.
+  uint64_t wall_ticks_per_us = 100;
 };
 
 constexpr int kSlots = 16384;
+
+// How long a finishing workgroup waits for the partial results it needs
+// before it gives up: far beyond any producer's running time (a 64M-element
+// reduction runs for ~40 us), far below a stalled-queue watchdog.
+constexpr int64_t kSlotWaitUs = 50000;
+
+// Codes a kernel stores into the failure word.
+constexpr uint32_t kFailSlotWait = 1;
+
+// What a kernel that publishes or takes slots needs.
+struct slot_ctl {
+  uint64_t *slots;      // kSlots slots, zero at rest
+  uint32_t *fail;       // failure word (host-mapped)
+  uint64_t wait_ticks;  // wall-clock ticks a finisher waits before giving up
+};
+
+// slot_ctl of the context with the library's wait limit.
+inline slot_ctl slot_control(const context *c) {
+  return slot_ctl{c->slots, c->fail_dev, uint64_t(kSlotWaitUs) * c->wall_ticks_per_us};
+}
+
+// Reports (and clears) a failure recorded by a kernel, re-zeroing the slots
+// after every launch issued so far.  `idle`: the stream has just been
+// synchronised, so the clearing is waited for too.
+int check_device_failure(context *c, bool idle);
 
 // ---- slots: one 64-bit location per published value, zero at rest ----------
 //
@@ -55,12 +88,16 @@ constexpr int kSlots = 16384;
 // consumer in the same launch waits until the slot reads non-zero, takes the
 // value and clears the slot, so the area is zero again when the launch ends.
 // Each slot is written once and read as a whole, so no fence is needed.
-// Polls of one slot before a consumer stops waiting: every producer has been
-// dispatched before its consumer and publishes unconditionally, so the wait
-// ends within a memory round trip or two; the bound only keeps a broken
-// device from hanging the stream (and lets a value that really is all ones,
-// a NaN with a full payload, through after the wait).
-constexpr int kSpinLimit = 1 << 24;
+//
+// Forward progress: a consumer only waits for producers with a lower
+// workgroup index, and producers never wait.  Workgroups are dispatched in
+// index order on each XCD (the eight XCDs dispatch independently), so the
+// lowest-indexed waiting consumer always has every producer it waits for
+// either running, finished, or queued behind workgroups that will finish
+// without waiting: every wait ends once the producers have run.  The bound
+// below (one deadline per consumer thread, read from the device wall clock)
+// only turns a device that breaks this into a reported failure instead of a
+// stalled stream.
 
 __device__ __forceinline__ void slot_publish(uint64_t *slot, uint64_t bits) {
   __hip_atomic_store(slot, ~bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -68,15 +105,29 @@ __device__ __forceinline__ void slot_publish(uint64_t *slot, uint64_t bits) {
 __device__ __forceinline__ uint64_t slot_peek(uint64_t *slot) {
   return __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// Completes a read started with slot_peek(): waits while the slot reads zero,
-// clears it and returns the published bits.
-__device__ __forceinline__ uint64_t slot_take(uint64_t *slot, uint64_t seen) {
-  for (int it = 0; seen == 0 && it < kSpinLimit; ++it) {
-    __builtin_amdgcn_s_sleep(1);
-    seen = slot_peek(slot);
+// Completes a read started with slot_peek(): waits while the slot reads zero
+// (at most until `deadline`, set at this thread's first wait and shared by
+// its later ones), clears the slot and returns true with the published bits.
+// After the deadline it records kFailSlotWait in the failure word, leaves
+// the slot alone (the host clears every slot once the launch has ended) and
+// returns false: the caller leaves that partial out and the host reports
+// the result as failed.
+__device__ __forceinline__ bool slot_take(uint64_t *slot, uint64_t seen, uint64_t &deadline,
+                                          const slot_ctl &sc, uint64_t &bits) {
+  if (seen == 0) {
+    if (deadline == 0) deadline = wall_clock64() + sc.wait_ticks;
+    do {
+      __builtin_amdgcn_s_sleep(1);
+      seen = slot_peek(slot);
+    } while (seen == 0 && wall_clock64() < deadline);
+    if (seen == 0) {
+      __hip_atomic_store(sc.fail, kFailSlotWait, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      return false;
+    }
   }
   __hip_atomic_store(slot, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return ~seen;
+  bits = ~seen;
+  return true;
 }
 // Two floats in one slot.
 __device__ __forceinline__ uint64_t pack_f2(float a, float b) {

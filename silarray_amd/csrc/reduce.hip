@@ -25,6 +25,7 @@
 
 #include <cfloat>
 #include <cmath>
+#include <vector>
 
 #include "internal.h"
 
@@ -130,23 +131,28 @@ __device__ __forceinline__ typename racc<R>::T stream4(const float4 *__restrict_
 // g = t, t + kBlock, ..., kFinishLoads of them in flight), then across the
 // workgroup.
 template <int R>
-__device__ __forceinline__ void finish_full(typename racc<R>::T own, uint64_t *__restrict__ slots,
-                                            int G, float *__restrict__ out) {
+__device__ __forceinline__ void finish_full(typename racc<R>::T own, const slot_ctl &sc, int G,
+                                            float *__restrict__ out) {
   using T = typename racc<R>::T;
   T f = racc<R>::init();
+  uint64_t deadline = 0;
   for (int j0 = threadIdx.x; j0 < G; j0 += kFinishLoads * kBlock) {
     uint64_t seen[kFinishLoads];
 #pragma unroll
     for (int g = 0; g < kFinishLoads; ++g) {
       const int j = j0 + g * kBlock;
-      seen[g] = j < G - 1 ? slot_peek(slots + j) : 0;
+      seen[g] = j < G - 1 ? slot_peek(sc.slots + j) : 0;
     }
 #pragma unroll
     for (int g = 0; g < kFinishLoads; ++g) {
       const int j = j0 + g * kBlock;
       T v = racc<R>::init();
-      if (j < G - 1) v = racc<R>::unpack(slot_take(slots + j, seen[g]));
-      else if (j == G - 1) v = own;
+      uint64_t bits;
+      if (j < G - 1) {
+        if (slot_take(sc.slots + j, seen[g], deadline, sc, bits)) v = racc<R>::unpack(bits);
+      } else if (j == G - 1) {
+        v = own;
+      }
       f = racc<R>::merge(f, v);
     }
   }
@@ -160,7 +166,7 @@ __device__ __forceinline__ void finish_full(typename racc<R>::T own, uint64_t *_
 template <int R>
 __global__ __launch_bounds__(kBlock) void reduce_k(
     const float *__restrict__ head_ptr, int head, const float4 *__restrict__ x4, int64_t n4,
-    int64_t chunk4, const float *__restrict__ tail_ptr, int tail, uint64_t *__restrict__ slots,
+    int64_t chunk4, const float *__restrict__ tail_ptr, int tail, slot_ctl sc,
     float *__restrict__ out) {
   using T = typename racc<R>::T;
   const int64_t c0 = int64_t(blockIdx.x) * chunk4;
@@ -173,18 +179,17 @@ __global__ __launch_bounds__(kBlock) void reduce_k(
   const T b = block_merge<R>(acc);
   const int G = gridDim.x;
   if (blockIdx.x != G - 1) {
-    if (threadIdx.x == 0) slot_publish(slots + blockIdx.x, racc<R>::pack(b));
+    if (threadIdx.x == 0) slot_publish(sc.slots + blockIdx.x, racc<R>::pack(b));
     return;
   }
-  finish_full<R>(b, slots, G, out);
+  finish_full<R>(b, sc, G, out);
 }
 
 // Inputs that are not 4-byte aligned (never produced by the allocator; kept
 // so every pointer is accepted): scalar loads, same slots and finish.
 template <int R>
 __global__ __launch_bounds__(kBlock) void reduce_scalar_k(const float *__restrict__ x, int64_t n,
-                                                          int64_t chunk,
-                                                          uint64_t *__restrict__ slots,
+                                                          int64_t chunk, slot_ctl sc,
                                                           float *__restrict__ out) {
   using T = typename racc<R>::T;
   const int64_t c0 = int64_t(blockIdx.x) * chunk;
@@ -194,10 +199,10 @@ __global__ __launch_bounds__(kBlock) void reduce_scalar_k(const float *__restric
   const T b = block_merge<R>(acc);
   const int G = gridDim.x;
   if (blockIdx.x != G - 1) {
-    if (threadIdx.x == 0) slot_publish(slots + blockIdx.x, racc<R>::pack(b));
+    if (threadIdx.x == 0) slot_publish(sc.slots + blockIdx.x, racc<R>::pack(b));
     return;
   }
-  finish_full<R>(b, slots, G, out);
+  finish_full<R>(b, sc, G, out);
 }
 
 template <int R>
@@ -206,6 +211,7 @@ int launch_reduce(const float *x, int64_t n, float *out) {
   SILGPU_REQUIRE(n > 0 || R == R_SUM, "reduce: min/max of an empty array");
   SILGPU_REQUIRE(out != nullptr && (n == 0 || x != nullptr), "reduce: null pointer");
   SILGPU_CTX(c);
+  if (int rc = check_device_failure(c, false)) return rc;
   if (n == 0) return silgpu_fill_u32(out, 0u, 1);  // sum of nothing: +0.0f
   int64_t blocks;
   static_assert(kFullBlocks <= kSlots, "a full reduction's partials need a slot each");
@@ -215,7 +221,7 @@ int launch_reduce(const float *x, int64_t n, float *out) {
     int64_t chunk = cdiv(n, blocks);
     blocks = cdiv(n, chunk);
     reduce_scalar_k<R><<<static_cast<unsigned>(blocks), kBlock, 0, c->stream>>>(
-        x, n, chunk, c->slots, out);
+        x, n, chunk, slot_control(c), out);
     SILGPU_LAUNCH_CHECK("reduce_scalar_k");
   } else {
     int head = static_cast<int>(((16 - (reinterpret_cast<uintptr_t>(x) & 15)) & 15) / 4);
@@ -228,7 +234,7 @@ int launch_reduce(const float *x, int64_t n, float *out) {
     blocks = n4 > 0 ? cdiv(n4, chunk4) : 1;
     reduce_k<R><<<static_cast<unsigned>(blocks), kBlock, 0, c->stream>>>(
         x, head, reinterpret_cast<const float4 *>(x + head), n4, chunk4, x + head + 4 * n4,
-        tail, c->slots, out);
+        tail, slot_control(c), out);
     SILGPU_LAUNCH_CHECK("reduce_k");
   }
   return SILGPU_OK;
@@ -404,8 +410,7 @@ __device__ __forceinline__ vi unpack_vi(uint64_t b) {
 // the dispatcher starts after the row's other chunks, merges them in chunk
 // order and writes out[r].
 __global__ __launch_bounds__(kBlock) void argmax_k(const float *__restrict__ x, int64_t cols,
-                                                   int64_t chunk, bool vec,
-                                                   uint64_t *__restrict__ slots,
+                                                   int64_t chunk, bool vec, slot_ctl sc,
                                                    int32_t *__restrict__ out) {
   const int64_t r = blockIdx.y;
   const float *row = x + r * cols;
@@ -476,13 +481,14 @@ __global__ __launch_bounds__(kBlock) void argmax_k(const float *__restrict__ x, 
     if (threadIdx.x == 0) out[r] = b.i == kNoIndex ? 0 : b.i;
     return;
   }
-  uint64_t *row_slots = slots + r * chunks;
+  uint64_t *row_slots = sc.slots + r * chunks;
   if (blockIdx.x != chunks - 1) {
     if (threadIdx.x == 0) slot_publish(row_slots + blockIdx.x, pack_vi(b));
     return;
   }
   // The row's finish, in chunk order (thread t takes chunks t, t + kBlock, ...).
   vi f{NAN, kNoIndex};
+  uint64_t deadline = 0;
   for (int64_t j0 = threadIdx.x; j0 < chunks; j0 += kFinishLoads * kBlock) {
     uint64_t seen[kFinishLoads];
 #pragma unroll
@@ -494,8 +500,12 @@ __global__ __launch_bounds__(kBlock) void argmax_k(const float *__restrict__ x, 
     for (int g = 0; g < kFinishLoads; ++g) {
       const int64_t j = j0 + g * kBlock;
       vi v{NAN, kNoIndex};
-      if (j < chunks - 1) v = unpack_vi(slot_take(row_slots + j, seen[g]));
-      else if (j == chunks - 1) v = b;
+      uint64_t bits;
+      if (j < chunks - 1) {
+        if (slot_take(row_slots + j, seen[g], deadline, sc, bits)) v = unpack_vi(bits);
+      } else if (j == chunks - 1) {
+        v = b;
+      }
       f = better(f, v);
     }
   }
@@ -535,6 +545,32 @@ int64_t chunk_len(int64_t rows, int64_t cols, size_t partial_bytes, int64_t &chu
   int64_t chunk = cdiv(cdiv(cols, chunks), group) * group;
   chunks = cdiv(cols, chunk);
   return chunk;
+}
+
+// Test hook for the bounded slot wait: workgroup 1 finishes over slots
+// [0, nslots) that no producer of this launch writes, so every wait ends at
+// its deadline; workgroup 0, when late_ticks > 0, publishes slot 0 once
+// late_ticks have passed (a producer later than the finisher's deadline),
+// which leaves a stale value behind for the host's clean-up to remove.
+// Every wait in it is bounded by the wall clock.
+__global__ __launch_bounds__(kBlock) void slot_wait_selftest_k(slot_ctl sc, int nslots,
+                                                               uint64_t late_ticks,
+                                                               uint32_t *__restrict__ taken) {
+  if (blockIdx.x == 0) {
+    if (late_ticks > 0 && threadIdx.x == 0) {
+      const uint64_t until = wall_clock64() + late_ticks;
+      while (wall_clock64() < until) __builtin_amdgcn_s_sleep(127);
+      slot_publish(sc.slots, 0x5117ull);
+    }
+    return;
+  }
+  uint64_t deadline = 0;
+  uint32_t n = 0;
+  for (int j = threadIdx.x; j < nslots; j += kBlock) {
+    uint64_t bits;
+    if (slot_take(sc.slots + j, slot_peek(sc.slots + j), deadline, sc, bits)) ++n;
+  }
+  if (n) atomicAdd(taken, n);
 }
 
 }  // namespace
@@ -630,6 +666,7 @@ int silgpu_argmax_rows_f32(const float *d_in, int64_t rows, int64_t cols, int32_
   SILGPU_REQUIRE(cols <= INT32_MAX, "silgpu_argmax_rows_f32: cols %lld exceed int32",
                  (long long)cols);
   SILGPU_CTX(c);
+  if (int rc = check_device_failure(c, false)) return rc;
   if (cols == 0) return silgpu_fill_u32(d_out, 0u, rows);
   SILGPU_REQUIRE(d_in != nullptr, "silgpu_argmax_rows_f32: d_in is null");
   if (cols <= 2048) {
@@ -653,8 +690,41 @@ int silgpu_argmax_rows_f32(const float *d_in, int64_t rows, int64_t cols, int32_
     return set_error(SILGPU_ERR_INVALID, "silgpu_argmax_rows_f32: %lld x %lld partials exceed "
                      "the %d slots", (long long)rows, (long long)chunks, kSlots);
   dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(rows));
-  argmax_k<<<grid, kBlock, 0, c->stream>>>(d_in, cols, chunk, vec, c->slots, d_out);
+  argmax_k<<<grid, kBlock, 0, c->stream>>>(d_in, cols, chunk, vec, slot_control(c), d_out);
   SILGPU_LAUNCH_CHECK("argmax_k");
+  return SILGPU_OK;
+}
+
+int silgpu_slot_wait_selftest(int nslots, int64_t wait_us, int64_t late_us,
+                              uint32_t *d_taken) {
+  SILGPU_REQUIRE(nslots >= 1 && nslots <= kSlots,
+                 "silgpu_slot_wait_selftest: nslots %d outside [1, %d]", nslots, kSlots);
+  SILGPU_REQUIRE(wait_us >= 1 && wait_us <= 1000000,
+                 "silgpu_slot_wait_selftest: wait_us %lld outside [1, 1e6]", (long long)wait_us);
+  SILGPU_REQUIRE(late_us >= 0 && late_us <= 2000000,
+                 "silgpu_slot_wait_selftest: late_us %lld outside [0, 2e6]", (long long)late_us);
+  SILGPU_REQUIRE(d_taken != nullptr, "silgpu_slot_wait_selftest: d_taken is null");
+  SILGPU_CTX(c);
+  if (int rc = check_device_failure(c, false)) return rc;
+  slot_ctl sc = slot_control(c);
+  sc.wait_ticks = uint64_t(wait_us) * c->wall_ticks_per_us;
+  slot_wait_selftest_k<<<2, kBlock, 0, c->stream>>>(sc, nslots,
+                                                    uint64_t(late_us) * c->wall_ticks_per_us,
+                                                    d_taken);
+  SILGPU_LAUNCH_CHECK("slot_wait_selftest_k");
+  return SILGPU_OK;
+}
+
+int silgpu_slots_in_use(int64_t *count) {
+  SILGPU_REQUIRE(count != nullptr, "silgpu_slots_in_use: count is null");
+  SILGPU_CTX(c);
+  SILGPU_HIP_CHECK(hipStreamSynchronize(c->stream));
+  std::vector<uint64_t> h(kSlots);
+  SILGPU_HIP_CHECK(hipMemcpy(h.data(), c->slots, kSlots * sizeof(uint64_t),
+                             hipMemcpyDeviceToHost));
+  int64_t n = 0;
+  for (uint64_t v : h) n += v != 0;
+  *count = n;
   return SILGPU_OK;
 }
 

@@ -60,6 +60,19 @@ int init_locked() {
   SILGPU_HIP_CHECK(hipMalloc(&g_ctx.partials, kPartialBytes));
   SILGPU_HIP_CHECK(hipMalloc(&g_ctx.slots, kSlots * sizeof(uint64_t)));
   SILGPU_HIP_CHECK(hipMemsetAsync(g_ctx.slots, 0, kSlots * sizeof(uint64_t), g_ctx.stream));
+  // The failure word: pinned, coherent host memory, so the host reads what a
+  // kernel stored without a copy (a plain load after the stream has synchronised).
+  void *fw = nullptr;
+  SILGPU_HIP_CHECK(hipHostMalloc(&fw, sizeof(uint32_t), hipHostMallocCoherent | hipHostMallocMapped));
+  g_ctx.fail_host = static_cast<uint32_t *>(fw);
+  __atomic_store_n(g_ctx.fail_host, 0u, __ATOMIC_RELEASE);
+  void *fwd = nullptr;
+  SILGPU_HIP_CHECK(hipHostGetDevicePointer(&fwd, fw, 0));
+  g_ctx.fail_dev = static_cast<uint32_t *>(fwd);
+  int wall_khz = 0;
+  SILGPU_HIP_CHECK(hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, 0));
+  SILGPU_REQUIRE(wall_khz >= 1000, "init: wall clock rate of %d kHz", wall_khz);
+  g_ctx.wall_ticks_per_us = uint64_t(wall_khz) / 1000;
   // With device 0 current: this device's copy of the no-allocation scratch.
   void *sp = nullptr;
   SILGPU_HIP_CHECK(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)));
@@ -172,6 +185,28 @@ context *ctx() {
   return &g_ctx;
 }
 
+int check_device_failure(context *c, bool idle) {
+  const uint32_t f = __atomic_load_n(c->fail_host, __ATOMIC_ACQUIRE);
+  if (f == 0) return SILGPU_OK;
+  __atomic_store_n(c->fail_host, 0u, __ATOMIC_RELEASE);
+  // Zero every slot after the launches issued so far, so a producer that
+  // published after its finisher gave up leaves nothing for the next launch.
+  int rc = silgpu_fill_u32(c->slots, 0u, int64_t(kSlots) * 2);
+  if (rc == SILGPU_OK && idle) {
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess)
+      return set_error(SILGPU_ERR_HIP, "hipStreamSynchronize after a reduction failure: %s",
+                       hipGetErrorString(e));
+  }
+  if (rc != SILGPU_OK) return rc;
+  return set_error(SILGPU_ERR_HIP,
+                   "a one-launch reduction (sum/min/max/argmax) gave up waiting for a "
+                   "workgroup's partial result (failure code %u; the library waits up to %lld us "
+                   "before giving up); that result is wrong. The slots have been cleared for "
+                   "later calls.",
+                   f, (long long)kSlotWaitUs);
+}
+
 context *ctx_if_ready() {
   if (g_ready.load(std::memory_order_acquire)) return &g_ctx;
   set_error(SILGPU_ERR_INVALID, "the library is not initialised: call silgpu_init() first");
@@ -194,7 +229,7 @@ int silgpu_init(void) {
 int silgpu_sync(void) {
   SILGPU_CTX(c);
   SILGPU_HIP_CHECK(hipStreamSynchronize(c->stream));
-  return SILGPU_OK;
+  return check_device_failure(c, true);
 }
 
 int silgpu_device_info(int *cu_count, int *clock_khz, int *lds_bytes, char *arch,
