@@ -13,7 +13,9 @@ from pathlib import Path
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB_PATH = HERE / "liboracle.so"
+# oracle/cpubase.py loads this file a second time with LIB_OVERRIDE set to one
+# of the -O3 builds of the same C source (the CPU baseline).
+LIB_PATH = Path(globals().get("LIB_OVERRIDE", HERE / "liboracle.so"))
 
 
 def build() -> Path:
@@ -21,7 +23,7 @@ def build() -> Path:
     return LIB_PATH
 
 
-if not LIB_PATH.exists():
+if not LIB_PATH.exists() and "LIB_OVERRIDE" not in globals():
     build()
 
 _lib = C.CDLL(str(LIB_PATH))
@@ -153,6 +155,13 @@ def affine(x, scale, offset):
     out = np.empty_like(x)
     _lib.oracle_affine(_p(x), _p(out), x.size, scale, offset)
     return out
+
+
+def affine_into(x, out, scale, offset):
+    """out[i] = fmaf(x[i], scale, offset) into an existing array."""
+    assert x.dtype == np.float32 and out.dtype == np.float32 and x.size == out.size
+    assert x.flags.c_contiguous and out.flags.c_contiguous
+    _lib.oracle_affine(_p(x), _p(out), x.size, scale, offset)
 
 
 def affine_chain(x, scales, offsets):
