@@ -141,21 +141,30 @@ struct encoder {
   //   h = LN1(x); [q k v] = split(h Wqkv + bqkv) into H heads of D/H
   //   attn = softmax(q k^T / sqrt(D/H)) v; r1 = x + merge(attn) Wo + bo
   //   out = r1 + relu(LN2(r1) W1 + c1) W2 + c2
-  array<float> build() const {
+  // stages() keeps the intermediate arrays (for per-stage parity checks);
+  // build() drops them, so only `out` holds the graph.
+  struct stages_t {
+    array<float> h, qkv, merged, r1, h2, ff, out;
+  };
+  stages_t stages() const {
     const size_t dh = D / H;
     const float scale = 1.0f / std::sqrt(float(dh));
-    auto h = x.layer_norm(g1, b1);
-    auto qkv = h.linear(Wqkv, bqkv);                                   // [B*S, 3D]
-    auto heads = qkv.view({B, S, 3, H, dh}).permute({2, 0, 3, 1, 4});  // [3, B, H, S, dh]
+    stages_t st;
+    st.h = x.layer_norm(g1, b1);
+    st.qkv = st.h.linear(Wqkv, bqkv);                                     // [B*S, 3D]
+    auto heads = st.qkv.view({B, S, 3, H, dh}).permute({2, 0, 3, 1, 4});  // [3, B, H, S, dh]
     auto q = heads.select(0, 0), k = heads.select(0, 1), v = heads.select(0, 2);
-    auto scores = q.batched_dot(k.permute({0, 1, 3, 2})) * scale;      // [B, H, S, S]
+    auto scores = q.batched_dot(k.permute({0, 1, 3, 2})) * scale;         // [B, H, S, S]
     auto attn = scores.view({B * H * S, S}).softmax().view({B, H, S, S});
-    auto ctx = attn.batched_dot(v);                                    // [B, H, S, dh]
-    auto merged = ctx.permute({0, 2, 1, 3}).view({B * S, D});
-    auto r1 = x + merged.linear(Wo, bo);
-    auto ff = r1.layer_norm(g2, b2).linear(W1, c1).relu();
-    return r1 + ff.linear(W2, c2);
+    auto ctx = attn.batched_dot(v);                                       // [B, H, S, dh]
+    st.merged = ctx.permute({0, 2, 1, 3}).view({B * S, D});
+    st.r1 = x + st.merged.linear(Wo, bo);
+    st.h2 = st.r1.layer_norm(g2, b2);
+    st.ff = st.h2.linear(W1, c1).relu();
+    st.out = st.r1 + st.ff.linear(W2, c2);
+    return st;
   }
+  array<float> build() const { return stages().out; }
 
   double gemm_flops() const {
     const double M = double(B * S);
@@ -600,6 +609,18 @@ int main(int argc, char **argv) {
         const std::string dir = has_dims && argc > 7 ? argv[7] : ".";
         auto out = e.build();
         eval(out);
+        // The same block with its intermediates held and evaluated in one
+        // eval, so each stage can be checked against float64 computed from
+        // this run's own fp32 inputs to that stage.
+        auto st = e.stages();
+        eval(st.out, st.h, st.qkv, st.merged, st.r1, st.h2, st.ff);
+        write_raw(dir + "/h.bin", st.h);
+        write_raw(dir + "/qkv.bin", st.qkv);
+        write_raw(dir + "/merged.bin", st.merged);
+        write_raw(dir + "/r1.bin", st.r1);
+        write_raw(dir + "/h2.bin", st.h2);
+        write_raw(dir + "/ff.bin", st.ff);
+        write_raw(dir + "/out_staged.bin", st.out);
         write_raw(dir + "/x.bin", e.x);
         write_raw(dir + "/Wqkv.bin", e.Wqkv);
         write_raw(dir + "/bqkv.bin", e.bqkv);
