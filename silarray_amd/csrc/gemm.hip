@@ -786,7 +786,8 @@ __global__ __launch_bounds__(kSkWaves *kWave) void sgemm_skinny_k(gemm_args p) {
 // parity of lane bits 2-4) over 64 banks, as measured with the bank-conflict
 // counter; the swizzle and pitches make every read conflict-free under that
 // model (tests/test_gemm_layout.py).  256 x 256: 8 waves (2 x 4) of 128 x 64;
-// 128 x 128: 4 waves (2 x 2) of 64 x 64; 128 x 64: 4 waves of 64 x 32.  The
+// 128 x 128: 4 waves (2 x 2) of 64 x 64; 128 x 64: 4 waves of 64 x 32, or 8
+// of 64 x 16 for launches of at most one workgroup per CU.  The
 // next K tile's loads are issued before the current tile is multiplied, and
 // one s_waitcnt + barrier ends each tile.  256 x 128 tiles run three 16-deep
 // stages (75 KB of LDS, two workgroups per CU), so each barrier waits only
@@ -811,7 +812,7 @@ constexpr int dtl_pitch() {
 // BM x BN tiles, NW waves in a 2 x NW/2 grid: 256 x 128 with 4 waves of 128
 // x 64 (two workgroups per CU, so two waves per SIMD), 256 x 256 with 8
 // waves of 128 x 64 (one workgroup per CU); 128 x 128 with 4 waves of 64 x
-// 64; 128 x 64 with 4 waves of 64 x 32.
+// 64; 128 x 64 with 4 waves of 64 x 32 or (BK = 32) 8 waves of 64 x 16.
 template <int BM, int BN, int BK, int NW = (BM == 256 ? 8 : 4), int NS = 2>
 struct dtl_cfg {
   static constexpr int WM = 2, WN = NW / 2;
@@ -1558,7 +1559,22 @@ int launch_tb(const gemm_args &a, int64_t batch, int splits, bool vec, hipStream
       } else if constexpr (BN == 128) {
         return launch_dtl<BM, BN, kDtlBK, 4, 2, TA, TB>(a, batch, splits, s);
       } else {
-        if (a.K % 32 == 0) return launch_dtl<BM, BN, 32, 4, 2, TA, TB>(a, batch, splits, s);
+        if (a.K % 32 == 0) {
+          // A launch of at most one workgroup per CU runs the tile on 8
+          // waves of 64 x 16 (two per SIMD, so each hides the other's
+          // fragment and barrier waits); with more workgroups per CU the
+          // 4 waves of 64 x 32 read fewer fragments per MFMA and win.
+          // MI355X, µs, 4 waves against 8: 1024^3 (2 K splits, 256
+          // workgroups) 24.9 / 24.1, 640x2560x640 27.5 / 24.6,
+          // 256x1024x4096 24.7 / 23.9; 2048x768x768 (4 splits, 768
+          // workgroups) 30.4 / 33.4, 2048x3072x768 76.5 / 81.4.
+          const int64_t klen = cdiv(cdiv(a.K, splits), 32) * 32;
+          const int64_t wgs = int64_t(a.M / BM) * (a.N / BN) * batch * cdiv(a.K, klen);
+          const context *c = ctx();
+          if (c && wgs <= c->cu_count)
+            return launch_dtl<BM, BN, 32, 8, 2, TA, TB>(a, batch, splits, s);
+          return launch_dtl<BM, BN, 32, 4, 2, TA, TB>(a, batch, splits, s);
+        }
         return launch_dtl<BM, BN, kDtlBK, 4, 2, TA, TB>(a, batch, splits, s);
       }
     }
