@@ -1743,10 +1743,16 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dtl_ok) {
   // -> LDS round trip that nothing else hides when a CU holds few
   // workgroups: the floor of small products).  Split-K adds the partial-sum
   // pass: a launch, (splits + 1) M x N fp32 passes and a per-plane latency.
-  // Fitted on MI355X to full tile x split sweeps of 42 shapes (30 the
-  // LDS-direct kernel takes, from 64 x 768 x 2048 to 4096^3, and 12 ragged
-  // ones): the plan costs on average 0.2% (aligned; at most 2.2%) and 2.3%
-  // (ragged) more than the best fixed plan.
+  // A 128x64 launch of at most one workgroup per CU runs 8 waves (two per
+  // SIMD, launch_tb), at kEff8 of the 4-wave tile's rate.  Fitted on MI355X
+  // to full tile x split sweeps (splits 1, 2, 3, 4, 6, 8, 16) of 46 shapes
+  // from 64 x 768 x 2048 to 2048 x 2304 x 768, aligned and ragged, with the
+  // picks of the large squares (2048^3 .. 8192^3) held: the plan costs 1.5%
+  // more than the best fixed plan (geometric mean; before the 3- and 6-way
+  // splits and the 8-wave tile were modelled, 2.1%).  Against the previous
+  // plans, 51 shapes: 0.57% faster in the geometric mean, 2048x768x768
+  // 30.0 -> 28.3 us, 768^3 20.0 -> 17.6, 512x1024x4096 41.2 -> 39.6, and
+  // one shape slower, 100x5000x5000 70.3 -> 74.7.
   struct cand {
     int tile, bm, bn, bk, waves, occupancy;
     double eff, lat;
@@ -1759,17 +1765,18 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dtl_ok) {
   const cand cands[] = {{TILE_256x256, 256, 256, 16, 8, 1, 0.87, 1.15e-6},
                         {TILE_128x128, 128, 128, 16, 4, 3, dtl128 ? 0.81 : 0.70, 1.25e-6},
                         {TILE_128x64, 128, 64, 16, 4, dtl64 ? 3 : 5, dtl64 ? 0.86 : 0.71, 0.57e-6},
-                        {TILE_64x64, 64, 64, 16, 4, 8, 0.64, 0.52e-6}};
-  constexpr double kK0 = 48.0, kSingleWave = 0.85, kLaunch = 4.0e-6;
+                        {TILE_64x64, 64, 64, 16, 4, 8, 0.64, 0.442e-6}};
+  constexpr double kK0 = 48.0, kSingleWave = 0.8755, kLaunch = 4.0e-6, kEff8 = 0.909;
   const double rate_cu = 157.3e12 / 256.0;
   auto round_time = [&](const cand &cd, int64_t nwg, double klen) {
     const int64_t per_cu = cdiv(nwg, 256);
     const int64_t conc = per_cu < cd.occupancy ? per_cu : cd.occupancy;
-    const double per_simd = double(conc) * cd.waves / 4.0;
+    const bool w8 = cd.tile == TILE_128x64 && dtl64 && K % 32 == 0 && nwg <= 256;
+    const double per_simd = double(conc) * (w8 ? 8 : cd.waves) / 4.0;
     const double f = per_simd >= 2.0 ? 1.0 : per_simd >= 1.0 ? kSingleWave
                                                               : kSingleWave * per_simd;
     const double t = double(per_cu) * 2.0 * cd.bm * cd.bn * klen /
-                     (rate_cu * cd.eff * f * (klen / (klen + kK0)));
+                     (rate_cu * cd.eff * (w8 ? kEff8 : 1.0) * f * (klen / (klen + kK0)));
     const double floor_t = double(cdiv(per_cu, conc)) * (klen / 16.0) * cd.lat;
     return t > floor_t ? t : floor_t;
   };
@@ -1779,8 +1786,12 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dtl_ok) {
   plan best{TILE_128x128, 1};
   double best_t = 1e30;
   for (const cand &cd : cands) {
-    for (int sp : {1, 2, 4, 8, 16}) {
+    for (int sp : {1, 2, 3, 4, 6, 8, 16}) {
       if (sp > 1 && (batch != 1 || K / sp < 64)) continue;
+      // 3- and 6-way splits only for the two smaller tiles: for the larger
+      // ones they won nowhere in the sweeps and moved 3000^3 to a plan 7%
+      // slower.
+      if ((sp == 3 || sp == 6) && (cd.tile == TILE_256x256 || cd.tile == TILE_128x128)) continue;
       const int64_t wg = tiles(cd.bm, cd.bn) * sp;
       const double klen = double(cdiv(cdiv(K, sp), cd.bk) * cd.bk);
       double t = round_time(cd, wg, klen);
