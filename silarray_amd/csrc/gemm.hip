@@ -928,6 +928,10 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
 }
 
+// Third word of a raw buffer resource descriptor: 32-bit data format, no
+// swizzle.
+constexpr int kRawRsrcWord3 = 0x00020000;
+
 // Sixteen bytes of zeros in device memory: the source of the LDS-direct
 // loads of convolution taps that fall into the padding.  Never written.
 __device__ __attribute__((aligned(16))) float conv_zero_page[4];
@@ -1198,18 +1202,23 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU,
     }
   }
   if (gridDim.y > 1) {
-    float *W = p.ws + int64_t(blockIdx.y) * M * N;
+    // The raw accumulators to plane y through a buffer descriptor based at
+    // this tile: one 32-bit lane offset, each store's row and column step in
+    // the scalar offset (the host splits K here only where BM * N * 4 <
+    // 2^30).  Against per-element 64-bit addresses this measured 1.3-3.6%
+    // faster on products that do not split, from the block layout the
+    // compiler then gives the K loop (2048^3 132.9 -> 128.4 us).
+    const __amdgpu_buffer_rsrc_t w = __builtin_amdgcn_make_buffer_rsrc(
+        p.ws + int64_t(blockIdx.y) * M * N + int64_t(m0) * N + n0, 0, 0x7fffffff, kRawRsrcWord3);
+    const int lane_b = ((wm * TM * 16 + F::row(lane, 0)) * N + wn * TN * 16 + lm) * 4;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int r = 0; r < F::R; ++r) {
-        const int row = m0 + wm * TM * 16 + i * 16 + F::row(lane, r);
+      for (int r = 0; r < F::R; ++r)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          W[int64_t(row) * N + n0 + wn * TN * 16 + j * 16 + lm] = acc[i][j][r];
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][r]), w, lane_b,
+                                                ((i * 16 + r) * N + j * 16) * 4, 0);
     return;
   }
   // The epilogue's bias values (one per column block) and residual values
@@ -1529,6 +1538,8 @@ int launch_dtl(const gemm_args &a, int64_t batch, int splits, hipStream_t s) {
   gemm_args g = a;
   g.tiles_m = static_cast<int>(a.M / BM);
   g.tiles_n = static_cast<int>(a.N / BN);
+  // The split planes are stored with 32-bit offsets within a tile's rows.
+  if (int64_t(BM) * a.N * 4 >= (int64_t(1) << 30)) splits = 1;
   g.klen = static_cast<int>(cdiv(cdiv(a.K, splits), BK) * BK);
   if (g.klen < BK) g.klen = BK;
   splits = static_cast<int>(a.K > 0 ? cdiv(a.K, g.klen) : 1);
@@ -2028,6 +2039,9 @@ int launch_conv_dtl(const gemm_args &a, int splits, hipStream_t s) {
   g.tiles_m = a.M / 128;
   g.tiles_n = a.N / 64;
   g.klen = a.K / splits;
+  SILGPU_REQUIRE(splits == 1 || int64_t(128) * a.N * 4 < (int64_t(1) << 30),
+                 "conv2d: %lld output channels are too many for a K split",
+                 static_cast<long long>(a.N));
   dim3 grid(static_cast<unsigned>(int64_t(g.tiles_m) * g.tiles_n), static_cast<unsigned>(splits),
             1u);
   kern<<<grid, D::kThreads, 0, s>>>(g);
