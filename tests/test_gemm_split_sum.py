@@ -131,3 +131,24 @@ def test_split_products_repeat_bit_identically(native):
     again = run(1024, 1024, 1024, 4, 3)
     assert not np.isnan(first).any()
     assert np.array_equal(first, again)
+
+
+def test_split_dropped_where_tile_rows_exceed_32_bit_offsets(native):
+    # 128 x 2^21 x 32 forced to two K splits: a 128-row tile of a split plane
+    # spans 128 * N * 4 = 2^30 bytes, beyond the kernel's 32-bit plane
+    # offsets, so the product runs unsplit (and correct)
+    M, N, K = 128, 1 << 21, 32
+    announce(f"split guard {M}x{N}x{K}")
+    g = rng(23)
+    A = g.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = g.uniform(-1, 1, (K, N)).astype(np.float32)
+    dA, dB, dC = up(native, A), up(native, B), _nan_buffer(native, M * N)
+    native.sgemm_tuned(0, 0, M, N, K, dA, K, 0, dB, N, 0, dC, N, 0, tile=TILE_128x64, splits=2)
+    assert native.last_plan() == [(TILE_128x64, 1, M)], native.last_plan()
+    C = down(native, dC, (M, N))
+    cols = np.concatenate([np.arange(0, 64), g.integers(0, N, 256), np.arange(N - 64, N)])
+    want = A.astype(np.float64) @ B[:, cols].astype(np.float64)
+    err = np.abs(C[:, cols] - want)
+    bar = 1e-5 * np.sqrt(K) * (np.abs(A).astype(np.float64) @ np.abs(B[:, cols]).astype(np.float64))
+    assert not np.isnan(C).any()
+    assert np.all(err <= bar), float(np.max(err / bar))
