@@ -152,3 +152,39 @@ def test_split_dropped_where_tile_rows_exceed_32_bit_offsets(native):
     bar = 1e-5 * np.sqrt(K) * (np.abs(A).astype(np.float64) @ np.abs(B[:, cols]).astype(np.float64))
     assert not np.isnan(C).any()
     assert np.all(err <= bar), float(np.max(err / bar))
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K,splits", [(1024, 1024, 1024, 2), (2048, 768, 768, 4)])
+def test_split_sum_with_transposed_operands(native, ta, tb, M, N, K, splits):
+    # the same bar for the NT, TN and TT instantiations of the kernel: A
+    # stored [K, M] when transposed, B stored [N, K]
+    announce(f"split sum ta={ta} tb={tb} {M}x{N}x{K} splits={splits}")
+    g = rng(M + N + K + 10 * ta + tb)
+    A = g.normal(0, 1, (M, K)).astype(np.float32)
+    B = g.normal(0, 1, (K, N)).astype(np.float32)
+    As = np.ascontiguousarray(A.T) if ta else A
+    Bs = np.ascontiguousarray(B.T) if tb else B
+    lda, ldb = (M if ta else K), (K if tb else N)
+    dA, dB, dC = up(native, As), up(native, Bs), _nan_buffer(native, M * N)
+    native.sgemm_tuned(ta, tb, M, N, K, dA, lda, 0, dB, ldb, 0, dC, N, 0, tile=TILE_128x64,
+                       splits=splits)
+    ranges = _ranges(K, splits)
+    assert native.last_plan() == [(TILE_128x64, len(ranges), M)], native.last_plan()
+    C = down(native, dC, (M, N))
+    # each plane: the same transposed product over its K range alone
+    planes = []
+    for ks, ke in ranges:
+        Ap = np.ascontiguousarray(A[:, ks:ke].T) if ta else np.ascontiguousarray(A[:, ks:ke])
+        Bp = np.ascontiguousarray(B[ks:ke].T) if tb else np.ascontiguousarray(B[ks:ke])
+        Kp = ke - ks
+        pA, pB, pC = up(native, Ap), up(native, Bp), _nan_buffer(native, M * N)
+        native.sgemm_tuned(ta, tb, M, N, Kp, pA, (M if ta else Kp), 0, pB, (Kp if tb else N), 0,
+                           pC, N, 0, tile=TILE_128x64, splits=1)
+        assert native.last_plan() == [(TILE_128x64, 1, M)], native.last_plan()
+        planes.append(down(native, pC, (M, N)))
+    want = np.zeros((M, N), np.float32)
+    for x in planes:
+        want = want + x
+    assert not np.isnan(C).any()
+    assert np.array_equal(C, want), float(np.max(np.abs(C - want)))
