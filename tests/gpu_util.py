@@ -37,6 +37,18 @@ def gemm_tolerance_ok(C, C64, Cabs, K):
     return normwise <= tol and elem_ok, normwise, float(np.max(diff / (Cabs + 1e-30)))
 
 
+def sigmoid_bound(C64, Cabs, K):
+    """Reference and per-element bound (in gemm_tolerance_ok's units) after a
+    sigmoid epilogue.  sigmoid is 1/4-Lipschitz, so the pre-activation bound
+    carries over as Cabs / 4; the fp32 sigmoid itself (exp, add, divide)
+    adds up to about 3 ulp of its result y, allowed as 4 * 2^-24 * y.
+    Without that term a short K (K = 2: a bar below 1 ulp of y) would hold
+    the sigmoid to more than fp32 can give."""
+    y = 1 / (1 + np.exp(-C64))
+    tol = 1e-5 * math.sqrt(max(K, 1))
+    return y, Cabs / 4 + 4 * 2.0 ** -24 * y / tol
+
+
 def ulp_diff(a, b):
     """Distance in float32 ulps (same-sign finite values)."""
     ai = np.asarray(a, np.float32).view(np.int32).astype(np.int64)

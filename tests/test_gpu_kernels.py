@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from conftest import rng
-from gpu_util import announce, down, empty, gemm_tolerance_ok, ulp_diff, up
+from gpu_util import announce, down, empty, gemm_tolerance_ok, sigmoid_bound, ulp_diff, up
 
 pytestmark = pytest.mark.gpu
 
@@ -596,9 +596,7 @@ def _gemm_case(native, oracle, M, N, K, ta=False, tb=False, epi=0, bias_len=0, s
         C64 = C64 + bb
         Cabs = Cabs + np.abs(bb)
     if epi == native.EPI_BIAS_SIGMOID:
-        # sigmoid is 1/4-Lipschitz: the pre-activation bound carries over
-        C64 = 1 / (1 + np.exp(-C64))
-        Cabs = Cabs / 4 + 1e-7
+        C64, Cabs = sigmoid_bound(C64, Cabs, K)
     if epi in (native.EPI_RELU, native.EPI_BIAS_RELU):
         C64 = np.maximum(C64, 0)
     return Cg, C64, Cabs
@@ -748,6 +746,28 @@ def test_linear_sigmoid_config(native, oracle):
     assert ok, (nw, el)
 
 
+@pytest.mark.parametrize("K", [1, 2, 3])
+def test_linear_sigmoid_short_k(native, oracle, K):
+    """K of 1-3 (B transposed, bias taken modulo 173): the propagated product
+    bound is then below one ulp of the sigmoid's output, so the bar rests on
+    the allowance for the fp32 sigmoid itself (sigmoid_bound)."""
+    M, N, bias_len = 1268, 279, 173
+    announce(f"linear_sigmoid {M}x{N}x{K} tb bias_len={bias_len}")
+    g = rng(900 + K)
+    A = g.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = g.uniform(-1, 1, (N, K)).astype(np.float32)
+    bias = g.normal(0, 1, bias_len).astype(np.float32)
+    dA, dB, dC, db = up(native, A), up(native, B), empty(native, M * N), up(native, bias)
+    native.sgemm(0, 1, M, N, K, dA, K, 0, dB, K, 0, dC, N, 0, 1, db, bias_len,
+                 native.EPI_BIAS_SIGMOID)
+    Cg = down(native, dC, (M, N))
+    C64, Cabs = oracle.sgemm_f64(A, B, tb=True, with_abs=True)
+    bb = bias[np.arange(N) % bias_len].astype(np.float64)
+    C64, Cabs = sigmoid_bound(C64 + bb, Cabs + np.abs(bb), K)
+    ok, nw, el = gemm_tolerance_ok(Cg, C64, Cabs, K)
+    assert ok, (nw, el)
+
+
 def test_small_batch_config(native, oracle):
     """configs[1](b): 32x4096 . 4096x768."""
     announce("sgemm 32x768x4096")
@@ -778,7 +798,7 @@ def test_sgemm_tuned_configs(native, oracle, tile, splits, M, N, K, ta, tb, epi)
     if bias_len:
         C64, Cabs = C64 + bias, Cabs + np.abs(bias)
     if epi == 2:
-        C64, Cabs = 1 / (1 + np.exp(-C64)), Cabs / 4 + 1e-7
+        C64, Cabs = sigmoid_bound(C64, Cabs, K)
     if epi in (3, 4):
         C64 = np.maximum(C64, 0)
     ok, nw, el = gemm_tolerance_ok(Cg, C64, Cabs, K)
@@ -829,7 +849,7 @@ def test_sgemm_small_m(native, oracle, tile, splits, M, N, K, tb, lpa, lpb, lpc,
     if bias_len:
         C64, Cabs = C64 + bias, Cabs + np.abs(bias)
     if epi == 2:
-        C64, Cabs = 1 / (1 + np.exp(-C64)), Cabs / 4 + 1e-7
+        C64, Cabs = sigmoid_bound(C64, Cabs, K)
     if epi in (3, 4):
         C64 = np.maximum(C64, 0)
     ok, nw, el = gemm_tolerance_ok(Cg, C64, Cabs, max(K, 1))

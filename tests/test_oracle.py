@@ -182,6 +182,19 @@ def test_sigmoid_vs_f64(oracle):
     assert np.max(np.abs(oracle.sigmoid(x) - ref) / ref) < 1e-6
 
 
+def test_sigmoid_bound_admits_fp32_sigmoid(oracle):
+    """The GPU tests' bar after a sigmoid epilogue (gpu_util.sigmoid_bound)
+    admits an fp32 sigmoid of an exact pre-activation at K = 1, where only
+    its allowance for the sigmoid's own rounding is left, and still rejects
+    a dropped bias of 0.02."""
+    from gpu_util import gemm_tolerance_ok, sigmoid_bound
+    x = rng(29).uniform(-12, 12, 100000).astype(np.float32)
+    y64, bound = sigmoid_bound(x.astype(np.float64), np.zeros(x.size), 1)
+    assert gemm_tolerance_ok(oracle.sigmoid(x), y64, bound, 1)[0]
+    y64b, bound_b = sigmoid_bound(x.astype(np.float64) + 0.02, np.full(x.size, 0.02), 1)
+    assert not gemm_tolerance_ok(oracle.sigmoid(x), y64b, bound_b, 1)[0]
+
+
 def test_bias_sigmoid_and_backward(oracle):
     g = rng(17)
     d = g.normal(0, 1, (6, 10)).astype(np.float32)
