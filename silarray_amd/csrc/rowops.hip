@@ -12,7 +12,9 @@
 // Numerics: softmax subtracts the row maximum and scales by the reciprocal
 // of an fp64-accumulated sum; layer_norm uses the two-pass form of cpu::layer_norm
 // (include/cpu.h:352-373): mean, then sum of squared deviations, then
-// 1/sqrtf(ss/cols + eps), then *gamma + beta.
+// 1/sqrtf(ss/cols + eps), then *gamma + beta; the sums are fp64 and each
+// deviation is taken from the fp64 mean (mean_split), not its float
+// rounding.
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
@@ -28,6 +30,20 @@ namespace {
 __device__ __forceinline__ float rescale(float m, float M) {
   return m == -INFINITY ? 0.0f : expf(m - M);
 }
+
+// The row mean as an unevaluated sum hi + lo of two floats (hi the fp64 mean
+// rounded to float, lo the rest), so a deviation x - mean is formed as
+// (x - hi) - lo: x - hi is exact wherever x lies within a factor of two of
+// the mean (Sterbenz), and the result then carries one float rounding of the
+// deviation itself.  Subtracting the float-rounded mean instead errs by up
+// to half an ulp of the mean, which for a row whose spread is small against
+// its mean (values 1000 +- 0.01) is most of the deviation.
+struct mean_split {
+  float hi, lo;
+  __device__ explicit mean_split(double m)
+      : hi(static_cast<float>(m)), lo(static_cast<float>(m - static_cast<double>(hi))) {}
+  __device__ float deviation(float x) const { return (x - hi) - lo; }
+};
 
 struct fmax_op {
   __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
@@ -257,14 +273,14 @@ __global__ __launch_bounds__(row_block<NT>()) void layer_norm_reg_k(
 #pragma unroll
     for (int j = 0; j < 4; ++j) s += static_cast<double>(x[k][j]);
   s = group<NT>::template reduce_once<0>(s, dsum_op{});
-  const float mu = static_cast<float>(s / static_cast<double>(cols));
+  const mean_split mu(s / static_cast<double>(cols));
   double ss = 0.0;
 #pragma unroll
   for (int k = 0; k < V; ++k)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       int64_t c = (int64_t(k) * NT + t) * 4 + j;
-      float d = x[k][j] - mu;
+      float d = mu.deviation(x[k][j]);
       x[k][j] = d;
       if (M == kFull || c < cols) ss += static_cast<double>(d) * static_cast<double>(d);
     }
@@ -297,7 +313,10 @@ __global__ __launch_bounds__(kLoopBlock) void softmax_loop_k(const float *__rest
     if (v > m) {
       s = s * static_cast<double>(expf(m - v)) + 1.0;
       m = v;
-    } else {
+    } else if (v != -INFINITY) {
+      // A -inf entry adds exp(-inf) = 0; skipped, so that one seen while m
+      // is still -inf does not add exp(-inf - -inf) = NaN.  NaN entries
+      // take this branch and make the row NaN.
       s += static_cast<double>(expf(v - m));
     }
   }
@@ -315,16 +334,16 @@ __global__ __launch_bounds__(kLoopBlock) void layer_norm_loop_k(
   double s = 0.0;
   for (int64_t c = threadIdx.x; c < cols; c += kLoopBlock) s += static_cast<double>(src[c]);
   s = group<kLoopBlock>::reduce(s, dsum_op{});
-  const float mu = static_cast<float>(s / static_cast<double>(cols));
+  const mean_split mu(s / static_cast<double>(cols));
   double ss = 0.0;
   for (int64_t c = threadIdx.x; c < cols; c += kLoopBlock) {
-    float d = src[c] - mu;
+    float d = mu.deviation(src[c]);
     ss += static_cast<double>(d) * static_cast<double>(d);
   }
   ss = group<kLoopBlock>::reduce(ss, dsum_op{});
   const float inv_std = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(cols)) + eps);
   for (int64_t c = threadIdx.x; c < cols; c += kLoopBlock)
-    dst[c] = ((src[c] - mu) * inv_std) * gamma[c] + beta[c];
+    dst[c] = (mu.deviation(src[c]) * inv_std) * gamma[c] + beta[c];
 }
 
 // ---- dispatch ---------------------------------------------------------------

@@ -516,6 +516,28 @@ def test_softmax_rows(native, oracle, rows, cols):
     assert np.all(np.abs(out - ref) <= 1e-5 * ref + 1e-30)
 
 
+@pytest.mark.parametrize("rows,cols", [(5, 20000), (3, 16387), (4, 8192), (6, 1000), (7, 2)])
+def test_softmax_neg_inf_entries(native, oracle, rows, cols):
+    """-inf entries (masked scores) add exp(-inf) = 0 to their row, also when
+    they are the first values a thread of the looped kernel (rows over 16384)
+    reads; a row of -inf only is NaN, as exp(-inf - max) is in float64."""
+    announce(f"softmax -inf entries {rows}x{cols}")
+    x = rng(1150 + cols).normal(0, 3, (rows, cols)).astype(np.float32)
+    x[0, : min(cols - 1, 300): 3] = -np.inf   # the first value of every third thread
+    x[1, -1] = -np.inf
+    x[2, :] = -np.inf
+    if rows > 3:
+        x[3, 1:] = -np.inf                  # one finite entry: probability 1
+    dx, do = up(native, x), empty(native, rows * cols)
+    native.softmax_rows_f32(dx, do, rows, cols)
+    out = down(native, do, (rows, cols)).astype(np.float64)
+    with np.errstate(invalid="ignore"):
+        ref = oracle.softmax_rows_f64(x)
+    assert np.all(np.isnan(out[2])) and np.all(np.isnan(ref[2]))
+    keep = [r for r in range(rows) if r != 2]
+    assert np.all(np.abs(out[keep] - ref[keep]) <= 1e-5 * ref[keep] + 1e-30)
+
+
 def test_softmax_golden(native, ref_vectors):
     announce("softmax golden")
     s = ref_vectors["softmax"]
@@ -561,6 +583,28 @@ def test_layer_norm_outlier_and_constant_rows(native, oracle, rows, cols):
     ref = oracle.layer_norm_f64(x, gamma, beta, 1e-5)
     assert np.all(np.abs(out - ref) <= 1e-5 * np.maximum(1.0, np.abs(ref)))
     assert np.array_equal(out[2], beta.astype(np.float64))
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 2), (33, 5), (17, 768), (9, 8192), (3, 50000)])
+def test_layer_norm_large_mean(native, oracle, rows, cols):
+    """Rows whose spread is small against their mean (1000 +- 0.01, -300 +-
+    0.001, 1e5 +- 0.5): each deviation is taken from the fp64 mean, so the
+    output keeps the relative 1e-5 bar; subtracting the float-rounded mean
+    would err by up to half an ulp of the mean (3e-5 at 1000) in every
+    deviation."""
+    announce(f"layer_norm large mean {rows}x{cols}")
+    g = rng(1400 + cols)
+    x = np.empty((rows, cols), np.float32)
+    for r in range(rows):
+        mean, spread = [(1000.0, 0.01), (-300.0, 1e-3), (1e5, 0.5)][r % 3]
+        x[r] = (mean + g.normal(0, spread, cols)).astype(np.float32)
+    gamma = g.uniform(0.5, 1.5, cols).astype(np.float32)
+    beta = g.uniform(-1, 1, cols).astype(np.float32)
+    dx, dg, db, do = up(native, x), up(native, gamma), up(native, beta), empty(native, rows * cols)
+    native.layer_norm_rows_f32(dx, do, dg, db, rows, cols, 1e-5)
+    out = down(native, do, (rows, cols)).astype(np.float64)
+    ref = oracle.layer_norm_f64(x, gamma, beta, 1e-5)
+    assert np.all(np.abs(out - ref) <= 1e-5 * np.maximum(1.0, np.abs(ref)))
 
 
 def test_layer_norm_golden(native, ref_vectors):
