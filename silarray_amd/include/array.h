@@ -360,11 +360,14 @@ class array {
       return tmp;
     }
     if (dimension() == 2) {
-      if (shape_[0] == 1 && is_contiguous_()) {
+      // {1, n} -> {n} for every row view, as the reference does; the vector
+      // keeps the row's element stride (a row of a transposed view is not
+      // contiguous; the reference's unit stride would read other elements).
+      if (shape_[0] == 1) {
         array tmp = *this;
         tmp.node_.reset();
         tmp.shape_ = {shape_[1]};
-        tmp.strides_ = {1};
+        tmp.strides_ = {strides_[1]};
         return tmp;
       }
       array tmp = *this;
@@ -991,8 +994,13 @@ inline array<T> array<T>::dot(const array &rhs) const {
                                          out_shape));
   } else {
     // Integer products on the host, as the reference (include/cpu.h:239-264).
+    // A vector operand as a one-row (left) or one-column (right) view.
     auto a = dimension() == 1 ? broadcast({1, shape_[0]}) : *this;
-    auto b = rhs.dimension() == 1 ? rhs.broadcast({1, rhs.shape_[0]}).transpose() : rhs;
+    auto b = rhs;
+    if (rhs.dimension() == 1) {
+      b.shape_ = {rhs.shape_[0], 1};
+      b.strides_ = {rhs.strides_[0], 1};
+    }
     const size_t M = a.shape_[0], K = a.shape_[1], N = b.shape_[1];
     array out(out_shape, T{});
     T *o = out.buffer_data();
@@ -2085,6 +2093,10 @@ inline void evaluate(const std::vector<node *> &roots) {
     for (int side = 0; side < 2; side++) {
       node *p = n->inputs[side].get(), *x = n->inputs[1 - side].get();
       node *c = alias.count(p) ? alias[p] : p;
+      // A product evaluated earlier (a view of it forced it, or an earlier
+      // eval) has released its inputs: nothing to fuse, and its operands
+      // must not be read.
+      if (c->evaluated) continue;
       const bool ok_op = (c->operation == op::dot && c->inputs[0]->shape.size() == 2 &&
                           c->inputs[1]->shape.size() == 2) ||
                          ((c->operation == op::linear || c->operation == op::linear_sigmoid) &&

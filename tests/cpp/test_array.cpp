@@ -86,6 +86,13 @@ HOST_CASE("transpose views") {
   auto tT = t.transpose();
   CHECK(tT.shape() == (shape_type{4, 2, 2}));
   CHECK(array_equal(tT.transpose(), t));
+  // A row of a transposed view is a {1, n} view that is not contiguous: its
+  // transpose is the vector {n} (as for any row) holding that row's elements.
+  auto row = mT.slice(2, 1);  // {{3, 7, 11}}, strides {1, 4}
+  CHECK(array_equal(row, {{3, 7, 11}}));
+  auto rowT = row.transpose();
+  CHECK(rowT.shape() == (shape_type{3}));
+  CHECK(array_equal(rowT, {3, 7, 11}));
 }
 
 HOST_CASE("broadcast view") {
@@ -413,6 +420,28 @@ TEST_CASE("arrays held outside the graph are materialised") {
   bool ok = true;
   for (size_t i = 0; i < 1000; i++) ok = ok && (y.at(i) == x.at(i) * 2.0f) && (z.at(i) == y.at(i) + 1.0f);
   CHECK(ok);
+}
+
+TEST_CASE("a product evaluated early, then added in a later eval") {
+  // A row view of a lazy product (slice) evaluates the product and frees
+  // its graph inputs; the add that consumes it afterwards must not try to
+  // fold it into the product's epilogue (that read the freed inputs).
+  auto x = array<float>({2, 3}, std::vector<float>{1, 2, 3, 4, 5, 6});
+  auto W = array<float>({3, 3}, std::vector<float>{1, 0, 0, 0, 1, 0, 0, 0, 1});
+  auto b = array<float>({3}, std::vector<float>{10, 20, 30});
+  auto lin = x.linear(W, b);
+  auto prod = x.dot(W);
+  auto first = lin.slice(0, 1);   // evaluates lin
+  auto firstp = prod.slice(1, 1); // evaluates prod
+  auto r1 = x + lin;
+  auto r2 = prod + x;
+  auto r3 = lin.relu() + 1.0f;
+  eval(r1, r2, r3);
+  CHECK(array_equal(first, {{11, 22, 33}}));
+  CHECK(array_equal(firstp, {{4, 5, 6}}));
+  CHECK(array_equal(r1, {{12, 24, 36}, {18, 30, 42}}));
+  CHECK(array_equal(r2, {{2, 4, 6}, {8, 10, 12}}));
+  CHECK(array_equal(r3, {{12, 23, 34}, {15, 26, 37}}));
 }
 
 TEST_CASE("eval of a root that another root consumes") {
