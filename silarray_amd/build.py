@@ -95,13 +95,19 @@ def build_cpp_tests() -> Path:
                 "$ORIGIN/../../silarray_amd")
 
 
+def build_cpp_random_graphs() -> Path:
+    """Compiles the random sil::eval graph test (tests/cpp/random_graphs.cpp)."""
+    return _cxx(CPP_TESTS / "random_graphs.cpp", CPP_TESTS / "random_graphs",
+                "$ORIGIN/../../silarray_amd")
+
+
 def build_cpp_bench() -> Path:
     """Compiles the sil::eval graph benchmark (silarray_amd/bench/bench_graph.cpp)."""
     return _cxx(PKG / "bench" / "bench_graph.cpp", PKG / "bench" / "bench_graph", "$ORIGIN/..")
 
 
 def build_cpp() -> list[Path]:
-    return [build_cpp_tests(), build_cpp_bench()]
+    return [build_cpp_tests(), build_cpp_random_graphs(), build_cpp_bench()]
 
 
 if __name__ == "__main__":
