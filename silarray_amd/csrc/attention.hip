@@ -328,8 +328,38 @@ int silgpu_attention_f32(const silgpu_attn_desc *d) {
                  "silgpu_attention_f32: sequence length exceeds int32");
   const int64_t batch = d->batch_outer * d->batch_inner;
   if (d->Sq == 0 || batch == 0) return SILGPU_OK;
-  SILGPU_REQUIRE(batch <= 65535 && d->batch_inner <= INT32_MAX,
-                 "silgpu_attention_f32: batch %lld exceeds the grid", (long long)batch);
+  if (batch > kMaxGridBatch) {
+    // More (batch, head) pairs than one launch's grid.y holds: launches of
+    // at most kMaxGridBatch pairs, split as silgpu_gemm splits its batch.
+    silgpu_attn_desc p = *d;
+    auto shift = [&](int64_t o, int64_t i) {
+      auto at = [](const float *x, int64_t off) { return x ? x + off : x; };
+      p.Q = at(d->Q, o * d->stride_q_outer + i * d->stride_q_inner);
+      p.K = at(d->K, o * d->stride_k_outer + i * d->stride_k_inner);
+      p.V = at(d->V, o * d->stride_v_outer + i * d->stride_v_inner);
+      p.O = d->O ? d->O + o * d->stride_o_outer + i * d->stride_o_inner : d->O;
+    };
+    if (d->batch_inner <= kMaxGridBatch) {
+      const int64_t per = kMaxGridBatch / d->batch_inner;
+      for (int64_t o0 = 0; o0 < d->batch_outer; o0 += per) {
+        shift(o0, 0);
+        p.batch_outer = d->batch_outer - o0 < per ? d->batch_outer - o0 : per;
+        const int rc = silgpu_attention_f32(&p);
+        if (rc != SILGPU_OK) return rc;
+      }
+    } else {
+      for (int64_t o = 0; o < d->batch_outer; o++)
+        for (int64_t i0 = 0; i0 < d->batch_inner; i0 += kMaxGridBatch) {
+          shift(o, i0);
+          p.batch_outer = 1;
+          p.batch_inner =
+              d->batch_inner - i0 < kMaxGridBatch ? d->batch_inner - i0 : kMaxGridBatch;
+          const int rc = silgpu_attention_f32(&p);
+          if (rc != SILGPU_OK) return rc;
+        }
+    }
+    return SILGPU_OK;
+  }
   SILGPU_REQUIRE(d->O && (d->Sk == 0 || (d->Q && d->K && d->V)),
                  "silgpu_attention_f32: null pointer");
   SILGPU_REQUIRE(d->ldq >= d->D && d->ldk >= d->D && d->ldv >= d->D && d->ldo >= d->D,

@@ -2177,8 +2177,38 @@ int gemm_impl(const silgpu_gemm_desc &d, const plan *forced, bool noalloc = fals
   SILGPU_REQUIRE(d.ldb >= (tb ? K : N) && d.ldb >= 1, "silgpu_gemm: ldb %lld too small",
                  (long long)d.ldb);
   SILGPU_REQUIRE(d.ldc >= N, "silgpu_gemm: ldc %lld < N %lld", (long long)d.ldc, (long long)N);
-  SILGPU_REQUIRE(batch <= 65535 && d.batch_inner <= INT32_MAX,
-                 "silgpu_gemm: batch %lld exceeds the grid", (long long)batch);
+  if (batch > kMaxGridBatch) {
+    // More products than one launch's grid.z holds: launches of at most
+    // kMaxGridBatch products, whole outer indices where the inner batch
+    // fits in one, else pieces of each outer index's inner batch.
+    silgpu_gemm_desc p = d;
+    auto shift = [&](int64_t o, int64_t i) {
+      auto at = [](const float *x, int64_t off) { return x ? x + off : x; };
+      p.A = at(d.A, o * d.stride_a_outer + i * d.stride_a_inner);
+      p.B = at(d.B, o * d.stride_b_outer + i * d.stride_b_inner);
+      p.C = d.C + o * d.stride_c_outer + i * d.stride_c_inner;
+    };
+    if (d.batch_inner <= kMaxGridBatch) {
+      const int64_t per = kMaxGridBatch / d.batch_inner;
+      for (int64_t o0 = 0; o0 < d.batch_outer; o0 += per) {
+        shift(o0, 0);
+        p.batch_outer = d.batch_outer - o0 < per ? d.batch_outer - o0 : per;
+        const int rc = gemm_impl(p, forced, noalloc);
+        if (rc != SILGPU_OK) return rc;
+      }
+    } else {
+      for (int64_t o = 0; o < d.batch_outer; o++)
+        for (int64_t i0 = 0; i0 < d.batch_inner; i0 += kMaxGridBatch) {
+          shift(o, i0);
+          p.batch_outer = 1;
+          p.batch_inner =
+              d.batch_inner - i0 < kMaxGridBatch ? d.batch_inner - i0 : kMaxGridBatch;
+          const int rc = gemm_impl(p, forced, noalloc);
+          if (rc != SILGPU_OK) return rc;
+        }
+    }
+    return SILGPU_OK;
+  }
   const bool uses_bias = d.epilogue == SILGPU_EPI_BIAS || d.epilogue == SILGPU_EPI_BIAS_SIGMOID ||
                          d.epilogue == SILGPU_EPI_BIAS_RELU;
   SILGPU_REQUIRE(!uses_bias || (d.bias && d.bias_len > 0),

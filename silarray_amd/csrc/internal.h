@@ -138,6 +138,9 @@ __device__ __forceinline__ float2 unpack_f2(uint64_t v) {
 }
 
 constexpr size_t kPartialBytes = size_t(16) << 20;  // 16 MiB
+// Largest y or z extent of a launch grid: batched launches (products,
+// attention heads, reduction slices) beyond it are issued in pieces.
+constexpr int64_t kMaxGridBatch = 65535;
 // Size of the fixed scratch array behind silgpu_gemm_noalloc.
 constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;  // 32 MiB
 

@@ -629,8 +629,15 @@ int silgpu_sum_axis_f32(const float *d_in, int64_t outer, int64_t axis_len, int6
     }
     return SILGPU_OK;
   }
-  SILGPU_REQUIRE(outer <= 65535, "silgpu_sum_axis_f32: outer %lld exceeds the grid",
-                 (long long)outer);
+  if (outer > kMaxGridBatch) {  // grid.z limit: issue batches of outer slices
+    for (int64_t o0 = 0; o0 < outer; o0 += kMaxGridBatch) {
+      const int64_t no = outer - o0 < kMaxGridBatch ? outer - o0 : kMaxGridBatch;
+      const int rc =
+          silgpu_sum_axis_f32(d_in + o0 * axis_len * inner, no, axis_len, inner, d_out + o0 * inner);
+      if (rc != SILGPU_OK) return rc;
+    }
+    return SILGPU_OK;
+  }
   const int64_t tiles_x = cdiv(inner, kBlock);
   const int64_t tiles = tiles_x * outer;
   int64_t splits = 1;

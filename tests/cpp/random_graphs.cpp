@@ -18,6 +18,7 @@
 #include <silarray.h>
 
 #include <cstdlib>
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <functional>
@@ -223,7 +224,7 @@ static bool step(std::vector<Val> &pool) {
   Val &x = pool[irand(pool.size() > 4 ? pool.size() - 4 : 0, pool.size() - 1)];
   Val &y = pool[irand(0, pool.size() - 1)];
   const size_t nd = x.h.shape.size();
-  switch (irand(0, 26)) {
+  switch (irand(0, 28)) {
     case 0: {  // binary with a broadcast-compatible partner
       int op = static_cast<int>(irand(0, 3));
       std::vector<size_t> ps;
@@ -516,6 +517,99 @@ static bool step(std::vector<Val> &pool) {
       H hs = select(h3, ax, idx);
       if (hs.shape.size() != 2) return false;
       pool.push_back({x.a.view({a, b, C}).select(ax, idx) * 2.0f, unary(hs, [](double v) { return v * 2.0; }), "sel"});
+      return true;
+    }
+    case 27:
+    case 28: {  // an N-D chain of views (view, permute, select, slice, transpose,
+                // broadcast) over x, then an elementwise node, back to 2-D
+      if (nd != 2) return false;
+      const size_t n = x.h.v.size();
+      std::vector<size_t> sh;
+      for (size_t rem = n, k = irand(2, 5); k > 1; k--) {
+        size_t d = divisor(rem);
+        sh.push_back(d);
+        rem /= d;
+        if (k == 2) sh.push_back(rem);
+      }
+      H h{sh, x.h.v};
+      Arr a = x.a.view(shape_type(sh.begin(), sh.end()));
+      std::string desc = "views" + shp(h);
+      for (size_t step_i = 0, steps = irand(1, 4); step_i < steps; step_i++) {
+        const size_t d = h.shape.size();
+        switch (irand(0, 5)) {
+          case 0: {  // permute
+            std::vector<size_t> ax(d);
+            for (size_t i = 0; i < d; i++) ax[i] = i;
+            std::shuffle(ax.begin(), ax.end(), rng_);
+            h = permute(h, ax);
+            a = a.permute(ax);
+            desc += ".p";
+            break;
+          }
+          case 1: {  // select
+            if (d < 3) break;
+            size_t axis = irand(0, d - 1), idx = irand(0, h.shape[axis] - 1);
+            h = select(h, axis, idx);
+            a = a.select(axis, idx);
+            desc += ".s";
+            break;
+          }
+          case 2: {  // slice along axis 0
+            size_t st = irand(0, h.shape[0] - 1), cnt = irand(1, h.shape[0] - st);
+            size_t inner = count(std::vector<size_t>(h.shape.begin() + 1, h.shape.end()));
+            H o{h.shape, std::vector<double>(h.v.begin() + st * inner, h.v.begin() + (st + cnt) * inner)};
+            o.shape[0] = cnt;
+            h = o;
+            a = a.slice(st, cnt);
+            desc += ".sl";
+            break;
+          }
+          case 3: {  // transpose: 2-D or 3-D (the reference reverses the axes of a 3-D array)
+            if (d == 3) {
+              h = permute(h, {2, 1, 0});
+            } else if (d == 2) {
+              h = transpose(h);
+            } else {
+              break;
+            }
+            a = a.transpose();
+            desc += ".t";
+            break;
+          }
+          case 4: {  // reshape to another factorisation of the same count
+            const size_t m = h.v.size();
+            std::vector<size_t> ns;
+            for (size_t rem = m, k = irand(2, 4); k > 1; k--) {
+              size_t dd = divisor(rem);
+              ns.push_back(dd);
+              rem /= dd;
+              if (k == 2) ns.push_back(rem);
+            }
+            h.shape = ns;
+            a = a.view(shape_type(ns.begin(), ns.end()));
+            desc += ".v";
+            break;
+          }
+          default: {  // broadcast over a new leading axis of 1-3
+            if (d >= 5) break;
+            size_t k = irand(1, 3);
+            std::vector<size_t> ts{k};
+            ts.insert(ts.end(), h.shape.begin(), h.shape.end());
+            H o{ts, {}};
+            for (size_t r = 0; r < k; r++) o.v.insert(o.v.end(), h.v.begin(), h.v.end());
+            h = o;
+            a = a.broadcast(shape_type(ts.begin(), ts.end()));
+            desc += ".b";
+            break;
+          }
+        }
+        if (h.v.size() > 2000000) return false;
+      }
+      if (h.shape.size() < 2) return false;
+      H e = unary(h, [](double v) { return v * 1.5 + 0.25; });
+      size_t cols = e.shape.back(), rows = e.v.size() / cols;
+      Arr r = (a * 1.5f + 0.25f).view({rows, cols});
+      pool.push_back({r, H{{rows, cols}, e.v}, desc});
       return true;
     }
     default: {  // residual-style: x + f(x) with x reused

@@ -1117,6 +1117,59 @@ def test_attention_no_keys_gives_zero(native):
     assert np.all(down(native, dO, ob.shape) == 0)
 
 
+# ---- batches beyond one launch's grid (65535 in y and z) --------------------------
+
+@pytest.mark.parametrize("outer,inner", [(1, 70000), (3, 30000), (2, 65536)])
+def test_gemm_batch_beyond_the_grid(native, oracle, outer, inner):
+    """A batched product of more than 65535 matrices runs in several launches:
+    whole outer indices per launch while the inner batch fits, else pieces of
+    each outer index's inner batch (a batched_dot over a long leading axis)."""
+    announce(f"gemm batch {outer}x{inner}")
+    M, N, K = 3, 5, 7
+    g = rng(7700 + outer)
+    A = g.uniform(-1, 1, (outer, inner, M, K)).astype(np.float32)
+    B = g.uniform(-1, 1, (outer, inner, K, N)).astype(np.float32)
+    dA, dB = up(native, A), up(native, B)
+    dC = up(native, np.full(outer * inner * M * N + 16, np.nan, np.float32))
+    native.gemm(0, 0, M, N, K, dA, K, dB, N, dC, N, batch_outer=outer, batch_inner=inner,
+                strides_a=(inner * M * K, M * K), strides_b=(inner * K * N, K * N),
+                strides_c=(inner * M * N, M * N))
+    out = down(native, dC, (outer * inner * M * N + 16,))
+    assert np.all(np.isnan(out[outer * inner * M * N:]))
+    C = out[:outer * inner * M * N].reshape(outer, inner, M, N).astype(np.float64)
+    ref = np.matmul(A.astype(np.float64), B.astype(np.float64))
+    refabs = np.matmul(np.abs(A.astype(np.float64)), np.abs(B.astype(np.float64)))
+    assert np.all(np.abs(C - ref) <= 1e-5 * np.sqrt(K) * refabs + 1e-30)
+
+
+def test_attention_batch_beyond_the_grid(native):
+    """70000 (batch, head) pairs: several launches of at most 65535."""
+    announce("attention batch 2x35000")
+    Bo, Bi, S, D = 2, 35000, 3, 16
+    g = rng(7800)
+    Q, K, V = (g.normal(0, 1, (Bo, Bi, S, D)).astype(np.float32) for _ in range(3))
+    dQ, dK, dV = up(native, Q), up(native, K), up(native, V)
+    dO = up(native, np.full(Q.size, np.nan, np.float32))
+    st = (Bi * S * D, S * D)
+    native.attention(S, S, D, 0.25, dQ, D, dK, D, dV, D, dO, D, Bo, Bi, st, st, st, st)
+    out = down(native, dO, Q.shape).astype(np.float64)
+    ref = _attention_f64(Q, K, V, 0.25)
+    assert np.isfinite(out).all()
+    assert np.abs(out - ref).max() <= 2e-5 * np.sqrt(max(D, S)) * np.abs(V).max()
+
+
+def test_sum_axis_outer_beyond_the_grid(native, oracle):
+    """sum over the middle axis of [70000, 5, 3]: outer slices in batches."""
+    announce("sum_axis [70000, 5, 3] axis 1")
+    x = rng(7900).normal(0, 3, (70000, 5, 3)).astype(np.float32)
+    dx, do = up(native, x), empty(native, 70000 * 3)
+    native.sum_axis_f32(dx, 70000, 5, 3, do)
+    got = down(native, do, 70000 * 3).astype(np.float64)
+    ref = oracle.sum_axis_f64(x, 1).ravel()
+    absref = oracle.sum_axis_f64(np.abs(x), 1).ravel()
+    assert np.all(np.abs(got - ref) <= 1e-5 * np.abs(ref) + 6e-8 * absref + 1e-30)
+
+
 # ---- conv2d (implicit GEMM) ---------------------------------------------------------
 
 # N, H, W, C_in, K, C_out, by the kernel the entry point picks:
