@@ -344,7 +344,7 @@ int silgpu_gemm(const silgpu_gemm_desc *desc);
  *   - A plan whose partial planes exceed 32 MiB runs with fewer K splits
  *     (down to none), so its rounding may differ from silgpu_gemm's within
  *     the SGEMM tolerance; otherwise the result is bit-identical.  A vector
- *     product (M == 1) whose N exceeds 8M columns is rejected.
+ *     product (M == 1) wider than 8M columns runs in pieces of 8M columns.
  *   - All calls on one device share the array, and it keeps the last call's
  *     contents: calls that overlap in time on one device (several host
  *     threads, several streams) race. */

@@ -2076,6 +2076,17 @@ int launch_gemv_n(const float *x, const float *Bm, int64_t ldb, float *y, int64_
                   int64_t K, context *c, const scratch_src &ss) {
   float *partial = ss.fixed ? ss.fixed : static_cast<float *>(c->partials);
   const int64_t partial_bytes = ss.fixed ? int64_t(ss.fixed_bytes) : int64_t(kPartialBytes);
+  // Wider than one partial row of the scratch area holds: column pieces of
+  // whole 256-column tiles, each its own pass 1 and finish.
+  const int64_t max_cols = partial_bytes / int64_t(sizeof(float)) / kGemvCols * kGemvCols;
+  if (N > max_cols) {
+    for (int64_t c0 = 0; c0 < N; c0 += max_cols) {
+      const int rc = launch_gemv_n(x, Bm + c0, ldb, y + c0, N - c0 < max_cols ? N - c0 : max_cols,
+                                   K, c, ss);
+      if (rc != SILGPU_OK) return rc;
+    }
+    return SILGPU_OK;
+  }
   const bool vec = N % 4 == 0 && ldb % 4 == 0 && aligned16(Bm);
   const int64_t ct = cdiv(N, kGemvCols);
   const int64_t pitch = ct * kGemvCols;

@@ -781,6 +781,30 @@ def test_gemv_ragged(native, oracle, N, K, ldb):
     assert ok, (nw, el)
 
 
+@pytest.mark.parametrize("entry", ["sgemv", "gemm", "gemm_noalloc"])
+def test_gemv_wider_than_the_partials(native, oracle, entry):
+    """1 x 3 . 3 x 8,388,620: more columns than one partial row of the
+    scratch area holds (4M floats for silgpu_sgemv / silgpu_gemm, 8M for the
+    fixed array of silgpu_gemm_noalloc), so the product runs in column
+    pieces of whole 256-column tiles; the last piece is ragged."""
+    N, K = 8_388_620, 3
+    announce(f"gemv wide N={N} K={K} via {entry}")
+    g = rng(1650)
+    x = g.normal(0, 1, K).astype(np.float32)
+    B = g.normal(0, 1, (K, N)).astype(np.float32)
+    dx, dB = up(native, x), up(native, B)
+    dy = up(native, np.full(N + 16, np.nan, np.float32))
+    if entry == "sgemv":
+        native.sgemv(dx, dB, N, dy, N, K)
+    else:
+        native.gemm(0, 0, 1, N, K, dx, K, dB, N, dy, N, noalloc=entry == "gemm_noalloc")
+    y = down(native, dy, N + 16)
+    assert np.all(np.isnan(y[N:]))
+    C64, Cabs = oracle.sgemm_f64(x[None, :], B, with_abs=True)
+    ok, nw, el = gemm_tolerance_ok(y[None, :N], C64, Cabs, K)
+    assert ok, (nw, el)
+
+
 def test_linear_sigmoid_config(native, oracle):
     """configs[1](c): sigmoid(X . W + b), X 256x4096, W 4096x4096, N(0, 0.02)."""
     announce("linear_sigmoid 256x4096x4096")
