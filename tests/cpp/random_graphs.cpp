@@ -10,7 +10,8 @@
 // select and batched_dot, an attention graph with its head merge
 // (bench/composite/bench_transformer.cpp:55-68 batched), conv2d, and scalar
 // reductions and argmax taken mid-graph (which evaluate part of the graph
-// early).  Four roots per graph are evaluated in one sil::eval and each is
+// early), and host writes into evaluated arrays (directly and through row
+// views) that later device nodes read.  Four roots per graph are evaluated in one sil::eval and each is
 // compared with the shadow: |got - ref| <= 1e-3 (rms(ref) + |ref|) + 1e-6, a
 // bar loose enough for fp32 rounding through a chain of nodes and tight
 // enough for a wrong fusion, operand, index or broadcast, which err by O(1).
@@ -224,7 +225,7 @@ static bool step(std::vector<Val> &pool) {
   Val &x = pool[irand(pool.size() > 4 ? pool.size() - 4 : 0, pool.size() - 1)];
   Val &y = pool[irand(0, pool.size() - 1)];
   const size_t nd = x.h.shape.size();
-  switch (irand(0, 28)) {
+  switch (irand(0, 29)) {
     case 0: {  // binary with a broadcast-compatible partner
       int op = static_cast<int>(irand(0, 3));
       std::vector<size_t> ps;
@@ -610,6 +611,26 @@ static bool step(std::vector<Val> &pool) {
       size_t cols = e.shape.back(), rows = e.v.size() / cols;
       Arr r = (a * 1.5f + 0.25f).view({rows, cols});
       pool.push_back({r, H{{rows, cols}, e.v}, desc});
+      return true;
+    }
+    case 29: {  // host writes into an evaluated copy, directly and through a row view
+      if (nd != 2) return false;
+      const size_t C = x.h.shape[1], n = x.h.v.size();
+      Arr y = x.a * 1.0f;
+      y.eval();
+      H h = x.h;
+      for (size_t k = 0, writes = irand(1, 6); k < writes; k++) {
+        const size_t i = irand(0, n - 1);
+        const float v = float(unif(-2, 2));
+        if (irand(0, 1)) {
+          y.at(i) = v;
+        } else {
+          auto row = y.slice(i / C, 1);
+          row.at(i % C) = v;
+        }
+        h.v[i] = v;
+      }
+      pool.push_back({y, h, "hostw"});
       return true;
     }
     default: {  // residual-style: x + f(x) with x reused
