@@ -328,6 +328,10 @@ int silgpu_attention_f32(const silgpu_attn_desc *d) {
                  "silgpu_attention_f32: sequence length exceeds int32");
   const int64_t batch = d->batch_outer * d->batch_inner;
   if (d->Sq == 0 || batch == 0) return SILGPU_OK;
+  SILGPU_REQUIRE(d->O && (d->Sk == 0 || (d->Q && d->K && d->V)),
+                 "silgpu_attention_f32: null pointer");
+  SILGPU_REQUIRE(d->ldq >= d->D && d->ldk >= d->D && d->ldv >= d->D && d->ldo >= d->D,
+                 "silgpu_attention_f32: a row stride is below the head dim");
   if (batch > kMaxGridBatch) {
     // More (batch, head) pairs than one launch's grid.y holds: launches of
     // at most kMaxGridBatch pairs, split as silgpu_gemm splits its batch.
@@ -360,10 +364,6 @@ int silgpu_attention_f32(const silgpu_attn_desc *d) {
     }
     return SILGPU_OK;
   }
-  SILGPU_REQUIRE(d->O && (d->Sk == 0 || (d->Q && d->K && d->V)),
-                 "silgpu_attention_f32: null pointer");
-  SILGPU_REQUIRE(d->ldq >= d->D && d->ldk >= d->D && d->ldv >= d->D && d->ldo >= d->D,
-                 "silgpu_attention_f32: a row stride is below the head dim");
   SILGPU_CTX(c);
   attn_args a{};
   a.Sq = static_cast<int>(d->Sq);

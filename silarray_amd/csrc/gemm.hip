@@ -2188,6 +2188,13 @@ int gemm_impl(const silgpu_gemm_desc &d, const plan *forced, bool noalloc = fals
   SILGPU_REQUIRE(d.ldb >= (tb ? K : N) && d.ldb >= 1, "silgpu_gemm: ldb %lld too small",
                  (long long)d.ldb);
   SILGPU_REQUIRE(d.ldc >= N, "silgpu_gemm: ldc %lld < N %lld", (long long)d.ldc, (long long)N);
+  const bool uses_bias = d.epilogue == SILGPU_EPI_BIAS || d.epilogue == SILGPU_EPI_BIAS_SIGMOID ||
+                         d.epilogue == SILGPU_EPI_BIAS_RELU;
+  SILGPU_REQUIRE(!uses_bias || (d.bias && d.bias_len > 0),
+                 "silgpu_gemm: bias epilogue without bias");
+  SILGPU_REQUIRE(!d.residual || (batch == 1 && d.ldr >= N),
+                 "silgpu_gemm: a residual needs batch 1 and ldr >= N");
+  SILGPU_REQUIRE(d.C != nullptr && (K == 0 || (d.A && d.B)), "silgpu_gemm: null pointer");
   if (batch > kMaxGridBatch) {
     // More products than one launch's grid.z holds: launches of at most
     // kMaxGridBatch products, whole outer indices where the inner batch
@@ -2220,13 +2227,6 @@ int gemm_impl(const silgpu_gemm_desc &d, const plan *forced, bool noalloc = fals
     }
     return SILGPU_OK;
   }
-  const bool uses_bias = d.epilogue == SILGPU_EPI_BIAS || d.epilogue == SILGPU_EPI_BIAS_SIGMOID ||
-                         d.epilogue == SILGPU_EPI_BIAS_RELU;
-  SILGPU_REQUIRE(!uses_bias || (d.bias && d.bias_len > 0),
-                 "silgpu_gemm: bias epilogue without bias");
-  SILGPU_REQUIRE(!d.residual || (batch == 1 && d.ldr >= N),
-                 "silgpu_gemm: a residual needs batch 1 and ldr >= N");
-  SILGPU_REQUIRE(d.C != nullptr && (K == 0 || (d.A && d.B)), "silgpu_gemm: null pointer");
   context *c = noalloc ? ctx_if_ready() : ctx();
   if (!c) return noalloc ? SILGPU_ERR_INVALID : SILGPU_ERR_NODEVICE;
   scratch_src ss{};
