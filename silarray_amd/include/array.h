@@ -1804,10 +1804,6 @@ inline void eval_batched(node *n) {
       outer_begin = inner - 1;
       bouter = n->shape[inner - 1];
       while (outer_begin > 0 && uniform(outer_begin - 1)) bouter *= n->shape[--outer_begin];
-      if (bouter * binner > 65535) {  // grid limit: loop over the outer group instead
-        outer_begin = inner;
-        bouter = 1;
-      }
     }
   }
   silgpu_gemm_desc d{};
@@ -1857,7 +1853,7 @@ inline void eval_batched(node *n) {
 // Folds the leading `L` axes of `shape` into at most two groups that every
 // operand strides uniformly (stride[d] == stride[d+1] * shape[d+1]): the
 // inner group [inner, L) and the outer [0, inner).  False when the axes
-// need more groups or the batch exceeds the grid.
+// need more groups.
 inline bool fold_two_groups(const shape_type &shape, size_t L,
                             const std::vector<const strides_type *> &ops, int64_t &bo,
                             int64_t &bi, std::vector<std::pair<int64_t, int64_t>> &st) {
@@ -1878,7 +1874,6 @@ inline bool fold_two_groups(const shape_type &shape, size_t L,
     while (outer > 0 && uniform(outer - 1)) bo *= int64_t(shape[--outer]);
     if (outer > 0) return false;
   }
-  if (bo * bi > 65535) return false;
   for (size_t i = 0; i < ops.size(); i++)
     st[i] = {inner > 0 ? int64_t((*ops[i])[inner - 1]) : 0, int64_t((*ops[i])[L - 1])};
   return true;

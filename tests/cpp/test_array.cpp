@@ -617,6 +617,33 @@ TEST_CASE("attention graph runs as one fused launch, matching the unfused graph"
   CHECK(worst <= 1e-5f);  // v in [0, 1): outputs are convex combinations of v rows
 }
 
+TEST_CASE("batched products and attention over more batches than one launch's grid") {
+  // 70000 (batch, head) pairs: the library issues them in pieces of at most
+  // 65535; fused attention and plain batched_dot match the unfused graph.
+  const size_t B = 35000, H = 2, S = 3, dh = 16;
+  auto q = random({B, H, S, dh}), k = random({B, H, S, dh}), v = random({B, H, S, dh});
+  auto scores_of = [&] { return q.batched_dot(k.permute({0, 1, 3, 2})) * 0.25f; };
+  auto attend = [&](const array<float> &scores) {
+    return scores.view({B * H * S, S}).softmax().view({B, H, S, S}).batched_dot(v);
+  };
+  auto fused = attend(scores_of());
+  eval(fused);
+  auto scores = scores_of();
+  auto plain = attend(scores);
+  eval(scores, plain);
+  float worst = 0.0f;
+  for (size_t i = 0; i < B * H * S * dh; i++)
+    worst = std::max(worst, std::abs(fused.at(i) - plain.at(i)));
+  CHECK(worst <= 1e-5f);
+  // the scores themselves against a host dot product (first and last pair)
+  for (size_t bh : {size_t(0), B * H - 1}) {
+    const size_t b = bh / H, h = bh % H;
+    float s = 0.0f;
+    for (size_t d = 0; d < dh; d++) s += q.at({b, h, 2, d}) * k.at({b, h, 1, d});
+    CHECK(std::abs(scores.at({b, h, 2, 1}) - s * 0.25f) <= 1e-5f);
+  }
+}
+
 TEST_CASE("conv2d: same padding closed form and the 1x1 kernel as a product") {
   // ones in and ones weights: C_in times the taps inside the image
   auto x = ones<float>({1, 3, 3, 2});
