@@ -1194,6 +1194,10 @@ template <value_type T>
 inline array<float> array<T>::layer_norm(const array<float> &gamma, const array<float> &beta,
                                          float eps) const {
   if (dimension() != 2) throw std::runtime_error("array: layer_norm requires 2D array.");
+  // The kernel reads gamma[c] and beta[c] for every column c: shorter
+  // vectors would be read past their end (the reference does not check).
+  if (gamma.element_count() != shape_[1] || beta.element_count() != shape_[1])
+    throw std::runtime_error("array: layer_norm needs one gamma and one beta per column.");
   if constexpr (std::is_same_v<T, float>) {
     auto n = detail::node::make(detail::op::layer_norm,
                                 {to_node_(*this), to_node_(gamma), to_node_(beta)}, shape_);

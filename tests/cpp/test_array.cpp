@@ -69,6 +69,15 @@ HOST_CASE("bounds checks") {
   CHECK_THROWS_WITH(v.at(10), "array: index is out of bounds.");
   auto t = array<int>{{{1, 2, 3}, {4, 5, 6}}};
   CHECK_THROWS_WITH(t[3], "array: row is out of bounds.");
+  // layer_norm reads one gamma and one beta per column: other lengths are
+  // refused when the node is built, before any kernel could read past them
+  auto x = array<float>({2, 4}, std::vector<float>{1, 2, 3, 4, 5, 6, 7, 8});
+  auto g4 = array<float>({4}, std::vector<float>{1, 1, 1, 1});
+  auto g3 = array<float>({3}, std::vector<float>{1, 1, 1});
+  CHECK_THROWS_WITH(x.layer_norm(g3, g4), "array: layer_norm needs one gamma and one beta per column.");
+  CHECK_THROWS_WITH(x.layer_norm(g4, g3), "array: layer_norm needs one gamma and one beta per column.");
+  CHECK_THROWS_WITH(array<float>({3}, std::vector<float>{1, 2, 3}).layer_norm(g3, g3),
+                    "array: layer_norm requires 2D array.");
 }
 
 HOST_CASE("transpose views") {
