@@ -286,8 +286,11 @@ int silgpu_sgemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
  * reference counterpart.  tile: 1 = 128x128, 2 = 64x64, 3 = 32x128,
  * 4 = 128x64, 5 = 256x256 (workgroup tile of C); 6, 7, 8 = the small-M
  * kernel (M <= 32, batch 1, A not transposed; otherwise the 32x128 tile)
- * with 32, 64 or 128 columns per workgroup; splits: K splits (>= 1; batch
- * must be 1 for splits > 1).  Never routes to the GEMV kernels. */
+ * with 32, 64 or 128 columns per workgroup; 9 = 64x64 with each
+ * workgroup's K range halved between two groups of waves (M, N, K
+ * multiples of 64 and 16-byte aligned operands; otherwise the 64x64 tile);
+ * splits: K splits (>= 1; batch must be 1 for splits > 1).  Never routes to
+ * the GEMV kernels. */
 int silgpu_sgemm_tuned(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
                        const float *d_A, int64_t lda, int64_t stride_a, const float *d_B,
                        int64_t ldb, int64_t stride_b, float *d_C, int64_t ldc,

@@ -12,7 +12,10 @@
 // from LDS while the MFMAs of step s run (a scheduling barrier per step keeps
 // the compiler from hoisting further and spilling), and the workgroup -> tile
 // mapping keeps the workgroups of one XCD on neighbouring tiles so their A
-// and B panels are shared in that XCD's L2.
+// and B panels are shared in that XCD's L2.  Products too small to fill the
+// 256 CUs split K: across workgroups (partial planes added by a second
+// launch) or, for 64 x 64 tiles, also between two groups of waves inside a
+// workgroup (added through LDS, no second launch).
 //
 // Epilogues (bias, sigmoid, relu) are applied to the accumulators before the
 // single store, so linear / linear_sigmoid are one pass over C.
@@ -936,12 +939,21 @@ constexpr int kRawRsrcWord3 = 0x00020000;
 // loads of convolution taps that fall into the padding.  Never written.
 __device__ __attribute__((aligned(16))) float conv_zero_page[4];
 
-template <int BM, int BN, int BK, int NWV, int NS, bool TA, bool TB, bool CONV = false>
-__global__ __launch_bounds__((dtl_cfg<BM, BN, BK, NWV, NS>::kThreads))
+// KG > 1: the workgroup is KG groups of NWV waves.  Group g runs the tile's
+// K loop over the g-th of KG equal parts of the workgroup's K range, with
+// its own LDS stages, and the groups' accumulators are added through LDS at
+// the end (group 0 + group 1 + ...), so a product needs no second launch to
+// add K splits where KG parts fill the CU.  Every group runs the same number
+// of K tiles and so meets every barrier; the host keeps each K range a
+// multiple of KG * BK.
+template <int BM, int BN, int BK, int NWV, int NS, bool TA, bool TB, bool CONV = false, int KG = 1>
+__global__ __launch_bounds__((dtl_cfg<BM, BN, BK, NWV, NS>::kThreads * KG))
 __attribute__((amdgpu_waves_per_eu(dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU,
                                    dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU))) void sgemm_dtl_k(gemm_args p) {
   using D = dtl_cfg<BM, BN, BK, NWV, NS>;
   static_assert(NS >= 2 && NS <= 4, "stages");
+  static_assert(KG >= 1 && (KG == 1 || !CONV), "K groups");
+  static_assert(D::kLdsBytes * KG <= 160 * 1024, "LDS");
   using F = mfma<16>;
   constexpr int TM = D::TM, TN = D::TN, NW = D::WM * D::WN;
   constexpr int WPA = D::kWinA / NW, WPB = D::kWinB / NW;  // windows per wave
@@ -950,15 +962,21 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU,
   // into one stage cannot touch the fragment reads from another, and the
   // compiler adds no wait for the prefetch before those reads.  Tile kt
   // reads stage kt % NS and issues the loads of tile kt + NS - 1.
-  __shared__ __attribute__((aligned(16))) float lds0[D::kStage];
-  __shared__ __attribute__((aligned(16))) float lds1[D::kStage];
-  __shared__ __attribute__((aligned(16))) float lds2[NS > 2 ? D::kStage : 4];
-  __shared__ __attribute__((aligned(16))) float lds3[NS > 3 ? D::kStage : 4];
+  __shared__ __attribute__((aligned(16))) float lds0_[KG * D::kStage];
+  __shared__ __attribute__((aligned(16))) float lds1_[KG * D::kStage];
+  __shared__ __attribute__((aligned(16))) float lds2_[NS > 2 ? KG * D::kStage : 4];
+  __shared__ __attribute__((aligned(16))) float lds3_[NS > 3 ? KG * D::kStage : 4];
   // The wave index through readfirstlane: the compiler then keeps it, and
   // every window and LDS address derived from it, in SGPRs.
   // (Not for the convolution: its gathers measured 1.5-2% slower so.)
   const int t = threadIdx.x, lane = t % kWave;
-  const int wave = CONV ? t / kWave : __builtin_amdgcn_readfirstlane(t / kWave);
+  const int wave_all = CONV ? t / kWave : __builtin_amdgcn_readfirstlane(t / kWave);
+  const int grp = KG == 1 ? 0 : wave_all / NW;  // K group
+  const int wave = KG == 1 ? wave_all : wave_all % NW;  // wave within the group
+  float *const lds0 = lds0_ + (KG == 1 ? 0 : grp * D::kStage);
+  float *const lds1 = lds1_ + (KG == 1 ? 0 : grp * D::kStage);
+  float *const lds2 = lds2_ + (KG == 1 || NS <= 2 ? 0 : grp * D::kStage);
+  float *const lds3 = lds3_ + (KG == 1 || NS <= 3 ? 0 : grp * D::kStage);
   const int wm = wave / D::WN, wn = wave % D::WN;
   int tm, tn;
   tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
@@ -968,9 +986,11 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU,
   const float *__restrict__ B = p.B + zo * p.sB2 + zi * p.sB;
   float *__restrict__ Cp = p.C + zo * p.sC2 + zi * p.sC;
   const int M = p.M, N = p.N;
-  const int kbeg = blockIdx.y * p.klen;
-  const int kend = min(p.K, kbeg + p.klen);
-  const int KT = kend > kbeg ? (kend - kbeg) / BK : 0;  // K % BK == 0 on this path
+  const int kbeg0 = blockIdx.y * p.klen;
+  const int kend = min(p.K, kbeg0 + p.klen);
+  // K % BK == 0 on this path; with KG groups each takes KT whole tiles.
+  const int KT = kend > kbeg0 ? (kend - kbeg0) / BK / KG : 0;
+  const int kbeg = kbeg0 + grp * KT * BK;
   // This wave loads windows wave + q*NW (q < WPA, WPB) of each operand.
   int64_t a_uni[WPA], b_uni[WPB];
   uint32_t a_lane[WPA], b_lane[WPB];
@@ -1200,6 +1220,42 @@ __attribute__((amdgpu_waves_per_eu(dtl_cfg<BM, BN, BK, NWV, NS>::kWavesPerEU,
       if (kt + 2 < KT) tile(lds2, lds1, kt + 2);
       if (kt + 3 < KT) tile(lds3, lds2, kt + 3);
     }
+  }
+  if constexpr (KG > 1) {
+    // Groups 1.. hand their accumulators to group 0 through LDS, in group
+    // order, over the stage buffers (every wave's reads of them are done
+    // at the first barrier): slot (i, j) of wave w, lane l at float4
+    // ((i * TN + j) * NW + w) * 64 + l, so each store and load of a wave is
+    // 1 KiB of consecutive LDS.
+    static_assert(F::R == 4 && TM * TN * NW * kWave * 4 <= D::kStage * KG, "K-group exchange");
+    float4 *const red = reinterpret_cast<float4 *>(lds0_);
+    const int slot = wave * kWave + lane;
+#pragma unroll
+    for (int gs = 1; gs < KG; ++gs) {
+      __syncthreads();
+      if (grp == gs) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            red[(i * TN + j) * NW * kWave + slot] =
+                make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      }
+      __syncthreads();
+      if (grp == 0) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            const float4 v = red[(i * TN + j) * NW * kWave + slot];
+            acc[i][j][0] += v.x;
+            acc[i][j][1] += v.y;
+            acc[i][j][2] += v.z;
+            acc[i][j][3] += v.w;
+          }
+      }
+    }
+    if (grp != 0) return;
   }
   if (gridDim.y > 1) {
     // The raw accumulators to plane y through a buffer descriptor based at
@@ -1531,21 +1587,25 @@ int launch_cfg(const gemm_args &a, int64_t batch, int splits, hipStream_t s) {
   return splits;  // >= 1: the number of K splits actually launched
 }
 
-template <int BM, int BN, int BK, int NWV, int NS, bool TA, bool TB>
+// KG > 1 (K groups within the workgroup) needs K % (KG * BK) == 0: every
+// workgroup's K range is then a whole number of KG * BK.
+template <int BM, int BN, int BK, int NWV, int NS, bool TA, bool TB, int KG = 1>
 int launch_dtl(const gemm_args &a, int64_t batch, int splits, hipStream_t s) {
   using D = dtl_cfg<BM, BN, BK, NWV, NS>;
-  auto kern = sgemm_dtl_k<BM, BN, BK, NWV, NS, TA, TB>;
+  auto kern = sgemm_dtl_k<BM, BN, BK, NWV, NS, TA, TB, false, KG>;
+  constexpr int kGran = BK * KG;
+  SILGPU_REQUIRE(a.K % kGran == 0, "sgemm_dtl_k: K %d is not a multiple of %d", a.K, kGran);
   gemm_args g = a;
   g.tiles_m = static_cast<int>(a.M / BM);
   g.tiles_n = static_cast<int>(a.N / BN);
   // The split planes are stored with 32-bit offsets within a tile's rows.
   if (int64_t(BM) * a.N * 4 >= (int64_t(1) << 30)) splits = 1;
-  g.klen = static_cast<int>(cdiv(cdiv(a.K, splits), BK) * BK);
-  if (g.klen < BK) g.klen = BK;
+  g.klen = static_cast<int>(cdiv(cdiv(a.K, splits), kGran) * kGran);
+  if (g.klen < kGran) g.klen = kGran;
   splits = static_cast<int>(a.K > 0 ? cdiv(a.K, g.klen) : 1);
   dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(splits),
             static_cast<unsigned>(batch));
-  kern<<<grid, D::kThreads, 0, s>>>(g);
+  kern<<<grid, D::kThreads * KG, 0, s>>>(g);
   SILGPU_LAUNCH_CHECK("sgemm_dtl_k");
   return splits;
 }
@@ -1604,6 +1664,23 @@ int launch_tiles(const gemm_args &a, int64_t batch, int splits, bool ta, bool tb
   if (!ta && tb) return launch_tb<BM, BN, BK, WM, WN, MI, false, true>(a, batch, splits, vec, s);
   if (ta && !tb) return launch_tb<BM, BN, BK, WM, WN, MI, true, false>(a, batch, splits, vec, s);
   return launch_tb<BM, BN, BK, WM, WN, MI, true, true>(a, batch, splits, vec, s);
+}
+
+// 64 x 64 tiles on the LDS-direct kernel as two K groups of 4 waves (32 x 32
+// each, 8 waves per workgroup): where 64 x 64 tiles fill the CUs once, the
+// product runs in one launch with the K range halved inside each workgroup
+// instead of split across workgroups and added by a second launch.
+// Operands the LDS-direct loads cannot take run the register-staged 64 x 64
+// tile (`k2` false).
+int launch_k2(const gemm_args &a, int64_t batch, int splits, bool ta, bool tb, bool vec,
+              hipStream_t s, bool &k2) {
+  k2 = vec && a.M % 64 == 0 && a.N % 64 == 0 && a.K % 64 == 0 && a.lda < kDtlMaxLd &&
+       a.ldb < kDtlMaxLd;
+  if (!k2) return launch_tiles<64, 64, 16, 2, 2, 16>(a, batch, splits, ta, tb, vec, s);
+  if (!ta && !tb) return launch_dtl<64, 64, 32, 4, 2, false, false, 2>(a, batch, splits, s);
+  if (!ta && tb) return launch_dtl<64, 64, 32, 4, 2, false, true, 2>(a, batch, splits, s);
+  if (ta && !tb) return launch_dtl<64, 64, 32, 4, 2, true, false, 2>(a, batch, splits, s);
+  return launch_dtl<64, 64, 32, 4, 2, true, true, 2>(a, batch, splits, s);
 }
 
 // Adds the K-split partial planes ws[s][M][N] (s < splits) and applies the
@@ -1695,7 +1772,10 @@ enum tile_cfg {
   // deep products, TILE_SKINNY_Q2.
   TILE_SKINNY = 6,
   TILE_SKINNY_Q2 = 7,
-  TILE_SKINNY_Q4 = 8
+  TILE_SKINNY_Q4 = 8,
+  // 64 x 64 tiles with the K range halved between two wave groups of each
+  // workgroup (launch_k2).
+  TILE_64x64_K2 = 9
 };
 
 struct plan {
@@ -1838,6 +1918,25 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dtl_ok) {
       }
     }
   }
+  // Where the pick adds K splits in a second launch and 64 x 64 tiles times
+  // at most 8 K splits fill 7/8 or more of the CUs in one round, the 64 x 64
+  // tile with the K range halved inside each workgroup (TILE_64x64_K2)
+  // needs fewer splits, or none, for the same fill.  A rule rather than a
+  // candidate of the model: the model's times of the split plans miss by
+  // -5..+5 us on these shapes, while this tile's time is a steady ~4 us
+  // launch and ramp plus its MFMA time.  MI355X, us, previous pick ->
+  // TILE_64x64_K2: 1024^3 24.1 -> 20.7 (2 splits -> none), 256x4096x4096
+  // 70.1 -> 67.2, 512x1024x1024 18.3 -> 16.0, 256x2048x512 14.3 -> 12.2,
+  // 256x1024x4096 23.9 -> 22.7, 128x2048x768 12.6 -> 11.0, 512^3 10.8 ->
+  // 10.0; with 192 tiles (1024x768x2048) it lost, 34.2 -> 36.0.
+  if (batch == 1 && dtl_ok && best.splits > 1 && best.tail_rows == 0 && M % 64 == 0 &&
+      N % 64 == 0 && K % 64 == 0) {
+    const int64_t t64 = (M / 64) * (N / 64);
+    int64_t sp = t64 > 0 ? 256 / t64 : 0;
+    if (sp > 8) sp = 8;
+    while (sp > 1 && K / sp < 128) --sp;
+    if (sp >= 1 && t64 * sp >= 224) return plan{TILE_64x64_K2, static_cast<int>(sp)};
+  }
   return best;
 }
 
@@ -1943,8 +2042,9 @@ int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, boo
   const int64_t kLane = int64_t(1) << 30;
   const bool lane32 = int64_t(a.M) * a.lda + 8 < kLane &&
                       (tb ? (int64_t(a.N) + 4) * a.ldb + 8 : 8 * a.ldb + a.N) < kLane;
-  const bool skinny = pl.tile >= TILE_SKINNY && a.M <= 32 && batch == 1 && !ta && lane32;
-  if (pl.tile >= TILE_SKINNY && !skinny)
+  const bool skinny_tile = pl.tile >= TILE_SKINNY && pl.tile <= TILE_SKINNY_Q4;
+  const bool skinny = skinny_tile && a.M <= 32 && batch == 1 && !ta && lane32;
+  if (skinny_tile && !skinny)
     pl = pl.splits >= 1 ? plan{TILE_32x128, pl.splits} : small_m_tiles(a.M, a.N, a.K, batch);
   int splits = pl.splits;
   int q = 1;
@@ -1967,10 +2067,14 @@ int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, boo
     }
   }
   int launched;
+  bool k2 = false;
   if (skinny) {
     launched = launch_skinny(a, q, splits, tb, c->stream);
   } else {
     switch (pl.tile) {
+      case TILE_64x64_K2:
+        launched = launch_k2(a, batch, splits, ta, tb, vec, c->stream, k2);
+        break;
       case TILE_64x64:
         launched = launch_tiles<64, 64, 16, 2, 2, 16>(a, batch, splits, ta, tb, vec, c->stream);
         break;
@@ -1994,7 +2098,8 @@ int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, boo
     const bool known = pl.tile == TILE_64x64 || pl.tile == TILE_32x128 ||
                        pl.tile == TILE_128x64 || pl.tile == TILE_256x256;
     rec.tile[rec.n] = skinny ? (q == 4 ? TILE_SKINNY_Q4 : q == 2 ? TILE_SKINNY_Q2 : TILE_SKINNY)
-                             : known ? pl.tile : TILE_128x128;
+                      : pl.tile == TILE_64x64_K2 ? (k2 ? TILE_64x64_K2 : TILE_64x64)
+                      : known ? pl.tile : TILE_128x128;
     rec.splits[rec.n] = launched;
     rec.rows[rec.n] = a.M;
     ++rec.n;
@@ -2340,7 +2445,7 @@ int silgpu_sgemm_tuned(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K
                        int64_t ldb, int64_t stride_b, float *d_C, int64_t ldc, int64_t stride_c,
                        int64_t batch, const float *d_bias, int64_t bias_len, int epilogue,
                        int tile, int splits) {
-  SILGPU_REQUIRE(tile >= TILE_128x128 && tile <= TILE_SKINNY_Q4,
+  SILGPU_REQUIRE(tile >= TILE_128x128 && tile <= TILE_64x64_K2,
                  "silgpu_sgemm_tuned: unknown tile configuration %d", tile);
   SILGPU_REQUIRE(splits >= 1 && splits <= 256, "silgpu_sgemm_tuned: splits %d not in [1, 256]",
                  splits);

@@ -92,7 +92,7 @@ def test_split_sum_is_the_plane_sum_in_order(native, M, N, K, splits):
     assert np.array_equal(C, want), float(np.max(np.abs(C - want)))
 
 
-@pytest.mark.parametrize("M,N,K", [(1024, 1024, 1024), (2048, 768, 3072)])
+@pytest.mark.parametrize("M,N,K", [(1024, 768, 2048), (2048, 768, 3072)])
 def test_split_sum_with_residual_matches_the_plane_sum(native, M, N, K):
     # silgpu_gemm with bias and residual on the planner's own pick (128 x 64
     # tiles with a K split for these shapes)

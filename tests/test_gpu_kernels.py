@@ -844,7 +844,7 @@ def test_small_batch_config(native, oracle):
     assert ok, (nw, el)
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9])
 @pytest.mark.parametrize("splits", [1, 3, 8])
 @pytest.mark.parametrize("M,N,K,ta,tb,epi", [(33, 70, 200, 0, 0, 0), (128, 256, 512, 0, 0, 2),
                                              (100, 130, 1000, 1, 0, 1), (64, 96, 777, 0, 1, 4),
@@ -1047,6 +1047,70 @@ def test_sgemm_lds_direct_batched(native, oracle, ta, tb, tile, K, splits):
         ref = np.maximum(C64 + bias, 0)
         ok, nw, el = gemm_tolerance_ok(Cg[z], ref, Cabs + np.abs(bias), K)
         assert ok, (z, nw, el)
+
+
+@pytest.mark.parametrize("M,N,K,splits,batch", [(64, 64, 64, 1, 1), (256, 512, 1024, 1, 1),
+                                                (192, 128, 320, 3, 1), (128, 192, 4096, 8, 1),
+                                                (128, 256, 192, 1, 3)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_sgemm_k_groups(native, oracle, ta, tb, M, N, K, splits, batch):
+    """Tile 9: 64 x 64 tiles on the LDS-direct kernel with each workgroup's
+    K range halved between two wave groups and added through LDS.  Padded
+    leading dimensions, every transpose, bias + relu, K splits on top (K
+    ranges of whole 64s: 320 = 128 + 128 + 64) and batches; the plan record
+    shows the kernel ran, and the padding columns of C stay unwritten."""
+    announce(f"sgemm k-groups ta={ta} tb={tb} {M}x{N}x{K} splits={splits} batch={batch}")
+    g = rng(2400 + 2 * ta + tb + K)
+    lda = (M if ta else K) + 4
+    ldb = (K if tb else N) + 8
+    ldc = N + 4
+    rows_a, rows_b = (K if ta else M), (N if tb else K)
+    A = g.uniform(-1, 1, (batch, rows_a, lda)).astype(np.float32)
+    B = g.uniform(-1, 1, (batch, rows_b, ldb)).astype(np.float32)
+    bias = g.normal(0, 1, N).astype(np.float32)
+    canary = np.full((batch, M, ldc), 7.25, np.float32)
+    dA, dB, db, dC = up(native, A), up(native, B), up(native, bias), up(native, canary)
+    native.sgemm_tuned(ta, tb, M, N, K, dA, lda, rows_a * lda, dB, ldb, rows_b * ldb, dC, ldc,
+                       M * ldc, batch, db, N, native.EPI_BIAS_RELU, tile=9, splits=splits)
+    plan = native.last_plan()
+    assert plan and plan[0][0] == 9, plan
+    Cg = down(native, dC, (batch, M, ldc))
+    assert np.all(Cg[:, :, N:] == 7.25)
+    for z in range(batch):
+        a = A[z][:, :M] if ta else A[z][:, :K]
+        b = B[z][:, :K] if tb else B[z][:, :N]
+        C64, Cabs = oracle.sgemm_f64(np.ascontiguousarray(a), np.ascontiguousarray(b), ta=ta,
+                                     tb=tb, with_abs=True)
+        ref = np.maximum(C64 + bias, 0)
+        ok, nw, el = gemm_tolerance_ok(Cg[z][:, :N], ref, Cabs + np.abs(bias), K)
+        assert ok, (z, nw, el)
+
+
+@pytest.mark.parametrize("M,N,K,splits", [(1024, 1024, 1024, 1), (256, 2048, 512, 2),
+                                          (128, 2048, 768, 4)])
+def test_k_groups_planner_pick_with_residual(native, oracle, M, N, K, splits):
+    """Products whose 64 x 64 tiles (times a few K splits) fill the CUs once
+    run tile 9 by the planner's own choice, through silgpu_gemm with bias and
+    residual, and through silgpu_gemm_noalloc bit for bit the same."""
+    announce(f"k-groups planner pick {M}x{N}x{K}")
+    g = rng(2500 + M + K)
+    A = g.normal(0, 1, (M, K)).astype(np.float32)
+    B = g.normal(0, 1, (K, N)).astype(np.float32)
+    b = g.normal(0, 1, N).astype(np.float32)
+    R = g.normal(0, 1, (M, N)).astype(np.float32)
+    dA, dB, db, dR = up(native, A), up(native, B), up(native, b), up(native, R)
+    dC, dCn = empty(native, M * N), empty(native, M * N)
+    native.gemm(0, 0, M, N, K, dA, K, dB, N, dC, N, epi=native.EPI_BIAS, bias=db, bias_len=N,
+                residual=dR, ldr=N)
+    assert native.last_plan() == [(9, splits, M)], native.last_plan()
+    native.gemm(0, 0, M, N, K, dA, K, dB, N, dCn, N, epi=native.EPI_BIAS, bias=db, bias_len=N,
+                residual=dR, ldr=N, noalloc=True)
+    assert native.last_plan() == [(9, splits, M)], native.last_plan()
+    C, Cn = down(native, dC, (M, N)), down(native, dCn, (M, N))
+    assert np.array_equal(C, Cn)
+    C64, Cabs = oracle.sgemm_f64(A, B, with_abs=True)
+    ok, nw, el = gemm_tolerance_ok(C, C64 + b + R, Cabs + np.abs(b) + np.abs(R), K)
+    assert ok, (nw, el)
 
 
 # ---- fused attention ----------------------------------------------------------------
