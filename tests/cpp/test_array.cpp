@@ -9,6 +9,7 @@
 #include <cmath>
 #include <cstring>
 #include <numeric>
+#include <tuple>
 #include <ranges>
 #include <utility>
 #include <vector>
@@ -759,6 +760,69 @@ TEST_CASE("relu of linear runs in the GEMM epilogue") {
       some_pos = some_pos || yv > 0.0f;
     }
   CHECK(ok && some_zero && some_pos);
+}
+
+TEST_CASE("products the planner runs on the K-group 64x64 tile: transposed views, linear + relu") {
+  // Shapes whose 64 x 64 tiles (times a few K splits) fill the CUs once run
+  // with K halved between two wave groups of each workgroup; every operand
+  // layout through transposed views, against host double sums on sampled
+  // elements with the SGEMM bar 1e-5 * sqrt(K) * sum |a b|.
+  auto check = [](const array<float> &c, auto a_at, auto b_at, size_t M, size_t N, size_t K,
+                  auto off) {
+    bool ok = true;
+    for (size_t t = 0; t < 64; t++) {
+      const size_t i = (t * 389 + 7) % M, j = (t * 211 + 3) % N;
+      double s = off(j), sa = std::abs(off(j));
+      for (size_t k = 0; k < K; k++) {
+        const double p = double(a_at(i, k)) * double(b_at(k, j));
+        s += p;
+        sa += std::abs(p);
+      }
+      ok = ok && std::abs(double(c[i, j]) - s) <= 1e-5 * std::sqrt(double(K)) * sa + 1e-30;
+    }
+    return ok;
+  };
+  int n = 0, tiles[2] = {0, 0}, splits[2] = {0, 0}, rows[2] = {0, 0};
+  for (auto [M, N, K] : {std::tuple<size_t, size_t, size_t>{1024, 1024, 1024}, {256, 2048, 512}}) {
+    auto a = random({M, K}) - 0.5f, at = random({K, M}) - 0.5f;
+    auto b = random({K, N}) - 0.5f, bt = random({N, K}) - 0.5f;
+    eval(a, at, b, bt);
+    auto nn = a.dot(b), tn = at.transpose().dot(b), nt = a.dot(bt.transpose()),
+         tt = at.transpose().dot(bt.transpose());
+    eval(nn, tn, nt, tt);
+    silgpu_gemm_last_plan(&n, tiles, splits, rows);
+    CHECK(n == 1);
+    CHECK(tiles[0] == 9);
+    auto none = [](size_t) { return 0.0; };
+    CHECK(check(nn, [&](size_t i, size_t k) { return a[i, k]; },
+                [&](size_t k, size_t j) { return b[k, j]; }, M, N, K, none));
+    CHECK(check(tn, [&](size_t i, size_t k) { return at[k, i]; },
+                [&](size_t k, size_t j) { return b[k, j]; }, M, N, K, none));
+    CHECK(check(nt, [&](size_t i, size_t k) { return a[i, k]; },
+                [&](size_t k, size_t j) { return bt[j, k]; }, M, N, K, none));
+    CHECK(check(tt, [&](size_t i, size_t k) { return at[k, i]; },
+                [&](size_t k, size_t j) { return bt[j, k]; }, M, N, K, none));
+  }
+  // linear + relu at 128 x 2048 x 768 (4 K splits on the K-group tile),
+  // bit-identical to relu applied to the unfused twin
+  auto x = random({128, 768}) - 0.5f;
+  auto W = random({768, 2048}) - 0.5f;
+  auto bias = random({2048}) - 0.5f;
+  eval(x, W, bias);
+  auto y = x.linear(W, bias).relu();
+  eval(y);
+  silgpu_gemm_last_plan(&n, tiles, splits, rows);
+  CHECK(n == 1);
+  CHECK(tiles[0] == 9);
+  auto z = x.linear(W, bias);
+  eval(z);
+  bool ok = true;
+  for (size_t i = 0; i < 128; i++)
+    for (size_t j = 0; j < 2048; j++) ok = ok && y[i, j] == std::max(z[i, j], 0.0f);
+  CHECK(ok);
+  CHECK(check(z, [&](size_t i, size_t k) { return x[i, k]; },
+              [&](size_t k, size_t j) { return W[k, j]; }, 128, 2048, 768,
+              [&](size_t j) { return double(bias.at(j)); }));
 }
 
 //------------------------------------------------------------------------------
