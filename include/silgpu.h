@@ -289,6 +289,7 @@ int silgpu_sgemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
  * with 32, 64 or 128 columns per workgroup; 9 = 64x64 with each
  * workgroup's K range halved between two groups of waves (M, N, K
  * multiples of 64 and 16-byte aligned operands; otherwise the 64x64 tile);
+ * 10 = the same with four groups (K a multiple of 128);
  * splits: K splits (>= 1; batch must be 1 for splits > 1).  Never routes to
  * the GEMV kernels. */
 int silgpu_sgemm_tuned(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,

@@ -336,7 +336,7 @@ def sgemm(ta, tb, M, N, K, A, lda, sA, B, ldb, sB, Cm, ldc, sC, batch=1, bias=No
 
 
 TILE_128x128, TILE_64x64, TILE_32x128, TILE_128x64, TILE_256x256 = 1, 2, 3, 4, 5
-TILE_64x64_K2 = 9
+TILE_64x64_K2, TILE_64x64_K4 = 9, 10
 
 
 def sgemm_tuned(ta, tb, M, N, K, A, lda, sA, B, ldb, sB, Cm, ldc, sC, batch=1, bias=None,

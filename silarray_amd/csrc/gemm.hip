@@ -1672,6 +1672,18 @@ int launch_tiles(const gemm_args &a, int64_t batch, int splits, bool ta, bool tb
 // instead of split across workgroups and added by a second launch.
 // Operands the LDS-direct loads cannot take run the register-staged 64 x 64
 // tile (`k2` false).
+// The same tile as four K groups of 4 waves (16 waves, 136 KB of LDS: one
+// workgroup per CU, four waves per SIMD), for long K.
+int launch_k4(const gemm_args &a, int64_t batch, int splits, bool ta, bool tb, bool vec,
+              hipStream_t s, bool &k2) {
+  k2 = vec && a.M % 64 == 0 && a.N % 64 == 0 && a.K % 128 == 0 && a.lda < kDtlMaxLd &&
+       a.ldb < kDtlMaxLd;
+  if (!k2) return launch_tiles<64, 64, 16, 2, 2, 16>(a, batch, splits, ta, tb, vec, s);
+  if (!ta && !tb) return launch_dtl<64, 64, 32, 4, 2, false, false, 4>(a, batch, splits, s);
+  if (!ta && tb) return launch_dtl<64, 64, 32, 4, 2, false, true, 4>(a, batch, splits, s);
+  if (ta && !tb) return launch_dtl<64, 64, 32, 4, 2, true, false, 4>(a, batch, splits, s);
+  return launch_dtl<64, 64, 32, 4, 2, true, true, 4>(a, batch, splits, s);
+}
 int launch_k2(const gemm_args &a, int64_t batch, int splits, bool ta, bool tb, bool vec,
               hipStream_t s, bool &k2) {
   k2 = vec && a.M % 64 == 0 && a.N % 64 == 0 && a.K % 64 == 0 && a.lda < kDtlMaxLd &&
@@ -1774,8 +1786,9 @@ enum tile_cfg {
   TILE_SKINNY_Q2 = 7,
   TILE_SKINNY_Q4 = 8,
   // 64 x 64 tiles with the K range halved between two wave groups of each
-  // workgroup (launch_k2).
-  TILE_64x64_K2 = 9
+  // workgroup (launch_k2), or quartered between four (launch_k4).
+  TILE_64x64_K2 = 9,
+  TILE_64x64_K4 = 10
 };
 
 struct plan {
@@ -1935,6 +1948,11 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dtl_ok) {
     int64_t sp = t64 > 0 ? 256 / t64 : 0;
     if (sp > 8) sp = 8;
     while (sp > 1 && K / sp < 128) --sp;
+    // Unsplit with K >= 3072: four wave groups (four waves per SIMD) of at
+    // least 768 each beat two (256x4096x4096 67.4 -> 65.2 us, 1024x1024x3072
+    // 51.7 -> 50.8); with shorter groups the two-group tile wins (1024^3
+    // 20.9 against 21.5).
+    if (sp == 1 && t64 >= 224 && K >= 3072 && K % 128 == 0) return plan{TILE_64x64_K4, 1};
     if (sp >= 1 && t64 * sp >= 224) return plan{TILE_64x64_K2, static_cast<int>(sp)};
   }
   return best;
@@ -2075,6 +2093,9 @@ int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, boo
       case TILE_64x64_K2:
         launched = launch_k2(a, batch, splits, ta, tb, vec, c->stream, k2);
         break;
+      case TILE_64x64_K4:
+        launched = launch_k4(a, batch, splits, ta, tb, vec, c->stream, k2);
+        break;
       case TILE_64x64:
         launched = launch_tiles<64, 64, 16, 2, 2, 16>(a, batch, splits, ta, tb, vec, c->stream);
         break;
@@ -2099,6 +2120,7 @@ int run_sgemm(const gemm_args &a0, int64_t batch, plan pl, bool ta, bool tb, boo
                        pl.tile == TILE_128x64 || pl.tile == TILE_256x256;
     rec.tile[rec.n] = skinny ? (q == 4 ? TILE_SKINNY_Q4 : q == 2 ? TILE_SKINNY_Q2 : TILE_SKINNY)
                       : pl.tile == TILE_64x64_K2 ? (k2 ? TILE_64x64_K2 : TILE_64x64)
+                      : pl.tile == TILE_64x64_K4 ? (k2 ? TILE_64x64_K4 : TILE_64x64)
                       : known ? pl.tile : TILE_128x128;
     rec.splits[rec.n] = launched;
     rec.rows[rec.n] = a.M;
@@ -2445,7 +2467,7 @@ int silgpu_sgemm_tuned(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K
                        int64_t ldb, int64_t stride_b, float *d_C, int64_t ldc, int64_t stride_c,
                        int64_t batch, const float *d_bias, int64_t bias_len, int epilogue,
                        int tile, int splits) {
-  SILGPU_REQUIRE(tile >= TILE_128x128 && tile <= TILE_64x64_K2,
+  SILGPU_REQUIRE(tile >= TILE_128x128 && tile <= TILE_64x64_K4,
                  "silgpu_sgemm_tuned: unknown tile configuration %d", tile);
   SILGPU_REQUIRE(splits >= 1 && splits <= 256, "silgpu_sgemm_tuned: splits %d not in [1, 256]",
                  splits);

@@ -184,16 +184,19 @@ def test_bank_model_matches_the_measurements():
     assert b128_conflict_free([4 * (4 * r[l] + (g[l] ^ ((r[l] // 2) & 3))) for l in range(64)])
 
 
-def test_k_groups_lds_budget_and_exchange():
-    """The 64 x 64 tile with K halves (two groups of 4 waves of 32 x 32, BK
-    32, two stages each): both groups' stages fit in LDS twice over per CU
-    (69,632 B per workgroup, the size the compiler reports), and the
-    accumulator exchange slot ((i * TN + j) * NW + w) * 64 + l (float4 units)
-    is a bijection of (i, j, wave, lane) onto the first TM * TN * NW * 64
-    float4 of the first stage array, which holds 2 * kStage floats."""
-    kg, ns, nw, tm, tn = 2, 2, 4, 2, 2
+@pytest.mark.parametrize("kg,lds_bytes,per_cu", [(2, 69632, 2), (4, 139264, 1)])
+def test_k_groups_lds_budget_and_exchange(kg, lds_bytes, per_cu):
+    """The 64 x 64 tile with K split between two or four groups of 4 waves of
+    32 x 32 (BK 32, two stages each): the groups' stages fit in LDS (69,632
+    and 139,264 B per workgroup, the sizes the compiler reports; two and one
+    workgroups per CU), and the accumulator exchange slot ((i * TN + j) * NW
+    + w) * 64 + l (float4 units) is a bijection of (i, j, wave, lane) onto
+    the first TM * TN * NW * 64 float4 of the first stage array, which holds
+    kg * kStage floats."""
+    ns, nw, tm, tn = 2, 4, 2, 2
     stage = 2 * operand_floats(64, 32)  # A and B windows of one stage, floats
-    assert kg * ns * stage * 4 == 69632 and 2 * 69632 <= 160 * 1024
+    assert kg * ns * stage * 4 == lds_bytes
+    assert per_cu * lds_bytes <= 160 * 1024 < (per_cu + 1) * lds_bytes
     slots = {((i * tn + j) * nw + w) * 64 + l
              for i in range(tm) for j in range(tn) for w in range(nw) for l in range(64)}
     assert slots == set(range(tm * tn * nw * 64))

@@ -63,7 +63,7 @@ def _case(i):
                   if mode in ("gemm", "noalloc") and g.random() < 0.3 else None)
     c["resid"] = mode in ("gemm", "noalloc") and c["bo"] * c["bi"] == 1 and g.random() < 0.4
     c["ldr"] = N + int(g.choice([0, 1]))
-    c["tile"], c["splits"] = int(g.integers(1, 10)), int(g.choice([1, 2, 3, 4, 7, 16]))
+    c["tile"], c["splits"] = int(g.integers(1, 11)), int(g.choice([1, 2, 3, 4, 7, 16]))
     c["seed"] = 32000 + i
     return c
 

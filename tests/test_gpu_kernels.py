@@ -844,7 +844,7 @@ def test_small_batch_config(native, oracle):
     assert ok, (nw, el)
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
 @pytest.mark.parametrize("splits", [1, 3, 8])
 @pytest.mark.parametrize("M,N,K,ta,tb,epi", [(33, 70, 200, 0, 0, 0), (128, 256, 512, 0, 0, 2),
                                              (100, 130, 1000, 1, 0, 1), (64, 96, 777, 0, 1, 4),
@@ -1049,17 +1049,23 @@ def test_sgemm_lds_direct_batched(native, oracle, ta, tb, tile, K, splits):
         assert ok, (z, nw, el)
 
 
-@pytest.mark.parametrize("M,N,K,splits,batch", [(64, 64, 64, 1, 1), (256, 512, 1024, 1, 1),
-                                                (192, 128, 320, 3, 1), (128, 192, 4096, 8, 1),
-                                                (128, 256, 192, 1, 3)])
+K_GROUP_CASES = [(9, 64, 64, 64, 1, 1), (9, 256, 512, 1024, 1, 1), (9, 192, 128, 320, 3, 1),
+                 (9, 128, 192, 4096, 8, 1), (9, 128, 256, 192, 1, 3), (10, 128, 128, 128, 1, 1),
+                 (10, 256, 512, 3072, 1, 1), (10, 192, 128, 640, 2, 1), (10, 128, 192, 4096, 8, 1),
+                 (10, 128, 256, 384, 1, 3)]
+
+
+@pytest.mark.parametrize("tile,M,N,K,splits,batch", K_GROUP_CASES)
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-def test_sgemm_k_groups(native, oracle, ta, tb, M, N, K, splits, batch):
-    """Tile 9: 64 x 64 tiles on the LDS-direct kernel with each workgroup's
-    K range halved between two wave groups and added through LDS.  Padded
-    leading dimensions, every transpose, bias + relu, K splits on top (K
-    ranges of whole 64s: 320 = 128 + 128 + 64) and batches; the plan record
-    shows the kernel ran, and the padding columns of C stay unwritten."""
-    announce(f"sgemm k-groups ta={ta} tb={tb} {M}x{N}x{K} splits={splits} batch={batch}")
+def test_sgemm_k_groups(native, oracle, ta, tb, tile, M, N, K, splits, batch):
+    """Tiles 9 and 10: 64 x 64 tiles on the LDS-direct kernel with each
+    workgroup's K range split between two (9) or four (10) wave groups and
+    added through LDS.  Padded leading dimensions, every transpose, bias +
+    relu, K splits on top (K ranges of whole 64s or 128s: 320 = 128 + 128 +
+    64, 640 = 384 + 256) and batches; the plan record shows the kernel ran,
+    and the padding columns of C stay unwritten."""
+    announce(f"sgemm k-groups tile={tile} ta={ta} tb={tb} {M}x{N}x{K} splits={splits} "
+             f"batch={batch}")
     g = rng(2400 + 2 * ta + tb + K)
     lda = (M if ta else K) + 4
     ldb = (K if tb else N) + 8
@@ -1071,9 +1077,9 @@ def test_sgemm_k_groups(native, oracle, ta, tb, M, N, K, splits, batch):
     canary = np.full((batch, M, ldc), 7.25, np.float32)
     dA, dB, db, dC = up(native, A), up(native, B), up(native, bias), up(native, canary)
     native.sgemm_tuned(ta, tb, M, N, K, dA, lda, rows_a * lda, dB, ldb, rows_b * ldb, dC, ldc,
-                       M * ldc, batch, db, N, native.EPI_BIAS_RELU, tile=9, splits=splits)
+                       M * ldc, batch, db, N, native.EPI_BIAS_RELU, tile=tile, splits=splits)
     plan = native.last_plan()
-    assert plan and plan[0][0] == 9, plan
+    assert plan and plan[0][0] == tile, plan
     Cg = down(native, dC, (batch, M, ldc))
     assert np.all(Cg[:, :, N:] == 7.25)
     for z in range(batch):
@@ -1086,12 +1092,13 @@ def test_sgemm_k_groups(native, oracle, ta, tb, M, N, K, splits, batch):
         assert ok, (z, nw, el)
 
 
-@pytest.mark.parametrize("M,N,K,splits", [(1024, 1024, 1024, 1), (256, 2048, 512, 2),
-                                          (128, 2048, 768, 4)])
-def test_k_groups_planner_pick_with_residual(native, oracle, M, N, K, splits):
+@pytest.mark.parametrize("M,N,K,tile,splits", [(1024, 1024, 1024, 9, 1), (256, 2048, 512, 9, 2),
+                                               (128, 2048, 768, 9, 4), (256, 4096, 4096, 10, 1)])
+def test_k_groups_planner_pick_with_residual(native, oracle, M, N, K, tile, splits):
     """Products whose 64 x 64 tiles (times a few K splits) fill the CUs once
-    run tile 9 by the planner's own choice, through silgpu_gemm with bias and
-    residual, and through silgpu_gemm_noalloc bit for bit the same."""
+    run tile 9 (tile 10 where K >= 3072 needs no split) by the planner's own
+    choice, through silgpu_gemm with bias and residual, and through
+    silgpu_gemm_noalloc bit for bit the same."""
     announce(f"k-groups planner pick {M}x{N}x{K}")
     g = rng(2500 + M + K)
     A = g.normal(0, 1, (M, K)).astype(np.float32)
@@ -1102,10 +1109,10 @@ def test_k_groups_planner_pick_with_residual(native, oracle, M, N, K, splits):
     dC, dCn = empty(native, M * N), empty(native, M * N)
     native.gemm(0, 0, M, N, K, dA, K, dB, N, dC, N, epi=native.EPI_BIAS, bias=db, bias_len=N,
                 residual=dR, ldr=N)
-    assert native.last_plan() == [(9, splits, M)], native.last_plan()
+    assert native.last_plan() == [(tile, splits, M)], native.last_plan()
     native.gemm(0, 0, M, N, K, dA, K, dB, N, dCn, N, epi=native.EPI_BIAS, bias=db, bias_len=N,
                 residual=dR, ldr=N, noalloc=True)
-    assert native.last_plan() == [(9, splits, M)], native.last_plan()
+    assert native.last_plan() == [(tile, splits, M)], native.last_plan()
     C, Cn = down(native, dC, (M, N)), down(native, dCn, (M, N))
     assert np.array_equal(C, Cn)
     C64, Cabs = oracle.sgemm_f64(A, B, with_abs=True)
