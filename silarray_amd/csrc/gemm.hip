@@ -14,8 +14,8 @@
 // mapping keeps the workgroups of one XCD on neighbouring tiles so their A
 // and B panels are shared in that XCD's L2.  Products too small to fill the
 // 256 CUs split K: across workgroups (partial planes added by a second
-// launch) or, for 64 x 64 tiles, also between two groups of waves inside a
-// workgroup (added through LDS, no second launch).
+// launch) or, for 64 x 64 tiles, also between two or four groups of waves
+// inside a workgroup (added through LDS, no second launch).
 //
 // Epilogues (bias, sigmoid, relu) are applied to the accumulators before the
 // single store, so linear / linear_sigmoid are one pass over C.
