@@ -1955,6 +1955,16 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dtl_ok) {
     if (sp == 1 && t64 >= 224 && K >= 3072 && K % 128 == 0) return plan{TILE_64x64_K4, 1};
     if (sp >= 1 && t64 * sp >= 224) return plan{TILE_64x64_K2, static_cast<int>(sp)};
   }
+  // Batched products never split K across workgroups; where their 64 x 64
+  // tiles fill at most one round of the CUs, the K groups are the only K
+  // parallelism there is.  MI355X, us, previous pick -> K groups: 8 x
+  // 256x256x4096 120.8 -> 65.7 (four groups), 4 x 512x512x2048 63.3 -> 36.5,
+  // 16 x 128x128x1024 33.0 -> 20.4, 48 x 64x64x512 18.5 -> 12.4, 64 x
+  // 64x64x256 11.2 -> 8.9; with 512 tiles (8 x 512x512x512) two groups lost,
+  // 21.4 -> 23.0.
+  if (batch > 1 && dtl_ok && M % 64 == 0 && N % 64 == 0 && K % 64 == 0 &&
+      (M / 64) * (N / 64) * batch <= 256)
+    return plan{K >= 3072 && K % 128 == 0 ? TILE_64x64_K4 : TILE_64x64_K2, 1};
   return best;
 }
 

@@ -1120,6 +1120,30 @@ def test_k_groups_planner_pick_with_residual(native, oracle, M, N, K, tile, spli
     assert ok, (nw, el)
 
 
+@pytest.mark.parametrize("batch,M,N,K,tile", [(8, 256, 256, 4096, 10), (16, 128, 128, 1024, 9),
+                                              (48, 64, 64, 512, 9), (3, 64, 192, 3200, 10)])
+def test_k_groups_planner_pick_batched(native, oracle, batch, M, N, K, tile):
+    """Batched products whose 64 x 64 tiles fill at most one round of the CUs
+    run the K-group tile by the planner's own choice (four groups for K >=
+    3072), through silgpu_gemm with a two-level batch and bias."""
+    announce(f"k-groups batched planner pick {batch} x {M}x{N}x{K}")
+    g = rng(2600 + batch + K)
+    A = g.normal(0, 1, (batch, M, K)).astype(np.float32)
+    B = g.normal(0, 1, (batch, K, N)).astype(np.float32)
+    b = g.normal(0, 1, N).astype(np.float32)
+    dA, dB, db, dC = up(native, A), up(native, B), up(native, b), empty(native, batch * M * N)
+    bo, bi = (batch // 2, 2) if batch % 2 == 0 else (batch, 1)
+    native.gemm(0, 0, M, N, K, dA, K, dB, N, dC, N, batch_outer=bo, batch_inner=bi,
+                strides_a=(bi * M * K, M * K), strides_b=(bi * K * N, K * N),
+                strides_c=(bi * M * N, M * N), epi=native.EPI_BIAS, bias=db, bias_len=N)
+    assert native.last_plan() == [(tile, 1, M)], native.last_plan()
+    C = down(native, dC, (batch, M, N))
+    for z in range(batch):
+        C64, Cabs = oracle.sgemm_f64(A[z], B[z], with_abs=True)
+        ok, nw, el = gemm_tolerance_ok(C[z], C64 + b, Cabs + np.abs(b), K)
+        assert ok, (z, nw, el)
+
+
 # ---- fused attention ----------------------------------------------------------------
 
 def _attention_f64(Q, K, V, scale):
