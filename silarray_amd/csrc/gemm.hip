@@ -1965,6 +1965,19 @@ plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dtl_ok) {
   if (batch > 1 && dtl_ok && M % 64 == 0 && N % 64 == 0 && K % 64 == 0 &&
       (M / 64) * (N / 64) * batch <= 256)
     return plan{K >= 3072 && K % 128 == 0 ? TILE_64x64_K4 : TILE_64x64_K2, 1};
+  // A batched pick of unsplit 128 x 64 tiles that leaves its last round at
+  // most half full (batched products cannot peel it into a split second
+  // launch) runs faster as twice as many 64 x 64 tiles on two K groups:
+  // MI355X, us, 288 to 640 tiles of 128 x 64: 3 x 1024^3 66.8 -> 55.6,
+  // 12 x 512x512x1024 67.3 -> 56.9, 5 x 512x1024x2048 126.6 -> 101.1,
+  // 9 x 512x512x2048 126.5 -> 101.2, 10 x 512x1024x1024 96.0 -> 90.1 (11 of
+  // 11 shapes); with a fuller last round (448 tiles) 67.1 against 72.2, and
+  // with whole rounds or one partial one it lost 2-8%.
+  if (batch > 1 && dtl_ok && best.tile == TILE_128x64 && best.splits == 1 && M % 128 == 0 &&
+      N % 64 == 0 && K % 64 == 0) {
+    const int64_t t = (M / 128) * (N / 64) * batch;
+    if (t > 256 && t < 768 && t % 256 != 0 && t % 256 <= 128) return plan{TILE_64x64_K2, 1};
+  }
   return best;
 }
 

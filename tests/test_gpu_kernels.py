@@ -1121,11 +1121,15 @@ def test_k_groups_planner_pick_with_residual(native, oracle, M, N, K, tile, spli
 
 
 @pytest.mark.parametrize("batch,M,N,K,tile", [(8, 256, 256, 4096, 10), (16, 128, 128, 1024, 9),
-                                              (48, 64, 64, 512, 9), (3, 64, 192, 3200, 10)])
+                                              (48, 64, 64, 512, 9), (3, 64, 192, 3200, 10),
+                                              (3, 1024, 1024, 512, 9), (9, 256, 1024, 256, 9),
+                                              (7, 512, 1024, 256, 4)])
 def test_k_groups_planner_pick_batched(native, oracle, batch, M, N, K, tile):
     """Batched products whose 64 x 64 tiles fill at most one round of the CUs
     run the K-group tile by the planner's own choice (four groups for K >=
-    3072), through silgpu_gemm with a two-level batch and bias."""
+    3072), and so do those whose 128 x 64 tiles would leave a last round at
+    most half full (384 and 288 tiles here, not 448), through silgpu_gemm
+    with a two-level batch and bias."""
     announce(f"k-groups batched planner pick {batch} x {M}x{N}x{K}")
     g = rng(2600 + batch + K)
     A = g.normal(0, 1, (batch, M, K)).astype(np.float32)
